@@ -1,0 +1,324 @@
+"""Benchmark of the attention hot path on one MI355X.
+
+Headline workload (one "step"): the Qwen3-0.6B decode step of configuration 2 —
+28 layers, batch 32, GQA 16/8, head_dim 128, block 16, contexts U[60, 600],
+each layer with its own 4096-block KV pool (7 GiB in total, so every layer's
+43.5 MB of K/V is read cold from HBM rather than from the 256 MB MALL) and the
+store of the 32 new K/V rows fused into the same launch.  The 28 launches are
+captured once in a HIP graph and replayed, as the engine's decode graph does.
+
+Prints ONE JSON line: value = algorithmic HBM GB/s of the decode step (bytes
+defined in voiceagent_amd.workloads.decode_bytes plus the stored rows) over
+the timed region; also µs per layer, the roofline object of the decode
+kernel, the prefill (config 3) TFLOP/s, the encoder (config 4) time, and the
+CPU baseline (the per-sequence fp32 fallback on the host's cores).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import platform
+import sys
+import time
+
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+from voiceagent_amd import ops, workloads  # noqa: E402
+
+METRIC = "decode-attn µs/layer & HBM GB/s at B=32; prefill TFLOP/s; vs CPU ref"
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def timed_graph(fn, steps: int, warmup: int, stream: torch.cuda.Stream):
+    """Capture fn() in a graph, replay warmup + steps times; return ms per replay.
+
+    The replays and the timing events are issued on the same stream, so the
+    events bracket exactly the replayed kernels.
+    """
+    with torch.cuda.stream(stream):
+        fn()  # eager warm-up: workspace allocation happens outside the capture
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        fn()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(stream):
+        for _ in range(warmup):
+            graph.replay()
+        torch.cuda.synchronize()
+        start.record(stream)
+        for _ in range(steps):
+            graph.replay()
+        end.record(stream)
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps, graph
+
+
+def bench_decode(args, dev, stream):
+    lens = workloads.cfg2_lens(0)
+    layers = workloads.LAYERS
+    log(f"[decode] building 28 layer pools (B=32, ctx {min(lens)}..{max(lens)}, "
+        f"sum {sum(lens)})")
+    batch = workloads.make_decode_batch(lens, num_blocks=4096, num_layers=layers,
+                                        dtype=torch.bfloat16, kv_std=0.5, device=dev, seed=0,
+                                        device_rng=True)
+    g = torch.Generator(device=dev).manual_seed(7)
+    B = batch.num_seqs
+    qs = torch.randn(layers, B, workloads.HQ, workloads.HEAD_DIM, generator=g, device=dev
+                     ).to(torch.bfloat16)
+    nks = (torch.randn(layers, B, workloads.HKV, workloads.HEAD_DIM, generator=g, device=dev)
+           * 0.5).to(torch.bfloat16)
+    nvs = (torch.randn(layers, B, workloads.HKV, workloads.HEAD_DIM, generator=g, device=dev)
+           * 0.5).to(torch.bfloat16)
+    outs = torch.empty_like(qs)
+
+    def step():
+        for i in range(layers):
+            ops.paged_decode(qs[i], batch.k_pools[i], batch.v_pools[i], batch.block_tables,
+                             batch.cu_seqlens_k, lens_cumulative=True,
+                             max_seq_len=batch.max_seq_len, scale=batch.scale, new_k=nks[i],
+                             new_v=nvs[i], new_slots=batch.slot_mapping, out=outs[i],
+                             split_tokens=args.split)
+
+    ms, _ = timed_graph(step, args.steps, args.warmup, stream)
+    per_layer_bytes = workloads.decode_bytes(lens) + 2 * B * workloads.HKV * \
+        workloads.HEAD_DIM * 2 + 4 * B
+    us_layer = ms * 1000.0 / layers
+    gbs = per_layer_bytes / (us_layer * 1e-6) / 1e9
+    log(f"[decode] {ms:.3f} ms/step, {us_layer:.2f} us/layer, {gbs:.0f} GB/s "
+        f"({per_layer_bytes / 1e6:.2f} MB/layer)")
+    return dict(ms=ms, us_layer=us_layer, gbs=gbs, bytes_layer=per_layer_bytes, lens=lens,
+                batch=batch, qs=qs)
+
+
+def bench_store(args, dev, stream, dec):
+    """store_kvcache alone: 32 rows per layer over the 28 pools (latency-bound)."""
+    batch = dec["batch"]
+    B = batch.num_seqs
+
+    def step():
+        for i in range(workloads.LAYERS):
+            ops.store_kvcache(batch.new_k, batch.new_v, batch.k_pools[i], batch.v_pools[i],
+                              batch.slot_mapping)
+
+    ms, _ = timed_graph(step, args.steps, args.warmup, stream)
+    us = ms * 1000.0 / workloads.LAYERS
+    nbytes = workloads.store_bytes(B)
+    log(f"[store] {us:.2f} us/layer ({nbytes} B, latency-bound)")
+    return dict(us_layer=us, gbs=nbytes / (us * 1e-6) / 1e9)
+
+
+def bench_prefill(args, dev, stream):
+    lens = workloads.cfg3_lens(0)
+    layers = 28
+    total = sum(lens)
+    log(f"[prefill] 32 prompts, {total} tokens, 28 rotating input sets, fused store")
+    g = torch.Generator(device=dev).manual_seed(11)
+    q = torch.randn(layers, total, 16, 128, generator=g, device=dev).to(torch.bfloat16)
+    k = torch.randn(layers, total, 8, 128, generator=g, device=dev).to(torch.bfloat16)
+    v = torch.randn(layers, total, 8, 128, generator=g, device=dev).to(torch.bfloat16)
+    out = torch.empty_like(q)
+    cu = torch.zeros(len(lens) + 1, dtype=torch.int32)
+    cu[1:] = torch.cumsum(torch.tensor(lens, dtype=torch.int32), 0)
+    cu = cu.to(dev)
+    bs = 16
+    width = max(math.ceil(n / bs) for n in lens)
+    nb = sum(math.ceil(n / bs) for n in lens) + 8
+    perm = torch.randperm(nb, generator=torch.Generator().manual_seed(12)).tolist()
+    rows, cur, slots = [], 0, []
+    for n in lens:
+        m = math.ceil(n / bs)
+        rows.append(perm[cur:cur + m] + [-1] * (width - m))
+        slots += [perm[cur + p // bs] * bs + p % bs for p in range(n)]
+        cur += m
+    table = torch.tensor(rows, dtype=torch.int32, device=dev)
+    slots = torch.tensor(slots, dtype=torch.int32, device=dev)
+    kp = torch.zeros(layers, nb, bs, 8, 128, dtype=torch.bfloat16, device=dev)
+    vp = torch.zeros_like(kp)
+    scale = 128 ** -0.5
+
+    def step():
+        for i in range(layers):
+            ops.varlen_attention(q[i], k[i], v[i], cu, cu, max(lens), max(lens), scale=scale,
+                                 causal=True, k_cache=kp[i], v_cache=vp[i], block_tables=table,
+                                 slot_mapping=slots, out=out[i])
+
+    ms, _ = timed_graph(step, args.steps, args.warmup, stream)
+    us = ms * 1000.0 / layers
+    flops = workloads.causal_flops(lens)
+    tflops = flops / (us * 1e-6) / 1e12
+    nbytes = workloads.varlen_bytes(lens, 16, 8, 128) + total * 2 * 8 * 128 * 2
+    log(f"[prefill] {us:.2f} us/layer, {tflops:.1f} TFLOP/s ({flops / 1e9:.2f} GFLOP), "
+        f"{nbytes / (us * 1e-6) / 1e9:.0f} GB/s")
+    return dict(us_layer=us, tflops=tflops, flops=flops, bytes=nbytes)
+
+
+def bench_encoder(args, dev, stream):
+    wins = workloads.cfg4_windows(0)
+    layers = 18
+    total = sum(wins)
+    g = torch.Generator(device=dev).manual_seed(13)
+    q = torch.randn(layers, total, 14, 64, generator=g, device=dev).to(torch.bfloat16)
+    k = torch.randn(layers, total, 14, 64, generator=g, device=dev).to(torch.bfloat16)
+    v = torch.randn(layers, total, 14, 64, generator=g, device=dev).to(torch.bfloat16)
+    out = torch.empty_like(q)
+    cu = torch.zeros(len(wins) + 1, dtype=torch.int32)
+    cu[1:] = torch.cumsum(torch.tensor(wins, dtype=torch.int32), 0)
+    cu = cu.to(dev)
+
+    def step():
+        for i in range(layers):
+            ops.varlen_attention(q[i], k[i], v[i], cu, cu, max(wins), max(wins), scale=0.125,
+                                 causal=False, out=out[i])
+
+    ms, _ = timed_graph(step, args.steps, args.warmup, stream)
+    us = ms * 1000.0 / layers
+    flops = workloads.bidir_flops(wins)
+    nbytes = workloads.varlen_bytes(wins, 14, 14, 64)
+    log(f"[encoder] {len(wins)} windows, {total} tokens: {us:.2f} us/layer, "
+        f"{flops / (us * 1e-6) / 1e12:.1f} TFLOP/s, {nbytes / (us * 1e-6) / 1e9:.0f} GB/s")
+    return dict(us_layer=us, tflops=flops / (us * 1e-6) / 1e12,
+                gbs=nbytes / (us * 1e-6) / 1e9, windows=len(wins), tokens=total)
+
+
+def cpu_baseline(dec, budget_s: float):
+    """The oracle's per-sequence fp32 fallback on the host, one cfg-2 layer per rep."""
+    from oracle import attention as oracle
+
+    threads = os.cpu_count() or 1
+    torch.set_num_threads(threads)
+    batch = dec["batch"]
+    q = dec["qs"][0].cpu()
+    kp, vp = batch.k_pools[0].cpu(), batch.v_pools[0].cpu()
+    table, lens = batch.block_tables.cpu(), batch.context_lens.cpu()
+    oracle.paged_decode(q, kp, vp, table, lens, batch.scale)  # warm-up
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while len(times) < 5 or time.perf_counter() < t_end:
+        t0 = time.perf_counter()
+        oracle.paged_decode(q, kp, vp, table, lens, batch.scale)
+        times.append(time.perf_counter() - t0)
+        if len(times) >= 2000:
+            break
+    times.sort()
+    med = times[len(times) // 2]
+    gbs = dec["bytes_layer"] / med / 1e9
+    cpu_model = platform.processor() or ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    cpu_model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    log(f"[cpu] {med * 1e6:.0f} us/layer median of {len(times)} reps on {threads} threads "
+        f"({cpu_model})")
+    return {"value": round(gbs, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"config 2, one layer (B=32 decode, bf16 pool upcast to fp32) through the "
+                      f"per-sequence matmul/softmax fallback, {len(times)} reps, median "
+                      f"{med * 1e6:.0f} us/layer; host CPU: {cpu_model}",
+            "us_per_layer": round(med * 1e6, 1)}
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--split", type=int, default=0, help="decode split_tokens (0 = auto)")
+    ap.add_argument("--only", choices=["decode", "prefill", "encoder", "store", "all"],
+                    default="all")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU only; --gpus {args.gpus} is not supported "
+              "(this build has no multi-GPU path).", file=sys.stderr)
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        sys.exit(2)
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    stream = torch.cuda.Stream(dev)
+    torch.manual_seed(0)
+
+    result = {}
+    if args.only in ("prefill",):
+        result["prefill"] = bench_prefill(args, dev, stream)
+        print(json.dumps({"prefill": {k: v for k, v in result["prefill"].items()}}))
+        return
+    if args.only in ("encoder",):
+        print(json.dumps({"encoder": bench_encoder(args, dev, stream)}))
+        return
+    dec = bench_decode(args, dev, stream)
+    if args.only == "store":
+        print(json.dumps({"store": bench_store(args, dev, stream, dec)}))
+        return
+    extra = {}
+    if args.only == "all":
+        extra["store"] = bench_store(args, dev, stream, dec)
+        pre = bench_prefill(args, dev, stream)
+        enc = bench_encoder(args, dev, stream)
+        extra["prefill"] = {"us_per_layer": round(pre["us_layer"], 2),
+                            "tflops": round(pre["tflops"], 2),
+                            "mfma_frac": round(pre["tflops"] / BF16_PEAK_TFLOPS, 4),
+                            "hbm_gbs": round(pre["bytes"] / (pre["us_layer"] * 1e-6) / 1e9, 1),
+                            "config": "cfg3: 32 prompts U[50,450], GQA 16/8, D128, fused store, "
+                                      "28 rotating input sets (cold)"}
+        extra["encoder"] = {"us_per_layer": round(enc["us_layer"], 2),
+                            "tflops": round(enc["tflops"], 2),
+                            "hbm_gbs": round(enc["gbs"], 1),
+                            "config": f"cfg4: {enc['windows']} windows / {enc['tokens']} tokens, "
+                                      "14 heads x 64, 18 rotating layers"}
+    cpu = None
+    if not args.no_cpu and args.only == "all":
+        cpu = cpu_baseline(dec, args.cpu_seconds)
+    line = {
+        "metric": METRIC,
+        "value": round(dec["gbs"], 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(dec["ms"], 4),
+        "us_per_layer": round(dec["us_layer"], 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (K/V N(0,1)*0.5 bf16, q N(0,1), seed 0)",
+        "config": {"workload": "cfg2: Qwen3-0.6B paged decode step, 28 layers, B=32, "
+                               "GQA 16q/8kv, head_dim 128, block 16, ctx U[60,600], "
+                               "4096-block pool per layer, store of 32 rows/layer fused",
+                   "batch": 32, "layers": 28, "context_tokens": sum(dec["lens"]),
+                   "parallelism": "single GPU, HIP graph replay"},
+        "roofline": {"bound": "hbm", "achieved": round(dec["gbs"], 2), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(dec["gbs"] / HBM_PEAK_GBS, 4),
+                     "traffic": None,
+                     "kernel": "paged_decode_kernel<BF16,128,2,4>",
+                     "bytes_per_launch": dec["bytes_layer"]},
+        "cpu_baseline": cpu,
+    }
+    line.update(extra)
+    if line["roofline"]["frac"] > 1.0:
+        log("[bench] WARNING: achieved bandwidth above the HBM peak: measurement error")
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

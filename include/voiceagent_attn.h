@@ -1,0 +1,201 @@
+/*
+ * voiceagent_attn.h — C ABI of the MI355X (gfx950) attention core for qwen_asr_vllm.
+ *
+ * Every entry point takes one plain-old-data argument struct plus a HIP stream
+ * handle (passed as void*, so this header needs no HIP include), launches on
+ * that stream, never allocates, never synchronises the host, and returns
+ * VA_OK (0) or a negative status.  The message for the last failure on the
+ * calling thread is available from va_last_error().
+ *
+ * Tensors are described by device pointers and element (not byte) strides;
+ * the innermost (head_dim) dimension is always contiguous.  Element type is
+ * chosen by a va_dtype; index arrays (block tables, lengths, slot maps) by a
+ * va_index_dtype.  The caller owns every buffer.
+ *
+ * Reference interfaces replaced (paths relative to the reference repository):
+ *   va_store_kvcache      <- store_kvcache / _store_kvcache_kernel,
+ *                            qwen_asr_vllm/layers/attention.py:31-67
+ *   va_paged_decode       <- flash_attn_varlen_func(block_table=..., q_len 1),
+ *                            qwen_asr_vllm/layers/attention.py:87-107, and
+ *                            paged_attention_decode / _paged_decode_attention_kernel,
+ *                            qwen_asr_vllm/agent/qwen_tts_paged_attention.py:130-287, 383-516
+ *   va_varlen_attention   <- flash_attn_varlen_func(causal=True, block_table / no cache),
+ *                            qwen_asr_vllm/layers/attention.py:92-107, and
+ *                            flash_attn_varlen_func(causal=False),
+ *                            qwen_asr_vllm/layers/attention.py:121-139
+ */
+#ifndef VOICEAGENT_ATTN_H
+#define VOICEAGENT_ATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define VA_ATTN_ABI_VERSION 1
+
+/* status codes */
+#define VA_OK 0
+#define VA_ERR_INVALID_ARG (-1)
+#define VA_ERR_UNSUPPORTED (-2)
+#define VA_ERR_WORKSPACE (-3)
+#define VA_ERR_LAUNCH (-4)
+
+/* element types */
+#define VA_BF16 0
+#define VA_F16 1
+#define VA_F32 2
+
+/* index types */
+#define VA_I32 0
+#define VA_I64 1
+
+/* how va_decode_args.lens is read */
+#define VA_LENS_PER_SEQ 0    /* lens[b] = context length of sequence b           */
+#define VA_LENS_CUMULATIVE 1 /* lens[b+1] - lens[b] (cu_seqlens_k, num_seqs + 1) */
+
+/*
+ * KV pool addressing shared by all entry points.  Token slot s of a sequence
+ * whose block table row is T lives at
+ *     base + T[s / block_size] * stride_block + (s % block_size) * stride_slot
+ *          + kv_head * stride_head + d
+ * which covers the engine's NHD pool [num_blocks, block_size, Hkv, D]
+ * (qwen_asr_vllm/engine/model_runner.py:116-131) and the TTS talker's HND
+ * pool [pages, Hkv, page_size, D]
+ * (qwen_asr_vllm/agent/qwen_tts_outer_paged_cache.py:116-119).
+ */
+typedef struct va_kv_pool {
+  void* k;                /* key pool                                    */
+  void* v;                /* value pool (same strides as k)              */
+  int64_t stride_block;   /* elements between consecutive blocks/pages   */
+  int64_t stride_slot;    /* elements between slots inside one block     */
+  int64_t stride_head;    /* elements between kv heads                   */
+  int32_t block_size;     /* tokens per block (any positive value)       */
+  int32_t num_blocks;     /* blocks in the pool; out-of-range ids are    */
+                          /* treated as masked and never dereferenced    */
+} va_kv_pool;
+
+/* ---------------------------------------------------------------- store */
+typedef struct va_store_args {
+  uint32_t struct_size;   /* sizeof(va_store_args)                        */
+  int32_t dtype;          /* VA_BF16 / VA_F16 / VA_F32                    */
+  const void* key;        /* [num_tokens, Hkv, D]                         */
+  const void* value;
+  int64_t key_stride_tok, key_stride_head;
+  int64_t value_stride_tok, value_stride_head;
+  va_kv_pool pool;
+  const void* slot_mapping; /* [num_tokens]; slot < 0 or >= capacity skips */
+  int32_t slot_dtype;       /* VA_I32 / VA_I64                             */
+  int32_t num_tokens;
+  int32_t num_kv_heads;
+  int32_t head_dim;
+} va_store_args;
+
+/* Scatter key/value rows into the pool by slot_mapping (bit-exact copy).
+ * Replaces store_kvcache, qwen_asr_vllm/layers/attention.py:52-67. */
+int va_store_kvcache(const va_store_args* args, void* stream);
+
+/* --------------------------------------------------------------- decode */
+typedef struct va_decode_args {
+  uint32_t struct_size;   /* sizeof(va_decode_args)                       */
+  int32_t dtype;          /* q, pool, out and new rows share it           */
+  const void* q;          /* [num_seqs, Hq, D]: one query token per seq   */
+  int64_t q_stride_seq, q_stride_head;
+  void* out;              /* [num_seqs, Hq, D] in dtype                   */
+  int64_t out_stride_seq, out_stride_head;
+  va_kv_pool pool;
+  const void* block_tables; /* [num_seqs, table_width]; entries at index  */
+  int32_t table_dtype;      /* >= table_width read as block 0, as the TTS  */
+  int64_t table_stride_seq; /* padding does (qwen_tts_paged_attention.py:458-465) */
+  int32_t table_width;
+  const void* lens;       /* see VA_LENS_*                                */
+  int32_t lens_dtype;
+  int32_t lens_kind;
+  const uint8_t* valid_mask; /* optional [num_seqs, valid_len] bool; token */
+  int64_t valid_stride_seq;  /* t < len is attended iff t >= valid_len or  */
+  int32_t valid_len;         /* valid_mask[b, t] != 0                      */
+  /* Optional current row, written to the pool at position len-1 and used
+   * for that position in the same launch (the TTS fused write,
+   * qwen_tts_paged_attention.py:181-221).  [num_seqs, Hkv, D]. */
+  const void* new_k;
+  const void* new_v;
+  int64_t new_stride_seq, new_stride_head;
+  /* Optional destination slots for the current row ([num_seqs], slot < 0
+   * skips the write and the substitution).  NULL: the slot of position len-1
+   * through the block table. */
+  const void* new_slots;
+  int32_t new_slots_dtype;
+  int32_t num_seqs, num_heads, num_kv_heads, head_dim;
+  int32_t max_seq_len;    /* upper bound of every len; sizes the grid     */
+  int32_t split_tokens;   /* tokens per context partition, 0 = automatic  */
+  float scale;            /* softmax scale                                */
+  void* workspace;        /* partial results; see va_paged_decode_workspace_bytes */
+  size_t workspace_bytes;
+  /* Arrival counters of the in-launch merge: at least num_seqs * num_kv_heads
+   * int32, zero-filled once before first use and kept at zero by every
+   * launch.  Needed only when the workspace size is non-zero.  Launches that
+   * share counters or workspace must be ordered (same stream). */
+  int32_t* counters;
+  int64_t counters_len;
+} va_decode_args;
+
+/* Bytes of workspace va_paged_decode needs for these arguments (the
+ * struct's workspace and counter fields are ignored); 0 when no sequence can
+ * span more than one context partition. */
+size_t va_paged_decode_workspace_bytes(const va_decode_args* args);
+
+/* One-token GQA attention over a paged pool with split-context partitions
+ * merged in the same launch.  Replaces the decode use of
+ * flash_attn_varlen_func (qwen_asr_vllm/layers/attention.py:96-107) and
+ * paged_attention_decode (qwen_tts_paged_attention.py:383-516). */
+int va_paged_decode(const va_decode_args* args, void* stream);
+
+/* --------------------------------------------------------------- varlen */
+typedef struct va_varlen_args {
+  uint32_t struct_size;   /* sizeof(va_varlen_args)                       */
+  int32_t dtype;          /* VA_BF16 / VA_F16                             */
+  const void* q;          /* [total_q, Hq, D]                             */
+  int64_t q_stride_tok, q_stride_head;
+  const void* k;          /* [total_k or total_q, Hkv, D]; NULL with a    */
+  int64_t k_stride_tok, k_stride_head; /* pool = every key from the pool  */
+  const void* v;
+  int64_t v_stride_tok, v_stride_head;
+  void* out;              /* [total_q, Hq, D]                             */
+  int64_t out_stride_tok, out_stride_head;
+  const int32_t* cu_seqlens_q; /* [num_seqs + 1]                          */
+  const int32_t* cu_seqlens_k; /* [num_seqs + 1]                          */
+  int32_t num_seqs, total_q;
+  int32_t num_heads, num_kv_heads, head_dim;
+  int32_t max_seqlen_q, max_seqlen_k;
+  int32_t causal;         /* 1: bottom-right aligned causal mask          */
+  float scale;
+  /* Optional paged pool.  Keys j < k_len - q_len of a sequence come from the
+   * pool; the rest from k/v rows aligned with the queries (or from the pool
+   * too when k is NULL). */
+  va_kv_pool pool;
+  const void* block_tables;
+  int32_t table_dtype;
+  int64_t table_stride_seq;
+  int32_t table_width;
+  /* Optional fused store: q row i's k/v row is also written to slot
+   * slot_mapping[i] (slot < 0 skips), as store_kvcache would. */
+  const void* slot_mapping;
+  int32_t slot_dtype;
+} va_varlen_args;
+
+/* Variable-length attention over packed sequences: causal with bottom-right
+ * alignment (prefill, optionally over a paged prefix and with the store
+ * fused), or non-causal block-diagonal (audio encoder windows). */
+int va_varlen_attention(const va_varlen_args* args, void* stream);
+
+/* ----------------------------------------------------------------- misc */
+const char* va_last_error(void);
+int va_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* VOICEAGENT_ATTN_H */

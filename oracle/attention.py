@@ -1,0 +1,188 @@
+"""CPU oracle for the attention hot path — TEST INFRASTRUCTURE, NOT PRODUCT CODE.
+
+Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s cpu_baseline
+leg may import this module, and only as the checker / CPU baseline.  The
+product path (``voiceagent_amd``) never calls it.
+
+Each function restates the reference's per-sequence matmul/softmax fallback
+in plain PyTorch on the CPU, evaluated in float32 (or float64 when asked):
+
+* :func:`store_kvcache`   — qwen_asr_vllm/layers/attention.py:31-67
+* :func:`write_current_kv` — qwen_asr_vllm/agent/qwen_tts_paged_attention.py:519-532
+* :func:`paged_decode`     — _reference_paged_attention,
+  qwen_asr_vllm/agent/qwen_tts_paged_attention.py:353-380 (kv head = h // G,
+  :169-170 and :370-372), with the Triton kernel's masking (:229-234, :267)
+* :func:`varlen_attention` — flash_attn_varlen_func semantics as the engine uses
+  them: causal with bottom-right alignment (qwen_asr_vllm/layers/attention.py:1-11,
+  92-107), non-causal block-diagonal windows (:121-139); equal to upstream
+  eager_attention_forward + the causal or _prepare_attention_mask masks
+  (reference/modeling_qwen3_asr.py:90-113, 649-667).
+
+Masking convention: masked scores are -inf; a query row with no attended key
+returns 0 (the Triton kernel's result, qwen_tts_paged_attention.py:223-279).
+
+Pinning (tests/test_oracle.py): golden vectors regenerated from the
+reference tests' own seeded fixtures and checked against a float64 brute
+force written with scalar loops; the reference's known-answer tests (exact
+1.0/9.0 outputs, the SDPA comparison, window boundaries); torch's
+scaled_dot_product_attention with independently built masks; closed forms
+(single key, constant V, zero query, block-table permutation); and planted
+mistakes (GQA mapping, causal alignment, block indexing) that must fail.
+"""
+
+from __future__ import annotations
+
+import torch
+
+NHD = "nhd"  # [num_blocks, block_size, Hkv, D]
+HND = "hnd"  # [pages, Hkv, page_size, D]
+
+
+def _block_size(pool: torch.Tensor, layout: str) -> int:
+    return int(pool.shape[1] if layout == NHD else pool.shape[2])
+
+
+def gather_rows(pool: torch.Tensor, table_row: torch.Tensor, positions: torch.Tensor,
+                layout: str = NHD) -> torch.Tensor:
+    """Rows [len(positions), Hkv, D] of one sequence's paged K or V.
+
+    Position p lives in block table_row[p // block_size], slot p % block_size
+    (qwen_tts_paged_attention.py:366-369; model_runner.py:202-204).
+    """
+    bs = _block_size(pool, layout)
+    pages = table_row.long().index_select(0, positions // bs)
+    offsets = positions % bs
+    if layout == NHD:
+        return pool[pages, offsets]
+    return pool[pages, :, offsets, :]
+
+
+def store_kvcache(key, value, k_cache, v_cache, slot_mapping, layout: str = NHD):
+    """Return copies of the pools after the store (slot -1 skips; others must be valid).
+
+    cache.view(-1, Hkv * D)[slot] = key[i]   (layers/attention.py:42-49)
+    """
+    kc, vc = k_cache.clone(), v_cache.clone()
+    bs = _block_size(kc, layout)
+    for i, slot in enumerate(slot_mapping.tolist()):
+        if slot == -1:
+            continue
+        blk, off = divmod(int(slot), bs)
+        if layout == NHD:
+            kc[blk, off] = key[i]
+            vc[blk, off] = value[i]
+        else:
+            kc[blk, :, off] = key[i]
+            vc[blk, :, off] = value[i]
+    return kc, vc
+
+
+def write_current_kv(key_pool, value_pool, page_table, seq_lens, new_key, new_value,
+                     layout: str = HND):
+    """Copies of the pools with row seq_len-1 of every sequence replaced
+    (qwen_tts_paged_attention.py:519-532).  new_key: [B, Hkv, D]."""
+    kp, vp = key_pool.clone(), value_pool.clone()
+    bs = _block_size(kp, layout)
+    for row in range(new_key.shape[0]):
+        position = int(seq_lens[row]) - 1
+        page = int(page_table[row, position // bs])
+        offset = position % bs
+        if layout == NHD:
+            kp[page, offset] = new_key[row]
+            vp[page, offset] = new_value[row]
+        else:
+            kp[page, :, offset] = new_key[row]
+            vp[page, :, offset] = new_value[row]
+    return kp, vp
+
+
+def _masked_softmax_av(scores: torch.Tensor, values: torch.Tensor, keep: torch.Tensor | None):
+    """softmax over the last dim with -inf masking, rows with no key -> 0, then @ values."""
+    if keep is not None:
+        scores = scores.masked_fill(~keep, float("-inf"))
+    probs = torch.softmax(scores, dim=-1)
+    probs = torch.nan_to_num(probs, nan=0.0)  # fully masked rows
+    return probs @ values
+
+
+def paged_decode(q, k_cache, v_cache, block_tables, context_lens, scale, *, layout: str = NHD,
+                 valid_mask=None, compute_dtype=torch.float32):
+    """One query token per sequence over a paged pool.  q: [B, Hq, D] -> [B, Hq, D].
+
+    Per row (qwen_tts_paged_attention.py:363-379): gather the first L rows
+    through the table, repeat_interleave the kv heads by G = Hq / Hkv, then
+    softmax(q . K^T * scale) @ V.  ``valid_mask[b, t]`` masks token t when t is
+    inside the mask's width (tokens past it count as valid).
+    """
+    B, hq, d = q.shape
+    outs = []
+    for b in range(B):
+        length = int(context_lens[b])
+        if length <= 0:
+            outs.append(torch.zeros(1, hq, d, dtype=compute_dtype))
+            continue
+        pos = torch.arange(length)
+        keys = gather_rows(k_cache, block_tables[b], pos, layout).to(compute_dtype)
+        values = gather_rows(v_cache, block_tables[b], pos, layout).to(compute_dtype)
+        group = hq // keys.shape[1]
+        keys = keys.permute(1, 0, 2).repeat_interleave(group, dim=0)  # [Hq, L, D]
+        values = values.permute(1, 0, 2).repeat_interleave(group, dim=0)
+        qb = q[b].to(compute_dtype).unsqueeze(1)  # [Hq, 1, D]
+        scores = (qb @ keys.transpose(-1, -2)) * scale  # [Hq, 1, L]
+        keep = None
+        if valid_mask is not None:
+            width = valid_mask.shape[1]
+            keep = torch.ones(length, dtype=torch.bool)
+            n = min(width, length)
+            keep[:n] = valid_mask[b, :n].bool()
+            keep = keep.view(1, 1, length)
+        outs.append(_masked_softmax_av(scores, values, keep).transpose(0, 1))
+    return torch.cat(outs, dim=0)
+
+
+def varlen_attention(q, k, v, cu_seqlens_q, cu_seqlens_k, scale, causal, *, k_cache=None,
+                     v_cache=None, block_tables=None, layout: str = NHD,
+                     compute_dtype=torch.float32):
+    """Packed variable-length attention.  q: [total_q, Hq, D] -> same shape.
+
+    Sequence s owns queries [cu_q[s], cu_q[s+1]) and k_len = cu_k[s+1]-cu_k[s]
+    keys.  Causal is bottom-right aligned: query i sees key j iff
+    j <= k_len - q_len + i (layers/attention.py:8-10).  Keys come from packed
+    k/v rows [cu_k[s], cu_k[s+1]) without a pool; with a pool, keys
+    j < k_len - q_len are read through ``block_tables`` and the rest from k/v
+    rows aligned with the queries (from the pool as well when k is None).
+    """
+    total_q, hq, d = q.shape
+    out = torch.zeros(total_q, hq, d, dtype=compute_dtype)
+    cq = [int(x) for x in cu_seqlens_q]
+    ck = [int(x) for x in cu_seqlens_k]
+    for s in range(len(cq) - 1):
+        q0, q1 = cq[s], cq[s + 1]
+        ql, kl = q1 - q0, ck[s + 1] - ck[s]
+        if ql <= 0:
+            continue
+        if k_cache is None:
+            keys = k[ck[s]:ck[s + 1]]
+            values = v[ck[s]:ck[s + 1]]
+        else:
+            prefix = kl - ql if k is not None else kl
+            pos = torch.arange(prefix)
+            keys = gather_rows(k_cache, block_tables[s], pos, layout)
+            values = gather_rows(v_cache, block_tables[s], pos, layout)
+            if k is not None:
+                keys = torch.cat([keys, k[q0:q1]], dim=0)
+                values = torch.cat([values, v[q0:q1]], dim=0)
+        keys = keys.to(compute_dtype)
+        values = values.to(compute_dtype)
+        group = hq // keys.shape[1]
+        keys = keys.permute(1, 0, 2).repeat_interleave(group, dim=0)  # [Hq, kl, D]
+        values = values.permute(1, 0, 2).repeat_interleave(group, dim=0)
+        qs = q[q0:q1].to(compute_dtype).permute(1, 0, 2)  # [Hq, ql, D]
+        scores = (qs @ keys.transpose(-1, -2)) * scale  # [Hq, ql, kl]
+        keep = None
+        if causal:
+            i = torch.arange(ql).view(ql, 1)
+            j = torch.arange(kl).view(1, kl)
+            keep = (j <= kl - ql + i).view(1, ql, kl)
+        out[q0:q1] = _masked_softmax_av(scores, values, keep).permute(1, 0, 2)
+    return out

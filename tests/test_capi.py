@@ -1,0 +1,110 @@
+"""CPU checks of the C-ABI library: it loads, exports every function the
+header declares, agrees with the ctypes struct layouts, and rejects bad
+arguments on the host (no GPU needed: only zero-work or invalid calls)."""
+
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+
+from voiceagent_amd import _native as N
+from voiceagent_amd import ops
+
+HEADER = os.path.join(os.path.dirname(os.path.dirname(__file__)), "include", "voiceagent_attn.h")
+
+
+def _declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return set(re.findall(r"^\s*(?:const\s+)?\w+\s*\*?\s*(va_\w+)\s*\(", text, flags=re.M))
+
+
+def test_header_functions_are_exported():
+    lib = N.lib()
+    declared = _declared_functions()
+    assert declared == set(N.SIGNATURES), declared ^ set(N.SIGNATURES)
+    for name in declared:
+        assert hasattr(lib, name), name
+    assert lib.va_abi_version() == 1
+
+
+@pytest.mark.parametrize(
+    "fn, cls, count_field",
+    [("va_store_kvcache", N.StoreArgs, "num_tokens"),
+     ("va_paged_decode", N.DecodeArgs, "num_seqs"),
+     ("va_varlen_attention", N.VarlenArgs, "num_seqs")],
+)
+def test_struct_size_contract(fn, cls, count_field):
+    lib = N.lib()
+    args = N.new_args(cls)
+    setattr(args, count_field, 0)
+    # matching layout, zero work: succeeds without touching a device
+    assert getattr(lib, fn)(ctypes.byref(args), None) == 0
+    args.struct_size = ctypes.sizeof(cls) - 8
+    assert getattr(lib, fn)(ctypes.byref(args), None) == -1
+    assert "struct_size" in N.last_error()
+
+
+def test_decode_rejects_bad_geometry():
+    lib = N.lib()
+    args = N.new_args(N.DecodeArgs)
+    args.num_seqs = 2
+    args.q = args.out = args.block_tables = args.lens = 16
+    args.pool.k = args.pool.v = 16
+    args.pool.block_size, args.pool.num_blocks = 16, 4
+    args.num_heads, args.num_kv_heads, args.head_dim = 6, 4, 128
+    assert lib.va_paged_decode(ctypes.byref(args), None) == -1
+    assert "multiple" in N.last_error()
+    args.num_heads = 8
+    args.head_dim = 96  # unsupported head_dim reaches the dispatcher only after host checks
+    args.q_stride_seq = 1  # not a 16-byte multiple
+    assert lib.va_paged_decode(ctypes.byref(args), None) == -1
+    assert "16-byte" in N.last_error()
+
+
+def test_decode_workspace_sizing():
+    lib = N.lib()
+    args = N.new_args(N.DecodeArgs)
+    args.num_seqs, args.num_heads, args.num_kv_heads, args.head_dim = 32, 16, 8, 128
+    args.max_seq_len = 48
+    assert lib.va_paged_decode_workspace_bytes(ctypes.byref(args)) == 0  # one partition
+    args.max_seq_len = 600
+    n = lib.va_paged_decode_workspace_bytes(ctypes.byref(args))
+    assert n > 0
+    args.max_seq_len = 16384
+    assert lib.va_paged_decode_workspace_bytes(ctypes.byref(args)) >= n
+    bad = N.DecodeArgs()
+    assert lib.va_paged_decode_workspace_bytes(ctypes.byref(bad)) == 0
+
+
+def test_ops_refuse_cpu_tensors():
+    q = torch.zeros(2, 16, 128)
+    pool = torch.zeros(4, 16, 8, 128)
+    with pytest.raises(ops.AttentionArgumentError, match="GPU"):
+        ops.paged_decode(q, pool, pool, torch.zeros(2, 1, dtype=torch.int32),
+                         torch.ones(2, dtype=torch.int32), max_seq_len=1, scale=1.0)
+    with pytest.raises(ops.AttentionArgumentError, match="GPU"):
+        ops.store_kvcache(torch.zeros(2, 8, 128), torch.zeros(2, 8, 128), pool, pool,
+                          torch.zeros(2, dtype=torch.int32))
+
+
+def test_tts_api_contract_errors_on_cpu():
+    from voiceagent_amd.agent import PagedAttentionKernelError, paged_attention_decode
+
+    page_table = torch.tensor([[3, 5, 0], [1, 7, 2]], dtype=torch.long)
+    seq_lens = torch.tensor([3, 5], dtype=torch.long)
+    kp = torch.zeros(8, 2, 2, 4)
+    q = torch.ones(2, 4, 1, 4)
+    bad = page_table.clone()
+    bad[0, 0] = 99
+    # test_qwen_tts_paged_attention_kernel.py:60-74: invalid page ids are rejected.
+    with pytest.raises(PagedAttentionKernelError, match="page table"):
+        paged_attention_decode(q, kp, kp, bad, seq_lens)
+    with pytest.raises(PagedAttentionKernelError, match="torch.long"):
+        paged_attention_decode(q, kp, kp, page_table, seq_lens.int())
+    with pytest.raises(PagedAttentionKernelError, match="together"):
+        paged_attention_decode(q, kp, kp, page_table, seq_lens, new_key=torch.zeros(2, 2, 1, 4))
+    with pytest.raises(PagedAttentionKernelError, match="GPU"):
+        paged_attention_decode(q, kp, kp, page_table, seq_lens)

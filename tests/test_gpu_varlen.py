@@ -1,0 +1,205 @@
+"""Varlen attention (causal prefill, block-diagonal encoder) on the GPU
+against the CPU oracle.  bf16/fp16 inputs: max-abs error <= 2e-2 against the
+oracle evaluated in fp32 on the same inputs; stores are bit-exact."""
+
+import math
+
+import pytest
+import torch
+
+from oracle import attention as oracle
+from voiceagent_amd import ops, workloads
+from voiceagent_amd.layers import (AttentionContext, PagedAttention, VarlenSelfAttention,
+                                   attention_context)
+
+pytestmark = pytest.mark.gpu
+TOL = 2e-2
+
+
+def _err(out, ref):
+    return (out.float().cpu() - ref.float()).abs().max().item()
+
+
+def _cu(lens):
+    cu = torch.zeros(len(lens) + 1, dtype=torch.int32)
+    cu[1:] = torch.cumsum(torch.tensor(lens, dtype=torch.int32), 0)
+    return cu
+
+
+def test_cfg3_causal_packed(dev):
+    b = workloads.make_varlen_batch(workloads.cfg3_lens(0), 16, 8, 128, causal=True, seed=0)
+    out = ops.varlen_attention(b.q.to(dev), b.k.to(dev), b.v.to(dev), b.cu_seqlens.to(dev),
+                               b.cu_seqlens.to(dev), b.max_seqlen, b.max_seqlen, scale=b.scale,
+                               causal=True)
+    ref = oracle.varlen_attention(b.q, b.k, b.v, b.cu_seqlens, b.cu_seqlens, b.scale, True)
+    assert _err(out, ref) <= TOL
+
+
+def test_cfg4_encoder_block_diagonal(dev):
+    wins = workloads.cfg4_windows(0)
+    b = workloads.make_varlen_batch(wins, 14, 14, 64, causal=False, seed=1)
+    out = ops.varlen_attention(b.q.to(dev), b.k.to(dev), b.v.to(dev), b.cu_seqlens.to(dev),
+                               b.cu_seqlens.to(dev), b.max_seqlen, b.max_seqlen, scale=b.scale,
+                               causal=False)
+    ref = oracle.varlen_attention(b.q, b.k, b.v, b.cu_seqlens, b.cu_seqlens, b.scale, False)
+    assert _err(out, ref) <= TOL
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("hq,hkv,d", [(16, 8, 128), (14, 14, 64), (16, 4, 64), (32, 4, 128),
+                                      (8, 8, 128)])
+def test_ragged_lengths_and_geometries(dev, dtype, causal, hq, hkv, d):
+    lens = [1, 2, 15, 16, 17, 31, 32, 33, 63, 64, 65, 127, 128, 129, 200]
+    b = workloads.make_varlen_batch(lens, hq, hkv, d, causal=causal, dtype=dtype,
+                                    seed=hq + d + int(causal))
+    out = ops.varlen_attention(b.q.to(dev), b.k.to(dev), b.v.to(dev), b.cu_seqlens.to(dev),
+                               b.cu_seqlens.to(dev), b.max_seqlen, b.max_seqlen, scale=b.scale,
+                               causal=causal)
+    ref = oracle.varlen_attention(b.q, b.k, b.v, b.cu_seqlens, b.cu_seqlens, b.scale, causal)
+    assert _err(out, ref) <= TOL
+
+
+def _paged_prefill_case(seed=3, bs=16, nb=512):
+    g = torch.Generator().manual_seed(seed)
+    # (cached prefix, new tokens) per sequence: prefix-cache hits and plain prompts
+    spec = [(0, 70), (32, 50), (160, 1), (48, 200), (0, 1), (17, 64)]
+    q_lens = [n for _, n in spec]
+    k_lens = [p + n for p, n in spec]
+    kp = (torch.randn(nb, bs, 8, 128, generator=g)).to(torch.bfloat16)
+    vp = (torch.randn(nb, bs, 8, 128, generator=g)).to(torch.bfloat16)
+    width = max(math.ceil(k / bs) for k in k_lens)
+    perm = torch.randperm(nb, generator=g).tolist()
+    rows, cur = [], 0
+    for k in k_lens:
+        n = math.ceil(k / bs)
+        rows.append(perm[cur:cur + n] + [-1] * (width - n))
+        cur += n
+    table = torch.tensor(rows, dtype=torch.int32)
+    total = sum(q_lens)
+    q = torch.randn(total, 16, 128, generator=g).to(torch.bfloat16)
+    k = torch.randn(total, 8, 128, generator=g).to(torch.bfloat16)
+    v = torch.randn(total, 8, 128, generator=g).to(torch.bfloat16)
+    slots = []
+    for s, (p, n) in enumerate(spec):
+        for pos in range(p, p + n):
+            slots.append(int(table[s, pos // bs]) * bs + pos % bs)
+    return dict(kp=kp, vp=vp, table=table, q=q, k=k, v=v, cu_q=_cu(q_lens), cu_k=_cu(k_lens),
+                max_q=max(q_lens), max_k=max(k_lens), slots=torch.tensor(slots, dtype=torch.int32))
+
+
+def test_paged_prefix_with_fused_store(dev):
+    c = _paged_prefill_case()
+    kd, vd = c["kp"].to(dev), c["vp"].to(dev)
+    out = ops.varlen_attention(c["q"].to(dev), c["k"].to(dev), c["v"].to(dev), c["cu_q"].to(dev),
+                               c["cu_k"].to(dev), c["max_q"], c["max_k"], scale=128 ** -0.5,
+                               causal=True, k_cache=kd, v_cache=vd, block_tables=c["table"].to(dev),
+                               slot_mapping=c["slots"].to(dev))
+    ek, ev = oracle.store_kvcache(c["k"], c["v"], c["kp"], c["vp"], c["slots"])
+    torch.cuda.synchronize()
+    assert torch.equal(kd.cpu(), ek) and torch.equal(vd.cpu(), ev)
+    ref = oracle.varlen_attention(c["q"], c["k"], c["v"], c["cu_q"], c["cu_k"], 128 ** -0.5, True,
+                                  k_cache=c["kp"], v_cache=c["vp"], block_tables=c["table"])
+    assert _err(out, ref) <= TOL
+    # every key from the pool (the reference's store-then-attend order)
+    out2 = ops.varlen_attention(c["q"].to(dev), None, None, c["cu_q"].to(dev), c["cu_k"].to(dev),
+                                c["max_q"], c["max_k"], scale=128 ** -0.5, causal=True,
+                                k_cache=kd, v_cache=vd, block_tables=c["table"].to(dev))
+    assert _err(out2, ref) <= TOL
+
+
+def test_rows_without_visible_keys_are_zero(dev):
+    # q_len > k_len with bottom-right alignment: the first q_len - k_len rows see nothing.
+    g = torch.Generator().manual_seed(4)
+    q = torch.randn(10, 16, 128, generator=g).to(torch.bfloat16)
+    k = torch.randn(4, 8, 128, generator=g).to(torch.bfloat16)
+    v = torch.randn(4, 8, 128, generator=g).to(torch.bfloat16)
+    cu_q = torch.tensor([0, 10], dtype=torch.int32)
+    cu_k = torch.tensor([0, 4], dtype=torch.int32)
+    out = ops.varlen_attention(q.to(dev), k.to(dev), v.to(dev), cu_q.to(dev), cu_k.to(dev), 10, 4,
+                               scale=0.1, causal=True).cpu()
+    ref = oracle.varlen_attention(q, k, v, cu_q, cu_k, 0.1, True)
+    assert torch.count_nonzero(out[:6]) == 0
+    assert _err(out, ref) <= TOL
+
+
+# ------------------------------------------------------------- layer drop-ins
+def test_paged_attention_layer_prefill_then_decode(dev):
+    """PagedAttention as the engine drives it: prefill writes the cache, then
+    decode steps (fused store) read it; each step is checked against the oracle."""
+    g = torch.Generator().manual_seed(5)
+    bs, nb = 16, 256
+    layer = PagedAttention(16, 128, 128 ** -0.5, 8)
+    kv = torch.zeros(2, nb, bs, 8, 128, dtype=torch.bfloat16, device=dev)
+    layer.k_cache, layer.v_cache = kv[0], kv[1]
+    lens = [37, 90, 5]
+    width = 12
+    perm = torch.randperm(nb, generator=g).tolist()
+    tables = [perm[i * width:(i + 1) * width] for i in range(3)]
+    table_t = torch.tensor(tables, dtype=torch.int32, device=dev)
+    total = sum(lens)
+    q = torch.randn(total, 16, 128, generator=g).to(torch.bfloat16)
+    k = torch.randn(total, 8, 128, generator=g).to(torch.bfloat16)
+    v = torch.randn(total, 8, 128, generator=g).to(torch.bfloat16)
+    slots = [tables[s][p // bs] * bs + p % bs for s, n in enumerate(lens) for p in range(n)]
+    cu = _cu(lens)
+    ctx = AttentionContext(cu.to(dev), cu.to(dev), max(lens), max(lens),
+                           torch.tensor(slots, dtype=torch.int32, device=dev), table_t)
+    with attention_context(ctx):
+        out = layer(q.to(dev), k.to(dev), v.to(dev))
+    ref = oracle.varlen_attention(q, k, v, cu, cu, 128 ** -0.5, True)
+    assert _err(out, ref) <= TOL
+    kc, vc = oracle.store_kvcache(k, v, torch.zeros(nb, bs, 8, 128, dtype=torch.bfloat16),
+                                  torch.zeros(nb, bs, 8, 128, dtype=torch.bfloat16),
+                                  torch.tensor(slots))
+    torch.cuda.synchronize()
+    assert torch.equal(kv[0].cpu(), kc) and torch.equal(kv[1].cpu(), vc)
+    for step in range(3):
+        lens = [n + 1 for n in lens]
+        qd = torch.randn(3, 16, 128, generator=g).to(torch.bfloat16)
+        # the engine's v is a strided view of the fused qkv projection
+        qkv = torch.randn(3, 32 * 128, generator=g).to(torch.bfloat16)
+        kd, vd = qkv[:, 2048:3072].view(3, 8, 128), qkv[:, 3072:].view(3, 8, 128)
+        dslots = [tables[s][(n - 1) // bs] * bs + (n - 1) % bs for s, n in enumerate(lens)]
+        cu_k = _cu(lens)
+        ctx = AttentionContext(torch.arange(4, dtype=torch.int32, device=dev), cu_k.to(dev), 1,
+                               max(lens), torch.tensor(dslots, dtype=torch.int32, device=dev),
+                               table_t)
+        qkv_d = qkv.to(dev)
+        with attention_context(ctx):
+            out = layer(qd.to(dev), qkv_d[:, 2048:3072].view(3, 8, 128),
+                        qkv_d[:, 3072:].view(3, 8, 128))
+        kc, vc = oracle.store_kvcache(kd, vd, kc, vc, torch.tensor(dslots))
+        ref = oracle.paged_decode(qd, kc, vc, torch.tensor(tables), torch.tensor(lens),
+                                  128 ** -0.5)
+        assert _err(out, ref) <= TOL, step
+        torch.cuda.synchronize()
+        assert torch.equal(kv[0].cpu(), kc) and torch.equal(kv[1].cpu(), vc), step
+
+
+def test_paged_attention_layer_profiling_pass_without_cache(dev):
+    g = torch.Generator().manual_seed(6)
+    layer = PagedAttention(16, 128, 128 ** -0.5, 8)
+    lens = [64, 64, 64]
+    cu = _cu(lens)
+    q = torch.randn(192, 16, 128, generator=g).to(torch.bfloat16)
+    k = torch.randn(192, 8, 128, generator=g).to(torch.bfloat16)
+    v = torch.randn(192, 8, 128, generator=g).to(torch.bfloat16)
+    ctx = AttentionContext(cu.to(dev), cu.to(dev), 64, 64, None, None)
+    with attention_context(ctx):
+        out = layer(q.to(dev), k.to(dev), v.to(dev))
+    assert _err(out, oracle.varlen_attention(q, k, v, cu, cu, 128 ** -0.5, True)) <= TOL
+
+
+def test_varlen_self_attention_layer(dev):
+    from voiceagent_amd.audio import batcher
+
+    g = torch.Generator().manual_seed(7)
+    cu, widest = batcher.window_cu_seqlens([46, 26, 95, 250], 104)
+    total = int(cu[-1])
+    q = torch.randn(total, 14, 64, generator=g).to(torch.bfloat16)
+    k = torch.randn(total, 14, 64, generator=g).to(torch.bfloat16)
+    v = torch.randn(total, 14, 64, generator=g).to(torch.bfloat16)
+    layer = VarlenSelfAttention(14, 64, 64 ** -0.5)
+    out = layer(q.to(dev), k.to(dev), v.to(dev), cu.to(dev), widest)
+    assert _err(out, oracle.varlen_attention(q, k, v, cu, cu, 0.125, False)) <= TOL

@@ -1,0 +1,93 @@
+"""Compile the HIP attention kernels and the C ABI into one shared library.
+
+``build_native()`` runs ``hipcc --offload-arch=gfx950`` on every ``csrc/*.hip``
+file (in parallel, one object per file) and links them into
+``voiceagent_amd/lib/libvoiceagent_attn.so``.  It always recompiles; the GPU
+box loads the library built here and never compiles.
+"""
+
+from __future__ import annotations
+
+import concurrent.futures
+import os
+import shutil
+import subprocess
+from pathlib import Path
+
+PACKAGE_DIR = Path(__file__).resolve().parent
+CSRC_DIR = PACKAGE_DIR / "csrc"
+LIB_DIR = PACKAGE_DIR / "lib"
+OBJ_DIR = PACKAGE_DIR / "_build"
+LIB_NAME = "libvoiceagent_attn.so"
+LIB_PATH = LIB_DIR / LIB_NAME
+OFFLOAD_ARCH = "gfx950"
+
+# Packed-fp32 VALU ops are disabled for every HIP object: ordinary float code
+# is compiled to scalar v_fma/v_mul/v_add.
+HIPCC_FLAGS = [
+    f"--offload-arch={OFFLOAD_ARCH}",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-Wall",
+    "-Wno-unused-variable",
+    "-Wno-unused-function",
+    "-Xclang",
+    "-target-feature",
+    "-Xclang",
+    "-packed-fp32-ops",
+]
+
+
+def _hipcc() -> str:
+    path = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+    if not Path(path).exists():
+        raise RuntimeError("hipcc not found; the HIP kernels cannot be built")
+    return path
+
+
+def _compile(hipcc: str, src: Path, obj: Path) -> tuple[Path, str]:
+    cmd = [hipcc, *HIPCC_FLAGS, "-c", str(src), "-o", str(obj)]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    noise = "is not a recognized feature for this target"
+    log = "\n".join(
+        line for line in (proc.stdout + proc.stderr).splitlines() if noise not in line
+    )
+    if proc.returncode != 0:
+        raise RuntimeError(f"hipcc failed on {src.name}:\n{log}")
+    return obj, log
+
+
+def build_native(verbose: bool = False) -> Path:
+    """Compile every HIP source and link the shared library; returns its path."""
+    hipcc = _hipcc()
+    sources = sorted(CSRC_DIR.glob("*.hip"))
+    if not sources:
+        raise RuntimeError(f"no HIP sources under {CSRC_DIR}")
+    OBJ_DIR.mkdir(parents=True, exist_ok=True)
+    LIB_DIR.mkdir(parents=True, exist_ok=True)
+    jobs = max(1, min(len(sources), int(os.environ.get("MAX_JOBS", os.cpu_count() or 4))))
+    objects = []
+    with concurrent.futures.ThreadPoolExecutor(max_workers=jobs) as pool:
+        futures = [
+            pool.submit(_compile, hipcc, src, OBJ_DIR / (src.stem + ".o")) for src in sources
+        ]
+        for fut in futures:
+            obj, log = fut.result()
+            objects.append(obj)
+            if verbose and log.strip():
+                print(log)
+    tmp = LIB_PATH.with_suffix(".so.tmp")
+    cmd = [hipcc, f"--offload-arch={OFFLOAD_ARCH}", "-shared", "-fPIC", "-o", str(tmp)]
+    cmd += [str(o) for o in objects]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"link failed:\n{proc.stdout}{proc.stderr}")
+    os.replace(tmp, LIB_PATH)
+    if verbose:
+        print(f"built {LIB_PATH}")
+    return LIB_PATH
+
+
+if __name__ == "__main__":
+    build_native(verbose=True)

@@ -1,0 +1,161 @@
+// Shared device helpers for the gfx950 attention kernels: element types,
+// 16-byte vector loads, wave64 lane reductions (DPP within a 16-lane row,
+// cross-row permutes above that) and the error channel of the C ABI.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/voiceagent_attn.h"
+
+namespace va {
+
+// ------------------------------------------------------------------ errors
+void set_error(const char* fmt, ...);
+
+#define VA_CHECK_ARG(cond, ...)          \
+  do {                                   \
+    if (!(cond)) {                       \
+      ::va::set_error(__VA_ARGS__);      \
+      return VA_ERR_INVALID_ARG;         \
+    }                                    \
+  } while (0)
+
+int check_launch(const char* what);
+
+// ------------------------------------------------------------ element types
+// Each type describes how 16 bytes (one dwordx4 lane load) unpack to floats
+// and how floats pack back.  bf16 -> f32 is exact (bit shift); f32 -> bf16
+// rounds to nearest even, as torch does.
+struct BF16 {
+  static constexpr int kBytes = 2;
+  static constexpr int kPerVec = 8;
+  __device__ static inline void unpack(const uint4 u, float* f) {
+    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      f[2 * i] = __uint_as_float(w[i] << 16);
+      f[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+    }
+  }
+  __device__ static inline uint16_t from_float(float x) {
+    uint32_t u = __float_as_uint(x);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);  // quiet NaN
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+  }
+  __device__ static inline uint4 pack(const float* f) {
+    uint32_t w[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      w[i] = (uint32_t)from_float(f[2 * i]) | ((uint32_t)from_float(f[2 * i + 1]) << 16);
+    return make_uint4(w[0], w[1], w[2], w[3]);
+  }
+};
+
+struct F16 {
+  static constexpr int kBytes = 2;
+  static constexpr int kPerVec = 8;
+  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+  __device__ static inline void unpack(const uint4 u, float* f) {
+    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      h2 h = __builtin_bit_cast(h2, w[i]);
+      f[2 * i] = (float)h.x;
+      f[2 * i + 1] = (float)h.y;
+    }
+  }
+  __device__ static inline uint4 pack(const float* f) {
+    uint32_t w[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      h2 h;
+      h.x = (_Float16)f[2 * i];
+      h.y = (_Float16)f[2 * i + 1];
+      w[i] = __builtin_bit_cast(uint32_t, h);
+    }
+    return make_uint4(w[0], w[1], w[2], w[3]);
+  }
+};
+
+struct F32 {
+  static constexpr int kBytes = 4;
+  static constexpr int kPerVec = 4;
+  __device__ static inline void unpack(const uint4 u, float* f) {
+    f[0] = __uint_as_float(u.x);
+    f[1] = __uint_as_float(u.y);
+    f[2] = __uint_as_float(u.z);
+    f[3] = __uint_as_float(u.w);
+  }
+  __device__ static inline uint4 pack(const float* f) {
+    return make_uint4(__float_as_uint(f[0]), __float_as_uint(f[1]), __float_as_uint(f[2]),
+                      __float_as_uint(f[3]));
+  }
+};
+
+// ------------------------------------------------------------ memory access
+__device__ inline uint4 ld16(const void* p) { return *reinterpret_cast<const uint4*>(p); }
+__device__ inline void st16(void* p, uint4 v) { *reinterpret_cast<uint4*>(p) = v; }
+
+__device__ inline int64_t load_index(const void* p, int64_t i, int is_i64) {
+  return is_i64 ? reinterpret_cast<const int64_t*>(p)[i]
+                : (int64_t)reinterpret_cast<const int32_t*>(p)[i];
+}
+
+// ------------------------------------------------------- lane reductions
+// DPP control words (GFX9 encoding).
+constexpr int kDppQuadXor1 = 0xB1;     // quad_perm [1,0,3,2]
+constexpr int kDppQuadXor2 = 0x4E;     // quad_perm [2,3,0,1]
+constexpr int kDppRowHalfMirror = 0x141;
+constexpr int kDppRowMirror = 0x140;
+
+template <int CTRL>
+__device__ inline float dpp(float x) {
+  return __int_as_float(
+      __builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, false));
+}
+
+// Sum / max over aligned groups of W lanes (W in 1..64, power of two).  Every
+// lane of a group ends with the group's result.  Groups of <= 16 stay inside
+// a DPP row; wider groups add cross-row permutes.
+template <int W>
+__device__ inline float group_sum(float x) {
+  if constexpr (W >= 2) x += dpp<kDppQuadXor1>(x);
+  if constexpr (W >= 4) x += dpp<kDppQuadXor2>(x);
+  if constexpr (W >= 8) x += dpp<kDppRowHalfMirror>(x);
+  if constexpr (W >= 16) x += dpp<kDppRowMirror>(x);
+  if constexpr (W >= 32) x += __shfl_xor(x, 16, 64);
+  if constexpr (W >= 64) x += __shfl_xor(x, 32, 64);
+  return x;
+}
+
+template <int W>
+__device__ inline float group_max(float x) {
+  if constexpr (W >= 2) x = fmaxf(x, dpp<kDppQuadXor1>(x));
+  if constexpr (W >= 4) x = fmaxf(x, dpp<kDppQuadXor2>(x));
+  if constexpr (W >= 8) x = fmaxf(x, dpp<kDppRowHalfMirror>(x));
+  if constexpr (W >= 16) x = fmaxf(x, dpp<kDppRowMirror>(x));
+  if constexpr (W >= 32) x = fmaxf(x, __shfl_xor(x, 16, 64));
+  if constexpr (W >= 64) x = fmaxf(x, __shfl_xor(x, 32, 64));
+  return x;
+}
+
+// Reduce across the lanes that share (lane % STRIDE), i.e. over lanes
+// l, l+STRIDE, l+2*STRIDE, ... (STRIDE a power of two dividing 64).
+template <int STRIDE>
+__device__ inline float strided_sum(float x) {
+#pragma unroll
+  for (int s = STRIDE; s < 64; s <<= 1) x += __shfl_xor(x, s, 64);
+  return x;
+}
+template <int STRIDE>
+__device__ inline float strided_max(float x) {
+#pragma unroll
+  for (int s = STRIDE; s < 64; s <<= 1) x = fmaxf(x, __shfl_xor(x, s, 64));
+  return x;
+}
+
+__device__ inline float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+}  // namespace va

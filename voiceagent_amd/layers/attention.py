@@ -1,0 +1,171 @@
+"""Drop-in attention layers for the qwen_asr_vllm engine on MI355X.
+
+Same classes, constructor arguments and forward signatures as
+qwen_asr_vllm/layers/attention.py:52-139; the computation runs in the HIP
+kernels of ``libvoiceagent_attn.so`` (there is no torch or CPU fallback).
+
+``PagedAttention.forward(q, k, v)`` reads the batch metadata from
+:func:`get_attention_context` exactly as the reference does
+(layers/attention.py:87-107):
+
+* with a bound cache and a decode-only batch (``max_seqlen_q == 1`` and one
+  query per sequence) it launches the split-context paged decode kernel with
+  the store of the new K/V rows fused in (one launch per layer);
+* with a bound cache and any other batch it launches the causal varlen
+  kernel over the paged prefix with the store fused;
+* without a cache (``k_cache.numel() == 0``, the memory-profiling pass) it
+  runs causal varlen attention over the packed k/v.
+
+Fusing the store relies on the engine's invariant that ``slot_mapping[i]``
+is the pool slot of query token i's position (model_runner.py:202-204,
+graph_runner.py:165-168); ``fuse_store = False`` restores the reference's
+store-then-attend order with two launches.
+"""
+
+from __future__ import annotations
+
+import torch
+from torch import nn
+
+from voiceagent_amd import ops
+from voiceagent_amd.layers.context import get_attention_context
+
+
+def store_kvcache(
+    key: torch.Tensor,
+    value: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    slot_mapping: torch.Tensor,
+) -> None:
+    """Scatter key/value rows [N, Hkv, D] into an NHD pool [nb, bs, Hkv, D].
+
+    Mirrors qwen_asr_vllm/layers/attention.py:52-67, including its stride
+    contract (assertions :61-64): rows may be strided (the engine's ``v`` is a
+    view of the fused qkv output) but each row's heads are contiguous.
+    """
+    num_tokens, num_heads, head_dim = key.shape
+    hidden = num_heads * head_dim
+    assert key.stride(-1) == 1 and value.stride(-1) == 1
+    assert key.stride(1) == head_dim and value.stride(1) == head_dim
+    assert k_cache.stride(1) == hidden and v_cache.stride(1) == hidden
+    assert slot_mapping.numel() == num_tokens
+    ops.store_kvcache(key, value, k_cache, v_cache, slot_mapping, layout=ops.LAYOUT_NHD)
+
+
+class PagedAttention(nn.Module):
+    fuse_store = True
+
+    def __init__(self, num_heads: int, head_dim: int, scale: float, num_kv_heads: int):
+        super().__init__()
+        self.num_heads = num_heads
+        self.head_dim = head_dim
+        self.scale = scale
+        self.num_kv_heads = num_kv_heads
+        # Bound to slices of the engine-owned cache by the model runner.
+        self.k_cache = torch.tensor([])
+        self.v_cache = torch.tensor([])
+
+    def forward(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> torch.Tensor:
+        context = get_attention_context()
+        if not self.k_cache.numel():
+            # Memory-profiling pass before the cache exists: packed causal varlen.
+            return ops.varlen_attention(
+                q,
+                k,
+                v,
+                context.cu_seqlens_q,
+                context.cu_seqlens_k,
+                context.max_seqlen_q,
+                context.max_seqlen_k,
+                scale=self.scale,
+                causal=True,
+            )
+        num_seqs = context.cu_seqlens_k.numel() - 1
+        if context.max_seqlen_q == 1 and q.shape[0] == num_seqs:
+            if self.fuse_store:
+                return ops.paged_decode(
+                    q,
+                    self.k_cache,
+                    self.v_cache,
+                    context.block_tables,
+                    context.cu_seqlens_k,
+                    lens_cumulative=True,
+                    max_seq_len=context.max_seqlen_k,
+                    scale=self.scale,
+                    new_k=k,
+                    new_v=v,
+                    new_slots=context.slot_mapping,
+                )
+            store_kvcache(k, v, self.k_cache, self.v_cache, context.slot_mapping)
+            return ops.paged_decode(
+                q,
+                self.k_cache,
+                self.v_cache,
+                context.block_tables,
+                context.cu_seqlens_k,
+                lens_cumulative=True,
+                max_seq_len=context.max_seqlen_k,
+                scale=self.scale,
+            )
+        if self.fuse_store:
+            return ops.varlen_attention(
+                q,
+                k,
+                v,
+                context.cu_seqlens_q,
+                context.cu_seqlens_k,
+                context.max_seqlen_q,
+                context.max_seqlen_k,
+                scale=self.scale,
+                causal=True,
+                k_cache=self.k_cache,
+                v_cache=self.v_cache,
+                block_tables=context.block_tables,
+                slot_mapping=context.slot_mapping,
+            )
+        store_kvcache(k, v, self.k_cache, self.v_cache, context.slot_mapping)
+        return ops.varlen_attention(
+            q,
+            None,
+            None,
+            context.cu_seqlens_q,
+            context.cu_seqlens_k,
+            context.max_seqlen_q,
+            context.max_seqlen_k,
+            scale=self.scale,
+            causal=True,
+            k_cache=self.k_cache,
+            v_cache=self.v_cache,
+            block_tables=context.block_tables,
+        )
+
+
+class VarlenSelfAttention(nn.Module):
+    """Non-causal block-diagonal varlen attention for the audio encoder (no KV cache)."""
+
+    def __init__(self, num_heads: int, head_dim: int, scale: float):
+        super().__init__()
+        self.num_heads = num_heads
+        self.head_dim = head_dim
+        self.scale = scale
+
+    def forward(
+        self,
+        q: torch.Tensor,
+        k: torch.Tensor,
+        v: torch.Tensor,
+        cu_seqlens: torch.Tensor,
+        max_seqlen: int,
+    ) -> torch.Tensor:
+        return ops.varlen_attention(
+            q,
+            k,
+            v,
+            cu_seqlens,
+            cu_seqlens,
+            max_seqlen,
+            max_seqlen,
+            scale=self.scale,
+            causal=False,
+        )

@@ -1,0 +1,375 @@
+"""Tensor-level entry points over the C ABI.
+
+Each function validates shapes, dtypes, devices and strides on the host
+(shape metadata only: no device synchronisation), fills the argument struct
+and launches on torch's current stream.  The HIP library is the only compute
+path: CPU tensors or a missing library raise.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import math
+
+import torch
+
+from voiceagent_amd import _native as N
+
+LAYOUT_NHD = "nhd"  # [num_blocks, block_size, Hkv, D]  (engine, model_runner.py:116-131)
+LAYOUT_HND = "hnd"  # [pages, Hkv, page_size, D]        (TTS, qwen_tts_outer_paged_cache.py:116-119)
+
+
+class AttentionArgumentError(ValueError):
+    """Host-side contract violation detected before launch."""
+
+
+def _require(cond: bool, msg: str) -> None:
+    if not cond:
+        raise AttentionArgumentError(msg)
+
+
+def _check_gpu(*tensors: torch.Tensor | None) -> torch.device:
+    device = None
+    for t in tensors:
+        if t is None:
+            continue
+        _require(t.is_cuda, "attention kernels need GPU tensors (there is no CPU path)")
+        if device is None:
+            device = t.device
+        _require(t.device == device, "all tensors must be on the same device")
+    return device
+
+
+def _dtype_code(t: torch.Tensor) -> int:
+    _require(t.dtype in N.DTYPE_CODES, f"unsupported dtype {t.dtype}")
+    return N.DTYPE_CODES[t.dtype]
+
+
+def _index_code(t: torch.Tensor, what: str) -> int:
+    _require(t.dtype in N.INDEX_CODES, f"{what} must be int32 or int64, got {t.dtype}")
+    return N.INDEX_CODES[t.dtype]
+
+
+def _rows(t: torch.Tensor, what: str) -> None:
+    _require(t.stride(-1) == 1, f"{what}: the last dimension must be contiguous")
+
+
+def kv_pool(k_cache: torch.Tensor, v_cache: torch.Tensor, layout: str = LAYOUT_NHD) -> N.KvPool:
+    """Describe a paged K/V pool pair (4-D, NHD or HND) for the C ABI."""
+    _require(k_cache.dim() == 4, "KV pool must be 4-D")
+    _require(
+        v_cache.shape == k_cache.shape and v_cache.stride() == k_cache.stride(),
+        "key and value pools must have identical shapes and strides",
+    )
+    _require(v_cache.dtype == k_cache.dtype, "key and value pools must share a dtype")
+    _rows(k_cache, "KV pool")
+    pool = N.KvPool()
+    pool.k = k_cache.data_ptr()
+    pool.v = v_cache.data_ptr()
+    if layout == LAYOUT_NHD:
+        nb, bs, _, _ = k_cache.shape
+        pool.stride_block, pool.stride_slot, pool.stride_head = (
+            k_cache.stride(0),
+            k_cache.stride(1),
+            k_cache.stride(2),
+        )
+    elif layout == LAYOUT_HND:
+        nb, _, bs, _ = k_cache.shape
+        pool.stride_block, pool.stride_slot, pool.stride_head = (
+            k_cache.stride(0),
+            k_cache.stride(2),
+            k_cache.stride(1),
+        )
+    else:
+        raise AttentionArgumentError(f"unknown pool layout {layout!r}")
+    pool.block_size = int(bs)
+    pool.num_blocks = int(nb)
+    return pool
+
+
+def pool_heads(k_cache: torch.Tensor, layout: str) -> tuple[int, int]:
+    """(num_kv_heads, head_dim) of a pool."""
+    if layout == LAYOUT_NHD:
+        return int(k_cache.shape[2]), int(k_cache.shape[3])
+    return int(k_cache.shape[1]), int(k_cache.shape[3])
+
+
+# --------------------------------------------------------------------- store
+def store_kvcache(
+    key: torch.Tensor,
+    value: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    slot_mapping: torch.Tensor,
+    layout: str = LAYOUT_NHD,
+) -> None:
+    """Write key[i] / value[i] ([N, Hkv, D]) to pool slot slot_mapping[i]; -1 skips."""
+    device = _check_gpu(key, value, k_cache, v_cache, slot_mapping)
+    _require(key.dim() == 3 and value.shape == key.shape, "key/value must be [N, Hkv, D]")
+    _rows(key, "key")
+    _rows(value, "value")
+    hkv, d = pool_heads(k_cache, layout)
+    _require(key.shape[1] == hkv and key.shape[2] == d, "key/value heads must match the pool")
+    _require(key.dtype == value.dtype == k_cache.dtype, "key/value/pool dtypes must match")
+    _require(slot_mapping.dim() == 1 and slot_mapping.numel() == key.shape[0],
+             "slot_mapping must have one entry per token")
+    args = N.new_args(N.StoreArgs)
+    args.dtype = _dtype_code(key)
+    args.key = key.data_ptr()
+    args.value = value.data_ptr()
+    args.key_stride_tok, args.key_stride_head = key.stride(0), key.stride(1)
+    args.value_stride_tok, args.value_stride_head = value.stride(0), value.stride(1)
+    args.pool = kv_pool(k_cache, v_cache, layout)
+    args.slot_mapping = slot_mapping.data_ptr()
+    args.slot_dtype = _index_code(slot_mapping, "slot_mapping")
+    args.num_tokens = int(key.shape[0])
+    args.num_kv_heads = hkv
+    args.head_dim = d
+    N.call("va_store_kvcache", args, device)
+
+
+# -------------------------------------------------------------------- decode
+_WORKSPACES: dict[int, torch.Tensor] = {}
+_COUNTERS: dict[int, torch.Tensor] = {}
+
+
+def _device_index(device: torch.device) -> int:
+    return device.index if device.index is not None else torch.cuda.current_device()
+
+
+def decode_workspace(device: torch.device, nbytes: int) -> torch.Tensor | None:
+    """Partial-result workspace shared by decode launches on one device (no
+    initialisation needed; grows by doubling)."""
+    if nbytes == 0:
+        return None
+    key = _device_index(device)
+    ws = _WORKSPACES.get(key)
+    if ws is None or ws.numel() < nbytes:
+        size = max(nbytes, 0 if ws is None else 2 * ws.numel())
+        ws = torch.empty(size, dtype=torch.uint8, device=device)
+        _WORKSPACES[key] = ws
+    return ws
+
+
+def decode_counters(device: torch.device, count: int) -> torch.Tensor:
+    """Zero-filled int32 arrival counters of the in-launch merge.
+
+    Every launch leaves the counters it used at zero, so the buffer is
+    zero-filled only when it is (re)allocated and holds nothing else.
+    """
+    key = _device_index(device)
+    cnt = _COUNTERS.get(key)
+    if cnt is None or cnt.numel() < count:
+        size = max(count, 1024, 0 if cnt is None else 2 * cnt.numel())
+        cnt = torch.zeros(size, dtype=torch.int32, device=device)
+        _COUNTERS[key] = cnt
+    return cnt
+
+
+def reserve_decode_workspace(device: torch.device, nbytes: int, pairs: int) -> None:
+    """Allocate the decode workspace and counters up front (before HIP graph capture)."""
+    device = torch.device(device)
+    decode_workspace(device, nbytes)
+    decode_counters(device, pairs)
+
+
+def paged_decode(
+    q: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    block_tables: torch.Tensor,
+    lens: torch.Tensor,
+    *,
+    max_seq_len: int,
+    scale: float,
+    lens_cumulative: bool = False,
+    layout: str = LAYOUT_NHD,
+    valid_mask: torch.Tensor | None = None,
+    new_k: torch.Tensor | None = None,
+    new_v: torch.Tensor | None = None,
+    new_slots: torch.Tensor | None = None,
+    out: torch.Tensor | None = None,
+    split_tokens: int = 0,
+) -> torch.Tensor:
+    """One-token paged GQA attention.
+
+    q: [B, Hq, D]; out: [B, Hq, D] (allocated if None); lens: per-sequence
+    context lengths [B], or cu_seqlens_k [B + 1] with ``lens_cumulative``.
+    ``new_k``/``new_v`` ([B, Hkv, D]) are written at position len-1 (or at
+    ``new_slots[b]``) and used for that position in the same launch.
+    """
+    device = _check_gpu(q, k_cache, v_cache, block_tables, lens, valid_mask, new_k, new_v,
+                        new_slots, out)
+    _require(q.dim() == 3, "q must be [num_seqs, num_heads, head_dim]")
+    _rows(q, "q")
+    B, hq, d = (int(x) for x in q.shape)
+    hkv, pd = pool_heads(k_cache, layout)
+    _require(pd == d, f"head_dim mismatch: q {d}, pool {pd}")
+    _require(hq % hkv == 0, "num_heads must be a multiple of num_kv_heads")
+    _require(q.dtype == k_cache.dtype, "q and the KV pool must share a dtype")
+    _require(block_tables.dim() == 2 and block_tables.shape[0] >= B,
+             "block_tables must be [num_seqs, width]")
+    _require(block_tables.stride(-1) == 1, "block_tables rows must be contiguous")
+    expect = B + 1 if lens_cumulative else B
+    _require(lens.dim() == 1 and lens.numel() >= expect and lens.is_contiguous(),
+             f"lens must be a contiguous vector of at least {expect} entries")
+    if out is None:
+        out = torch.empty_like(q)
+    _require(out.shape == q.shape and out.dtype == q.dtype, "out must match q")
+    _rows(out, "out")
+    args = N.new_args(N.DecodeArgs)
+    args.dtype = _dtype_code(q)
+    args.q = q.data_ptr()
+    args.q_stride_seq, args.q_stride_head = q.stride(0), q.stride(1)
+    args.out = out.data_ptr()
+    args.out_stride_seq, args.out_stride_head = out.stride(0), out.stride(1)
+    args.pool = kv_pool(k_cache, v_cache, layout)
+    args.block_tables = block_tables.data_ptr()
+    args.table_dtype = _index_code(block_tables, "block_tables")
+    args.table_stride_seq = block_tables.stride(0)
+    args.table_width = int(block_tables.shape[1])
+    args.lens = lens.data_ptr()
+    args.lens_dtype = _index_code(lens, "lens")
+    args.lens_kind = N.VA_LENS_CUMULATIVE if lens_cumulative else N.VA_LENS_PER_SEQ
+    if valid_mask is not None:
+        _require(valid_mask.dim() == 2 and valid_mask.shape[0] >= B and
+                 valid_mask.dtype == torch.bool and valid_mask.stride(-1) == 1,
+                 "key_valid_mask must be a [num_seqs, max_seq] bool tensor")
+        args.valid_mask = valid_mask.data_ptr()
+        args.valid_stride_seq = valid_mask.stride(0)
+        args.valid_len = int(valid_mask.shape[1])
+    _require((new_k is None) == (new_v is None), "new_k and new_v must be given together")
+    if new_k is not None:
+        _require(new_k.shape == (B, hkv, d) and new_v.shape == new_k.shape,
+                 "new_k/new_v must be [num_seqs, num_kv_heads, head_dim]")
+        _require(new_v.stride() == new_k.stride(), "new_k and new_v must share strides")
+        _require(new_k.dtype == new_v.dtype == q.dtype, "new_k/new_v must match q's dtype")
+        _rows(new_k, "new_k")
+        args.new_k = new_k.data_ptr()
+        args.new_v = new_v.data_ptr()
+        args.new_stride_seq, args.new_stride_head = new_k.stride(0), new_k.stride(1)
+    if new_slots is not None:
+        _require(new_k is not None, "new_slots requires new_k/new_v")
+        _require(new_slots.dim() == 1 and new_slots.numel() >= B and new_slots.is_contiguous(),
+                 "new_slots must be a contiguous [num_seqs] vector")
+        args.new_slots = new_slots.data_ptr()
+        args.new_slots_dtype = _index_code(new_slots, "new_slots")
+    args.num_seqs = B
+    args.num_heads = hq
+    args.num_kv_heads = hkv
+    args.head_dim = d
+    args.max_seq_len = int(max_seq_len)
+    args.split_tokens = int(split_tokens)
+    args.scale = float(scale)
+    nbytes = N.lib().va_paged_decode_workspace_bytes(ctypes.byref(args))
+    ws = decode_workspace(device, nbytes)
+    if ws is not None:
+        args.workspace = ws.data_ptr()
+        args.workspace_bytes = ws.numel()
+        cnt = decode_counters(device, B * hkv)
+        args.counters = cnt.data_ptr()
+        args.counters_len = cnt.numel()
+    N.call("va_paged_decode", args, device)
+    return out
+
+
+# -------------------------------------------------------------------- varlen
+def varlen_attention(
+    q: torch.Tensor,
+    k: torch.Tensor | None,
+    v: torch.Tensor | None,
+    cu_seqlens_q: torch.Tensor,
+    cu_seqlens_k: torch.Tensor,
+    max_seqlen_q: int,
+    max_seqlen_k: int,
+    *,
+    scale: float,
+    causal: bool,
+    k_cache: torch.Tensor | None = None,
+    v_cache: torch.Tensor | None = None,
+    block_tables: torch.Tensor | None = None,
+    slot_mapping: torch.Tensor | None = None,
+    layout: str = LAYOUT_NHD,
+    out: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """Packed variable-length attention (flash_attn_varlen_func semantics).
+
+    Causal attention is bottom-right aligned: query i of a sequence with
+    (q_len, k_len) sees keys j <= k_len - q_len + i.  With a pool, keys
+    j < k_len - q_len are read through ``block_tables``; the others from
+    ``k``/``v`` rows aligned with the queries (all from the pool if ``k`` is
+    None).  ``slot_mapping`` fuses store_kvcache of k/v into the same launch.
+    """
+    device = _check_gpu(q, k, v, cu_seqlens_q, cu_seqlens_k, k_cache, v_cache, block_tables,
+                        slot_mapping, out)
+    _require(q.dim() == 3, "q must be [total_q, num_heads, head_dim]")
+    _rows(q, "q")
+    total_q, hq, d = (int(x) for x in q.shape)
+    _require(cu_seqlens_q.dtype == torch.int32 and cu_seqlens_k.dtype == torch.int32,
+             "cu_seqlens must be int32")
+    _require(cu_seqlens_q.dim() == 1 and cu_seqlens_q.numel() >= 2 and
+             cu_seqlens_k.numel() == cu_seqlens_q.numel(), "cu_seqlens must be [num_seqs + 1]")
+    _require(cu_seqlens_q.is_contiguous() and cu_seqlens_k.is_contiguous(),
+             "cu_seqlens must be contiguous")
+    num_seqs = int(cu_seqlens_q.numel()) - 1
+    args = N.new_args(N.VarlenArgs)
+    if k_cache is not None:
+        _require(v_cache is not None and block_tables is not None,
+                 "a KV pool needs v_cache and block_tables")
+        hkv, pd = pool_heads(k_cache, layout)
+        _require(pd == d, "pool head_dim must match q")
+        _require(k_cache.dtype == q.dtype, "pool dtype must match q")
+        args.pool = kv_pool(k_cache, v_cache, layout)
+        _require(block_tables.dim() == 2 and block_tables.shape[0] >= num_seqs and
+                 block_tables.stride(-1) == 1, "block_tables must be [num_seqs, width]")
+        args.block_tables = block_tables.data_ptr()
+        args.table_dtype = _index_code(block_tables, "block_tables")
+        args.table_stride_seq = block_tables.stride(0)
+        args.table_width = int(block_tables.shape[1])
+    else:
+        _require(k is not None and v is not None, "k and v are required without a KV pool")
+        hkv = int(k.shape[1])
+    if k is not None:
+        _require(v is not None and k.dim() == 3 and v.shape == k.shape,
+                 "k/v must be [tokens, num_kv_heads, head_dim]")
+        _require(k.shape[1] == hkv and k.shape[2] == d, "k/v heads must match")
+        _require(k.dtype == v.dtype == q.dtype, "q/k/v dtypes must match")
+        _rows(k, "k")
+        _rows(v, "v")
+        args.k = k.data_ptr()
+        args.k_stride_tok, args.k_stride_head = k.stride(0), k.stride(1)
+        args.v = v.data_ptr()
+        args.v_stride_tok, args.v_stride_head = v.stride(0), v.stride(1)
+    _require(hq % hkv == 0, "num_heads must be a multiple of num_kv_heads")
+    if slot_mapping is not None:
+        _require(k_cache is not None and k is not None, "slot_mapping needs a pool and k/v")
+        _require(slot_mapping.dim() == 1 and slot_mapping.numel() == total_q and
+                 slot_mapping.is_contiguous(), "slot_mapping must have one entry per query")
+        args.slot_mapping = slot_mapping.data_ptr()
+        args.slot_dtype = _index_code(slot_mapping, "slot_mapping")
+    if out is None:
+        out = torch.empty_like(q)
+    _require(out.shape == q.shape and out.dtype == q.dtype, "out must match q")
+    _rows(out, "out")
+    args.dtype = _dtype_code(q)
+    args.q = q.data_ptr()
+    args.q_stride_tok, args.q_stride_head = q.stride(0), q.stride(1)
+    args.out = out.data_ptr()
+    args.out_stride_tok, args.out_stride_head = out.stride(0), out.stride(1)
+    args.cu_seqlens_q = cu_seqlens_q.data_ptr()
+    args.cu_seqlens_k = cu_seqlens_k.data_ptr()
+    args.num_seqs = num_seqs
+    args.total_q = total_q
+    args.num_heads = hq
+    args.num_kv_heads = hkv
+    args.head_dim = d
+    args.max_seqlen_q = int(max_seqlen_q)
+    args.max_seqlen_k = int(max_seqlen_k)
+    args.causal = 1 if causal else 0
+    args.scale = float(scale)
+    N.call("va_varlen_attention", args, device)
+    return out
+
+
+def default_scale(head_dim: int) -> float:
+    return 1.0 / math.sqrt(head_dim)
