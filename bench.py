@@ -40,6 +40,20 @@ def log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
 
 
+def profiled_traffic(summary: str = "paged_decode_cfg2.md") -> int | None:
+    """HBM bytes per decode launch measured by the FETCH_SIZE / WRITE_SIZE
+    counter runs recorded in profiles/ (None when no summary is present)."""
+    path = os.path.join(ROOT, "profiles", summary)
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(line.split(":", 1)[1])
+    except (OSError, ValueError):
+        return None
+    return None
+
+
 def timed_graph(fn, steps: int, warmup: int, stream: torch.cuda.Stream):
     """Capture fn() in a graph, replay warmup + steps times; return ms per replay.
 
@@ -65,6 +79,18 @@ def timed_graph(fn, steps: int, warmup: int, stream: torch.cuda.Stream):
         end.record(stream)
     torch.cuda.synchronize()
     return start.elapsed_time(end) / steps, graph
+
+
+def copy_calibration(dev, nbytes: int = 256 << 20, reps: int = 3) -> None:
+    """A plain device copy of known size (read nbytes, write nbytes), run so a
+    counter profile of this command also holds the scale factor between the
+    FETCH_SIZE / WRITE_SIZE counters and real bytes."""
+    src = torch.empty(nbytes // 2, dtype=torch.bfloat16, device=dev).fill_(1.0)
+    dst = torch.empty_like(src)
+    for _ in range(reps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    log(f"[calibration] {reps} copies of {nbytes} bytes")
 
 
 def bench_decode(args, dev, stream):
@@ -244,6 +270,8 @@ def main():
                     default="all")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="run a 256 MiB device copy first (counter scale for profiles)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only; --gpus {args.gpus} is not supported "
@@ -257,6 +285,8 @@ def main():
     stream = torch.cuda.Stream(dev)
     torch.manual_seed(0)
 
+    if args.calibrate_copy:
+        copy_calibration(dev)
     result = {}
     if args.only in ("prefill",):
         result["prefill"] = bench_prefill(args, dev, stream)
@@ -309,7 +339,7 @@ def main():
                    "parallelism": "single GPU, HIP graph replay"},
         "roofline": {"bound": "hbm", "achieved": round(dec["gbs"], 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(dec["gbs"] / HBM_PEAK_GBS, 4),
-                     "traffic": None,
+                     "traffic": profiled_traffic(),
                      "kernel": "paged_decode_kernel<BF16,128,2,4>",
                      "bytes_per_launch": dec["bytes_layer"]},
         "cpu_baseline": cpu,

@@ -71,6 +71,8 @@ def test_decode_workspace_sizing():
     args.max_seq_len = 48
     assert lib.va_paged_decode_workspace_bytes(ctypes.byref(args)) == 0  # one partition
     args.max_seq_len = 600
+    assert lib.va_paged_decode_workspace_bytes(ctypes.byref(args)) == 0  # one pair per CU
+    args.num_seqs = 1  # 8 pairs: the context is split over several workgroups
     n = lib.va_paged_decode_workspace_bytes(ctypes.byref(args))
     assert n > 0
     args.max_seq_len = 16384

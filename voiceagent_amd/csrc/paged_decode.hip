@@ -79,14 +79,27 @@ __device__ inline float uniform(float x) {
   return __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(x)));
 }
 
-template <typename ET, int D, int G, int NW>
-__global__ __launch_bounds__(NW * 64) void paged_decode_kernel(DecodeParams p) {
-  constexpr int E = ET::kPerVec;       // elements per 16-byte lane load
-  constexpr int LPR = D / E;           // lanes per K/V row
+// Per-configuration launch shape.  NW wavefronts per workgroup and CPW chunks
+// whose K/V loads are in flight together per wave, sized so that the data
+// registers (8 * NR per chunk) plus the query/accumulator state fit 128 VGPRs
+// at NW = 16 (four waves per SIMD).
+template <typename ET, int D, int G>
+struct DecodeShape {
+  static constexpr int E = ET::kPerVec;       // elements per 16-byte lane load
+  static constexpr int LPR = D / E;           // lanes per K/V row
+  static constexpr int RPL = 64 / LPR;        // rows per load instruction
+  static constexpr int NR = kChunk / RPL;     // rows per lane per chunk
+  static constexpr int CPW = (8 * NR >= 64) ? 1 : 64 / (8 * NR);
+  static constexpr int NW = (2 * G * E + CPW * 8 * NR <= 96) ? 16 : 8;
+};
+
+template <typename ET, int D, int G>
+__global__ __launch_bounds__((DecodeShape<ET, D, G>::NW * 64)) void paged_decode_kernel(
+    DecodeParams p) {
+  using S = DecodeShape<ET, D, G>;
+  constexpr int E = S::E, LPR = S::LPR, RPL = S::RPL, NR = S::NR, CPW = S::CPW, NW = S::NW;
   static_assert(LPR >= 1 && LPR <= 64 && 64 % LPR == 0, "unsupported head_dim");
-  constexpr int RPL = 64 / LPR;        // rows per load instruction
   static_assert(RPL <= kChunk, "unsupported head_dim");
-  constexpr int NR = kChunk / RPL;     // rows per lane per chunk
   constexpr int NT = NW * 64;
 
   __shared__ float s_m[NW][G];
@@ -102,16 +115,31 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_kernel(DecodeParams p) {
   const int lane = tid & 63;
   const int rg = lane / LPR;
   const int col = lane % LPR;
+  const int P = p.split_tokens;
+  const int start = part * P;
+  const int64_t table_row = (int64_t)b * p.t_sb;
 
+  // Independent loads first: the context length, this wave's block-table
+  // entries (lane k holds the block of the wave's k-th chunk) and the query.
   int L;
   if (p.lens_cum)
     L = (int)(load_index(p.lens, b + 1, p.lens_i64) - load_index(p.lens, b, p.lens_i64));
   else
     L = (int)load_index(p.lens, b, p.lens_i64);
+  int tab = 0;
+  if (p.block_is_chunk_aligned) {
+    const int c = wave + NW * lane;
+    const int tok = start + c * kChunk;
+    if (c * kChunk < P) tab = (int)table_entry(p, table_row, tok / p.block_size);
+  }
+  float qv[G][E];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    const uint4 u = ld16(p.q + b * p.q_sb + (int64_t)(h * G + g) * p.q_sh + col * 16);
+    ET::unpack(u, qv[g]);
+  }
   L = __builtin_amdgcn_readfirstlane(L);
 
-  const int P = p.split_tokens;
-  const int start = part * P;
   if (L <= 0) {
     // Nothing to attend: the output is defined as 0.
     if (part == 0) {
@@ -131,6 +159,11 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_kernel(DecodeParams p) {
   if (nparts > p.max_parts) nparts = p.max_parts;  // the last partition absorbs the rest
   const int end = last_grid_part ? L : min(start + P, L);
 
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+#pragma unroll
+    for (int e = 0; e < E; ++e) qv[g][e] *= p.scale_log2;
+
   // Current-row substitution / write (TTS fused write, engine fused store).
   int64_t new_dst = -1;  // byte offset of the destination slot (block/slot part)
   int new_tok = -1;
@@ -139,7 +172,7 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_kernel(DecodeParams p) {
     if (p.new_slots != nullptr) {
       slot = load_index(p.new_slots, b, p.new_slots_i64);
     } else {
-      const int64_t blk = table_entry(p, (int64_t)b * p.t_sb, (L - 1) / p.block_size);
+      const int64_t blk = table_entry(p, table_row, (L - 1) / p.block_size);
       slot = (blk < 0 || blk >= p.num_blocks) ? -1
                                               : blk * p.block_size + (L - 1) % p.block_size;
     }
@@ -148,16 +181,6 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_kernel(DecodeParams p) {
       new_dst = blk * p.s_blk + (slot - blk * p.block_size) * p.s_slot;
       new_tok = L - 1;
     }
-  }
-
-  // Query rows of the group, pre-scaled into the exp2 domain.
-  float qv[G][E];
-#pragma unroll
-  for (int g = 0; g < G; ++g) {
-    const uint4 u = ld16(p.q + b * p.q_sb + (int64_t)(h * G + g) * p.q_sh + col * 16);
-    ET::unpack(u, qv[g]);
-#pragma unroll
-    for (int e = 0; e < E; ++e) qv[g][e] *= p.scale_log2;
   }
 
   float m[G], l[G], o[G][E];
@@ -170,23 +193,25 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_kernel(DecodeParams p) {
   }
 
   const int64_t head_off = (int64_t)h * p.s_head + col * 16;
-  const int64_t table_row = (int64_t)b * p.t_sb;
   const int nch = (end - start + kChunk - 1) / kChunk;
+  const int my_chunks = nch > wave ? (nch - wave + NW - 1) / NW : 0;
 
-  // Issue the K/V loads of chunk c; `valid` gets bit r for every attended row.
-  auto load_chunk = [&](int c, uint4 (&kr)[NR], uint4 (&vr)[NR], uint32_t& valid) {
+  // Issue the K/V loads of the wave's k-th chunk; `valid` gets bit r for every
+  // attended row.
+  auto load_chunk = [&](int k, uint4 (&kr)[NR], uint4 (&vr)[NR], uint32_t& valid) {
+    const int c = wave + NW * k;
     const int tb = start + c * kChunk;
     int64_t chunk_blk = 0;
     if (p.block_is_chunk_aligned)
-      chunk_blk = table_entry(p, table_row, tb / p.block_size);
+      chunk_blk = (k < 64 && c * kChunk < P) ? (int64_t)__builtin_amdgcn_readlane(tab, k)
+                                             : table_entry(p, table_row, tb / p.block_size);
     valid = 0;
 #pragma unroll
     for (int r = 0; r < NR; ++r) {
       const int tok = tb + rg + r * RPL;
       bool ok = tok < end;
       int64_t blk = chunk_blk;
-      if (!p.block_is_chunk_aligned && ok)
-        blk = table_entry(p, table_row, tok / p.block_size);
+      if (!p.block_is_chunk_aligned && ok) blk = table_entry(p, table_row, tok / p.block_size);
       ok = ok && blk >= 0 && blk < p.num_blocks;
       if (ok && p.valid != nullptr && tok < p.valid_len)
         ok = p.valid[b * p.valid_sb + tok] != 0;
@@ -212,10 +237,10 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_kernel(DecodeParams p) {
     }
   };
 
-  auto process_chunk = [&](int c, const uint4 (&kr)[NR], const uint4 (&vr)[NR], uint32_t valid) {
+  auto process_chunk = [&](int k, const uint4 (&kr)[NR], const uint4 (&vr)[NR], uint32_t valid) {
     // Fused write of the current row (exactly one lane group in the grid).
     if (new_tok >= 0) {
-      const int tb = start + c * kChunk;
+      const int tb = start + (wave + NW * k) * kChunk;
 #pragma unroll
       for (int r = 0; r < NR; ++r) {
         if (tb + rg + r * RPL == new_tok) {
@@ -272,23 +297,23 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_kernel(DecodeParams p) {
     }
   };
 
-  {
-    uint4 kr[NR], vr[NR];
-    uint32_t valid = 0;
-    int c = wave;
-    if (c < nch) load_chunk(c, kr, vr, valid);
-    for (; c < nch; c += NW) {
-      uint4 kn[NR], vn[NR];
-      uint32_t validn = 0;
-      if (c + NW < nch) load_chunk(c + NW, kn, vn, validn);
-      process_chunk(c, kr, vr, valid);
+  // CPW chunks per group: all their loads are issued before the first is reduced.
+  for (int k0 = 0; k0 < my_chunks; k0 += CPW) {
+    uint4 kr[CPW][NR], vr[CPW][NR];
+    uint32_t valid[CPW];
 #pragma unroll
-      for (int r = 0; r < NR; ++r) {
-        kr[r] = kn[r];
-        vr[r] = vn[r];
+    for (int j = 0; j < CPW; ++j) {
+      if (k0 + j < my_chunks) {
+        load_chunk(k0 + j, kr[j], vr[j], valid[j]);
+      } else {
+        valid[j] = 0;
+#pragma unroll
+        for (int r = 0; r < NR; ++r) kr[j][r] = vr[j][r] = make_uint4(0, 0, 0, 0);
       }
-      valid = validn;
     }
+#pragma unroll
+    for (int j = 0; j < CPW; ++j)
+      if (k0 + j < my_chunks) process_chunk(k0 + j, kr[j], vr[j], valid[j]);
   }
 
   // Wave result: sum l and o over row groups (lanes sharing `col`).
@@ -366,22 +391,35 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_kernel(DecodeParams p) {
   __syncthreads();
   if (!s_last) return;
 
+  constexpr int kBatch = 8;  // partials whose loads are in flight together
   for (int idx = tid; idx < G * D; idx += NT) {
     const int g = idx / D, d = idx % D;
     float M = kNegBig, Lt = 0.f, Ot = 0.f;
-    for (int q = 0; q < nparts; ++q) {
-      const int64_t slot = (pair * p.max_parts + q) * G + g;
-      const float mq =
-          __hip_atomic_load(p.part_ml + slot * 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      const float lq =
-          __hip_atomic_load(p.part_ml + slot * 2 + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      const float oq =
-          __hip_atomic_load(p.part_o + slot * D + d, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      const float Mn = fmaxf(M, mq);
-      const float a = fast_exp2(M - Mn), bq = fast_exp2(mq - Mn);
-      Lt = Lt * a + lq * bq;
-      Ot = Ot * a + oq * bq;
-      M = Mn;
+    for (int q0 = 0; q0 < nparts; q0 += kBatch) {
+      float mq[kBatch], lq[kBatch], oq[kBatch];
+#pragma unroll
+      for (int j = 0; j < kBatch; ++j) {
+        mq[j] = kNegBig;
+        lq[j] = 0.f;
+        oq[j] = 0.f;
+        if (q0 + j < nparts) {
+          const int64_t slot = (pair * p.max_parts + q0 + j) * G + g;
+          mq[j] = __hip_atomic_load(p.part_ml + slot * 2, __ATOMIC_RELAXED,
+                                    __HIP_MEMORY_SCOPE_AGENT);
+          lq[j] = __hip_atomic_load(p.part_ml + slot * 2 + 1, __ATOMIC_RELAXED,
+                                    __HIP_MEMORY_SCOPE_AGENT);
+          oq[j] = __hip_atomic_load(p.part_o + slot * D + d, __ATOMIC_RELAXED,
+                                    __HIP_MEMORY_SCOPE_AGENT);
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < kBatch; ++j) {
+        const float Mn = fmaxf(M, mq[j]);
+        const float a = fast_exp2(M - Mn), bq = fast_exp2(mq[j] - Mn);
+        Lt = Lt * a + lq[j] * bq;
+        Ot = Ot * a + oq[j] * bq;
+        M = Mn;
+      }
     }
     const float val = Lt > 0.f ? Ot / Lt : 0.f;
     char* dst = p.out + b * p.o_sb + (int64_t)(h * G + g) * p.o_sh + d * ET::kBytes;
@@ -398,8 +436,9 @@ __global__ __launch_bounds__(NW * 64) void paged_decode_kernel(DecodeParams p) {
 }
 
 // ----------------------------------------------------------------- host side
-constexpr int kDecodeWaves = 4;
-constexpr int kDecodeTargetWorkgroups = 2048;  // about 8 per CU on 256 CUs
+// Workgroups resident at once on the 256 CUs of an MI355X (one 16-wave
+// workgroup per CU); the split aims to give every CU one workgroup.
+constexpr int kDecodeTargetWorkgroups = 256;
 
 struct DecodePlan {
   int split_tokens;
@@ -407,9 +446,18 @@ struct DecodePlan {
   size_t ml_bytes, o_bytes, total_bytes;
 };
 
+template <typename ET, int D, int G>
+static int decode_unit() {
+  return DecodeShape<ET, D, G>::NW * kChunk;  // one chunk per wave
+}
+
+static int decode_unit_for(int dtype, int D, int G);
+
 static DecodePlan plan_decode(const va_decode_args* a) {
   DecodePlan pl{};
-  const int unit = kChunk * kDecodeWaves;
+  const int G = a->num_kv_heads > 0 ? a->num_heads / a->num_kv_heads : 1;
+  int unit = decode_unit_for(a->dtype, a->head_dim, G);
+  if (unit <= 0) unit = 256;
   const int max_len = a->max_seq_len > 0 ? a->max_seq_len : 1;
   int P = a->split_tokens;
   if (P <= 0) {
@@ -422,7 +470,6 @@ static DecodePlan plan_decode(const va_decode_args* a) {
   if (P < unit) P = unit;
   pl.split_tokens = P;
   pl.max_parts = (max_len + P - 1) / P;
-  const int G = a->num_kv_heads > 0 ? a->num_heads / a->num_kv_heads : 1;
   const int64_t pairs = (int64_t)a->num_seqs * a->num_kv_heads;
   if (pl.max_parts > 1) {
     pl.ml_bytes = ((size_t)pairs * pl.max_parts * G * 2 * 4 + 255) / 256 * 256;
@@ -434,8 +481,8 @@ static DecodePlan plan_decode(const va_decode_args* a) {
 
 template <typename ET, int D, int G>
 static void launch_decode(const DecodeParams& p, dim3 grid, hipStream_t s) {
-  hipLaunchKernelGGL((paged_decode_kernel<ET, D, G, kDecodeWaves>), grid, dim3(kDecodeWaves * 64),
-                     0, s, p);
+  hipLaunchKernelGGL((paged_decode_kernel<ET, D, G>), grid,
+                     dim3(DecodeShape<ET, D, G>::NW * 64), 0, s, p);
 }
 
 template <typename ET, int D>
@@ -456,6 +503,34 @@ static bool dispatch_d(int D, int G, const DecodeParams& p, dim3 grid, hipStream
     case 128: return dispatch_g<ET, 128>(G, p, grid, s);
     case 256: return dispatch_g<ET, 256>(G, p, grid, s);
     default: return false;
+  }
+}
+
+template <typename ET>
+static int unit_for_d(int D, int G) {
+#define VA_UNIT_G(DD)                                      \
+  switch (G) {                                             \
+    case 1: return decode_unit<ET, DD, 1>();               \
+    case 2: return decode_unit<ET, DD, 2>();               \
+    case 4: return decode_unit<ET, DD, 4>();               \
+    case 8: return decode_unit<ET, DD, 8>();               \
+    default: return 0;                                     \
+  }
+  switch (D) {
+    case 64: VA_UNIT_G(64)
+    case 128: VA_UNIT_G(128)
+    case 256: VA_UNIT_G(256)
+    default: return 0;
+  }
+#undef VA_UNIT_G
+}
+
+static int decode_unit_for(int dtype, int D, int G) {
+  switch (dtype) {
+    case VA_BF16: return unit_for_d<BF16>(D, G);
+    case VA_F16: return unit_for_d<F16>(D, G);
+    case VA_F32: return unit_for_d<F32>(D, G);
+    default: return 0;
   }
 }
 
