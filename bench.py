@@ -340,7 +340,7 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(dec["gbs"], 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(dec["gbs"] / HBM_PEAK_GBS, 4),
                      "traffic": profiled_traffic(),
-                     "kernel": "paged_decode_kernel<BF16,128,2,4>",
+                     "kernel": "paged_decode_kernel<BF16,128,2,true>",
                      "bytes_per_launch": dec["bytes_layer"]},
         "cpu_baseline": cpu,
     }

@@ -132,22 +132,18 @@ typedef struct va_decode_args {
   int32_t split_tokens;   /* tokens per context partition, 0 = automatic  */
   float scale;            /* softmax scale                                */
   void* workspace;        /* partial results; see va_paged_decode_workspace_bytes */
-  size_t workspace_bytes;
-  /* Arrival counters of the in-launch merge: at least num_seqs * num_kv_heads
-   * int32, zero-filled once before first use and kept at zero by every
-   * launch.  Needed only when the workspace size is non-zero.  Launches that
-   * share counters or workspace must be ordered (same stream). */
-  int32_t* counters;
-  int64_t counters_len;
-} va_decode_args;
+  size_t workspace_bytes; /* (no initialisation needed; launches sharing one   */
+} va_decode_args;         /*  workspace must be ordered on one stream)         */
 
 /* Bytes of workspace va_paged_decode needs for these arguments (the
- * struct's workspace and counter fields are ignored); 0 when no sequence can
- * span more than one context partition. */
+ * struct's workspace fields are ignored); 0 when no sequence can span more
+ * than one context partition.  With split_tokens = 0 the partition size
+ * depends on the current device's compute-unit count, so query the size with
+ * the same device current as the launch. */
 size_t va_paged_decode_workspace_bytes(const va_decode_args* args);
 
-/* One-token GQA attention over a paged pool with split-context partitions
- * merged in the same launch.  Replaces the decode use of
+/* One-token GQA attention over a paged pool: split-context partitions, then
+ * (only when a context spans several) a merge pass.  Replaces the decode use of
  * flash_attn_varlen_func (qwen_asr_vllm/layers/attention.py:96-107) and
  * paged_attention_decode (qwen_tts_paged_attention.py:383-516). */
 int va_paged_decode(const va_decode_args* args, void* stream);

@@ -70,13 +70,18 @@ def test_decode_workspace_sizing():
     args.num_seqs, args.num_heads, args.num_kv_heads, args.head_dim = 32, 16, 8, 128
     args.max_seq_len = 48
     assert lib.va_paged_decode_workspace_bytes(ctypes.byref(args)) == 0  # one partition
+    # 256 (sequence, kv head) pairs fill the CUs: one partition per pair.
     args.max_seq_len = 600
-    assert lib.va_paged_decode_workspace_bytes(ctypes.byref(args)) == 0  # one pair per CU
-    args.num_seqs = 1  # 8 pairs: the context is split over several workgroups
+    assert lib.va_paged_decode_workspace_bytes(ctypes.byref(args)) == 0
+    # Few pairs: contexts are split to occupy the CUs -> partials.
+    args.num_seqs = 2
     n = lib.va_paged_decode_workspace_bytes(ctypes.byref(args))
     assert n > 0
     args.max_seq_len = 16384
     assert lib.va_paged_decode_workspace_bytes(ctypes.byref(args)) >= n
+    args.split_tokens = 1  # an explicit split is honoured (rounded up to a workgroup round)
+    args.num_seqs, args.max_seq_len = 32, 600
+    assert lib.va_paged_decode_workspace_bytes(ctypes.byref(args)) > 0
     bad = N.DecodeArgs()
     assert lib.va_paged_decode_workspace_bytes(ctypes.byref(bad)) == 0
 

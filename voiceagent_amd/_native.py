@@ -100,8 +100,6 @@ class DecodeArgs(ctypes.Structure):
         ("scale", c_float),
         ("workspace", c_void_p),
         ("workspace_bytes", c_size_t),
-        ("counters", c_void_p),
-        ("counters_len", c_int64),
     ]
 
 

@@ -27,9 +27,26 @@ int check_launch(const char* what);
 // Each type describes how 16 bytes (one dwordx4 lane load) unpack to floats
 // and how floats pack back.  bf16 -> f32 is exact (bit shift); f32 -> bf16
 // rounds to nearest even, as torch does.
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+
+// dot(q, k, acc): acc + sum over the 16-byte vectors' elements, fp32
+// accumulation.  16-bit types use v_dot2_f32_{bf16,f16} on raw (unscaled)
+// q; F32 uses FMAs.
 struct BF16 {
   static constexpr int kBytes = 2;
   static constexpr int kPerVec = 8;
+  __device__ static inline float dot(const uint4 q, const uint4 k, float acc) {
+    acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, q.x),
+                                          __builtin_bit_cast(bf16x2_t, k.x), acc, false);
+    acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, q.y),
+                                          __builtin_bit_cast(bf16x2_t, k.y), acc, false);
+    acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, q.z),
+                                          __builtin_bit_cast(bf16x2_t, k.z), acc, false);
+    acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, q.w),
+                                          __builtin_bit_cast(bf16x2_t, k.w), acc, false);
+    return acc;
+  }
   __device__ static inline void unpack(const uint4 u, float* f) {
     const uint32_t w[4] = {u.x, u.y, u.z, u.w};
 #pragma unroll
@@ -57,6 +74,17 @@ struct F16 {
   static constexpr int kBytes = 2;
   static constexpr int kPerVec = 8;
   typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+  __device__ static inline float dot(const uint4 q, const uint4 k, float acc) {
+    acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, q.x), __builtin_bit_cast(f16x2_t, k.x),
+                                 acc, false);
+    acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, q.y), __builtin_bit_cast(f16x2_t, k.y),
+                                 acc, false);
+    acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, q.z), __builtin_bit_cast(f16x2_t, k.z),
+                                 acc, false);
+    acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, q.w), __builtin_bit_cast(f16x2_t, k.w),
+                                 acc, false);
+    return acc;
+  }
   __device__ static inline void unpack(const uint4 u, float* f) {
     const uint32_t w[4] = {u.x, u.y, u.z, u.w};
 #pragma unroll
@@ -82,6 +110,13 @@ struct F16 {
 struct F32 {
   static constexpr int kBytes = 4;
   static constexpr int kPerVec = 4;
+  __device__ static inline float dot(const uint4 q, const uint4 k, float acc) {
+    acc = fmaf(__uint_as_float(q.x), __uint_as_float(k.x), acc);
+    acc = fmaf(__uint_as_float(q.y), __uint_as_float(k.y), acc);
+    acc = fmaf(__uint_as_float(q.z), __uint_as_float(k.z), acc);
+    acc = fmaf(__uint_as_float(q.w), __uint_as_float(k.w), acc);
+    return acc;
+  }
   __device__ static inline void unpack(const uint4 u, float* f) {
     f[0] = __uint_as_float(u.x);
     f[1] = __uint_as_float(u.y);

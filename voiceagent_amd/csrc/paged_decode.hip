@@ -1,5 +1,5 @@
 // Paged-KV decode attention (one query token per sequence) for GQA, with
-// split-context partitions merged inside the same launch.
+// optional split-context partitions merged by a second, small kernel.
 //
 // Semantics: for sequence b with context length L and query head hq,
 //     out[b, hq] = softmax_j( scale * q[b, hq] . K[j, hq / G] ) @ V[j, hq / G]
@@ -21,14 +21,20 @@
 // chunks; the 64 lanes of a wave split a chunk as (row group, 16-byte column):
 // a D = 128 bf16 row is 16 lanes x 16 B, four rows per dwordx4 load, so each
 // load instruction moves 1 KiB of fully used 128-byte lines.  Chunk c of the
-// partition goes to wave c % NW and the next chunk's K/V loads are issued
-// before the current chunk is reduced.  Scores are reduced over the row's
-// lanes with DPP, the running max over row groups with cross-row permutes;
-// softmax runs in the exp2 domain (q pre-scaled by scale * log2 e).  Waves
-// merge through LDS; a sequence split into several partitions writes
-// unnormalised partials (m, l, o) to the workspace, and the last workgroup
-// to arrive (device-scope counter, reset by that workgroup) merges them and
-// writes the output — no second launch.
+// partition goes to wave c % NW; a wave issues the K/V loads of CPW chunks
+// before reducing the first of them.  Scores (v_dot2 on 16-bit inputs) are
+// reduced over the row's lanes with DPP, the running max over row groups
+// with cross-row permutes; softmax runs in the exp2 domain (scores scaled by
+// scale * log2 e).  Waves merge through LDS.  A sequence split into several
+// partitions writes unnormalised partials (m, l, o) to the workspace, and a
+// small second kernel (one workgroup per sequence x kv head) merges them with
+// the log-sum-exp rule.  The kernel boundary publishes the partials, so no
+// workgroup ever waits on another.  Partitions are used only when there are
+// too few (sequence, kv head) pairs to give every CU a workgroup: one
+// 8-wave workgroup fills a CU, and a second round of workgroups costs more
+// than the imbalance between long and short contexts.
+#include <atomic>
+
 #include "common.h"
 
 namespace va {
@@ -43,6 +49,7 @@ struct DecodeParams {
   int64_t s_blk, s_slot, s_head;  // bytes
   int32_t block_size, num_blocks;
   int32_t block_is_chunk_aligned;  // block_size % 16 == 0
+  int32_t pool_off32;              // every pool byte offset fits 32 bits
   const void* table;
   int64_t t_sb;  // elements
   int32_t table_i64;
@@ -61,7 +68,6 @@ struct DecodeParams {
   int32_t split_tokens;
   int32_t max_parts;
   float scale_log2;
-  int32_t* counters;
   float* part_ml;
   float* part_o;
 };
@@ -79,10 +85,11 @@ __device__ inline float uniform(float x) {
   return __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(x)));
 }
 
-// Per-configuration launch shape.  NW wavefronts per workgroup and CPW chunks
-// whose K/V loads are in flight together per wave, sized so that the data
-// registers (8 * NR per chunk) plus the query/accumulator state fit 128 VGPRs
-// at NW = 16 (four waves per SIMD).
+// Per-configuration launch shape: NW = 8 wavefronts per workgroup (two per
+// SIMD, so a wave may hold up to 256 VGPRs and the state never spills), CPW
+// chunks whose K/V loads are in flight together per wave (8 * NR data VGPRs
+// each).  Measured on MI355X at B = 32: 8 waves x 2 chunks beat 16 waves
+// (128-VGPR cap, spills) and deeper per-wave prefetch (3-4 chunks).
 template <typename ET, int D, int G>
 struct DecodeShape {
   static constexpr int E = ET::kPerVec;       // elements per 16-byte lane load
@@ -90,11 +97,13 @@ struct DecodeShape {
   static constexpr int RPL = 64 / LPR;        // rows per load instruction
   static constexpr int NR = kChunk / RPL;     // rows per lane per chunk
   static constexpr int CPW = (8 * NR >= 64) ? 1 : 64 / (8 * NR);
-  static constexpr int NW = (2 * G * E + CPW * 8 * NR <= 96) ? 16 : 8;
+  static constexpr int NW = 8;
+  static constexpr int kWavesPerSimd = 2;     // occupancy the register budget is sized for
 };
 
-template <typename ET, int D, int G>
-__global__ __launch_bounds__((DecodeShape<ET, D, G>::NW * 64)) void paged_decode_kernel(
+template <typename ET, int D, int G, bool kAligned>
+__global__ __launch_bounds__((DecodeShape<ET, D, G>::NW * 64),
+                             (DecodeShape<ET, D, G>::kWavesPerSimd)) void paged_decode_kernel(
     DecodeParams p) {
   using S = DecodeShape<ET, D, G>;
   constexpr int E = S::E, LPR = S::LPR, RPL = S::RPL, NR = S::NR, CPW = S::CPW, NW = S::NW;
@@ -105,11 +114,13 @@ __global__ __launch_bounds__((DecodeShape<ET, D, G>::NW * 64)) void paged_decode
   __shared__ float s_m[NW][G];
   __shared__ float s_l[NW][G];
   __shared__ float s_o[NW][G][D];
-  __shared__ int s_last;
 
-  const int part = blockIdx.x;
+  // Partition-major grid: every sequence's first partition is dispatched
+  // before any second one, so workgroups past the end of short contexts
+  // (which exit after reading the length) queue behind the live ones.
+  const int b = blockIdx.x;
   const int h = blockIdx.y;
-  const int b = blockIdx.z;
+  const int part = blockIdx.z;
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
   const int lane = tid & 63;
@@ -127,17 +138,17 @@ __global__ __launch_bounds__((DecodeShape<ET, D, G>::NW * 64)) void paged_decode
   else
     L = (int)load_index(p.lens, b, p.lens_i64);
   int tab = 0;
-  if (p.block_is_chunk_aligned) {
+  if constexpr (kAligned) {
     const int c = wave + NW * lane;
     const int tok = start + c * kChunk;
     if (c * kChunk < P) tab = (int)table_entry(p, table_row, tok / p.block_size);
   }
-  float qv[G][E];
+  // The query slice of this lane, as loaded (16-bit types feed v_dot2 and
+  // are scaled after the row reduction; fp32 is pre-scaled below).
+  uint4 qv[G];
 #pragma unroll
-  for (int g = 0; g < G; ++g) {
-    const uint4 u = ld16(p.q + b * p.q_sb + (int64_t)(h * G + g) * p.q_sh + col * 16);
-    ET::unpack(u, qv[g]);
-  }
+  for (int g = 0; g < G; ++g)
+    qv[g] = ld16(p.q + b * p.q_sb + (int64_t)(h * G + g) * p.q_sh + col * 16);
   L = __builtin_amdgcn_readfirstlane(L);
 
   if (L <= 0) {
@@ -159,10 +170,16 @@ __global__ __launch_bounds__((DecodeShape<ET, D, G>::NW * 64)) void paged_decode
   if (nparts > p.max_parts) nparts = p.max_parts;  // the last partition absorbs the rest
   const int end = last_grid_part ? L : min(start + P, L);
 
+  constexpr bool kScaleAfter = ET::kBytes == 2;
+  if constexpr (!kScaleAfter) {
 #pragma unroll
-  for (int g = 0; g < G; ++g)
-#pragma unroll
-    for (int e = 0; e < E; ++e) qv[g][e] *= p.scale_log2;
+    for (int g = 0; g < G; ++g) {
+      qv[g].x = __float_as_uint(__uint_as_float(qv[g].x) * p.scale_log2);
+      qv[g].y = __float_as_uint(__uint_as_float(qv[g].y) * p.scale_log2);
+      qv[g].z = __float_as_uint(__uint_as_float(qv[g].z) * p.scale_log2);
+      qv[g].w = __float_as_uint(__uint_as_float(qv[g].w) * p.scale_log2);
+    }
+  }
 
   // Current-row substitution / write (TTS fused write, engine fused store).
   int64_t new_dst = -1;  // byte offset of the destination slot (block/slot part)
@@ -196,77 +213,76 @@ __global__ __launch_bounds__((DecodeShape<ET, D, G>::NW * 64)) void paged_decode
   const int nch = (end - start + kChunk - 1) / kChunk;
   const int my_chunks = nch > wave ? (nch - wave + NW - 1) / NW : 0;
 
-  // Issue the K/V loads of the wave's k-th chunk; `valid` gets bit r for every
-  // attended row.
-  auto load_chunk = [&](int k, uint4 (&kr)[NR], uint4 (&vr)[NR], uint32_t& valid) {
-    const int c = wave + NW * k;
-    const int tb = start + c * kChunk;
-    int64_t chunk_blk = 0;
-    if (p.block_is_chunk_aligned)
-      chunk_blk = (k < 64 && c * kChunk < P) ? (int64_t)__builtin_amdgcn_readlane(tab, k)
-                                             : table_entry(p, table_row, tb / p.block_size);
+  // Issue the K/V loads of the wave's k-th chunk.  `cb` is the chunk's block
+  // (16-aligned blocks) and `rbk` the per-row blocks (other block sizes),
+  // `mbits` the key_valid_mask bits of its rows; all were read before the
+  // chunk group's first K/V load.  No loaded value is consumed here: a value
+  // needed at a branch join makes the compiler wait for every outstanding
+  // load (s_waitcnt vmcnt(0)), which would serialise the K/V traffic.
+  // `valid` gets bit r for every attended row.
+  auto load_chunk = [&](int k, int32_t cb, const int32_t* rbk, uint32_t mbits, uint4 (&kr)[NR],
+                        uint4 (&vr)[NR], uint32_t& valid) {
+    const int tb = start + (wave + NW * k) * kChunk;
     valid = 0;
+    // Uniform: does this chunk hold the current row (read from new_k/new_v)?
+    const bool has_cur = new_tok >= tb && new_tok < tb + kChunk;
 #pragma unroll
     for (int r = 0; r < NR; ++r) {
       const int tok = tb + rg + r * RPL;
-      bool ok = tok < end;
-      int64_t blk = chunk_blk;
-      if (!p.block_is_chunk_aligned && ok) blk = table_entry(p, table_row, tok / p.block_size);
-      ok = ok && blk >= 0 && blk < p.num_blocks;
-      if (ok && p.valid != nullptr && tok < p.valid_len)
-        ok = p.valid[b * p.valid_sb + tok] != 0;
-      // The current row is loaded (and later written) even when it is masked.
-      if (ok || tok == new_tok) {
-        const char* kaddr;
-        const char* vaddr;
-        if (tok == new_tok) {
-          kaddr = p.new_k + b * p.n_sb + h * p.n_sh + col * 16;
-          vaddr = p.new_v + b * p.n_sb + h * p.n_sh + col * 16;
-        } else {
-          const int64_t off = blk * p.s_blk + (int64_t)(tok % p.block_size) * p.s_slot + head_off;
-          kaddr = p.kp + off;
-          vaddr = p.vp + off;
+      const int32_t blk = kAligned ? cb : rbk[r];
+      const bool ok = tok < end && blk >= 0 && blk < p.num_blocks && ((mbits >> r) & 1u);
+      valid |= (ok ? 1u : 0u) << r;
+      kr[r] = make_uint4(0, 0, 0, 0);
+      vr[r] = make_uint4(0, 0, 0, 0);
+      if (p.pool_off32 && !has_cur) {
+        // 32-bit offsets from the pool bases: one VGPR per address.
+        if (ok) {
+          const uint32_t off = (uint32_t)blk * (uint32_t)p.s_blk +
+                               (uint32_t)(tok % p.block_size) * (uint32_t)p.s_slot +
+                               (uint32_t)head_off;
+          kr[r] = ld16(p.kp + off);
+          vr[r] = ld16(p.vp + off);
         }
-        kr[r] = ld16(kaddr);
-        vr[r] = ld16(vaddr);
-        valid |= (ok ? 1u : 0u) << r;
       } else {
-        kr[r] = make_uint4(0, 0, 0, 0);
-        vr[r] = make_uint4(0, 0, 0, 0);
+        const bool cur = tok == new_tok;
+        // The current row is loaded (from new_k/new_v) even when it is masked.
+        if (ok || cur) {
+          const int64_t off =
+              (int64_t)blk * p.s_blk + (int64_t)(tok % p.block_size) * p.s_slot + head_off;
+          const char* kaddr = cur ? p.new_k + b * p.n_sb + h * p.n_sh + col * 16 : p.kp + off;
+          const char* vaddr = cur ? p.new_v + b * p.n_sb + h * p.n_sh + col * 16 : p.vp + off;
+          kr[r] = ld16(kaddr);
+          vr[r] = ld16(vaddr);
+        }
+      }
+    }
+  };
+
+  // Fused write of the current row from its register copy (exactly one lane
+  // group in the grid holds it).
+  auto store_current_row = [&](int k, const uint4 (&kr)[NR], const uint4 (&vr)[NR]) {
+    const int tb = start + (wave + NW * k) * kChunk;
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+      if (tb + rg + r * RPL == new_tok) {
+        st16(p.kp + new_dst + head_off, kr[r]);
+        st16(p.vp + new_dst + head_off, vr[r]);
       }
     }
   };
 
   auto process_chunk = [&](int k, const uint4 (&kr)[NR], const uint4 (&vr)[NR], uint32_t valid) {
-    // Fused write of the current row (exactly one lane group in the grid).
-    if (new_tok >= 0) {
-      const int tb = start + (wave + NW * k) * kChunk;
-#pragma unroll
-      for (int r = 0; r < NR; ++r) {
-        if (tb + rg + r * RPL == new_tok) {
-          st16(p.kp + new_dst + head_off, kr[r]);
-          st16(p.vp + new_dst + head_off, vr[r]);
-        }
-      }
-    }
     float s[NR][G];
 #pragma unroll
-    for (int r = 0; r < NR; ++r) {
-      float kf[E];
-      ET::unpack(kr[r], kf);
+    for (int r = 0; r < NR; ++r)
 #pragma unroll
-      for (int g = 0; g < G; ++g) {
-        float acc = 0.f;
-#pragma unroll
-        for (int e = 0; e < E; ++e) acc = fmaf(qv[g][e], kf[e], acc);
-        s[r][g] = acc;
-      }
-    }
+      for (int g = 0; g < G; ++g) s[r][g] = ET::dot(qv[g], kr[r], 0.f);
 #pragma unroll
     for (int r = 0; r < NR; ++r)
 #pragma unroll
       for (int g = 0; g < G; ++g) {
-        const float t = group_sum<LPR>(s[r][g]);
+        float t = group_sum<LPR>(s[r][g]);
+        if constexpr (kScaleAfter) t *= p.scale_log2;
         s[r][g] = ((valid >> r) & 1u) ? t : -INFINITY;
       }
 #pragma unroll
@@ -297,14 +313,47 @@ __global__ __launch_bounds__((DecodeShape<ET, D, G>::NW * 64)) void paged_decode
     }
   };
 
-  // CPW chunks per group: all their loads are issued before the first is reduced.
+  // CPW chunks per group: read their block ids (and mask bits) first, then
+  // issue all their K/V loads, then reduce them in order.
+  constexpr int kRbk = kAligned ? 1 : CPW * NR;
   for (int k0 = 0; k0 < my_chunks; k0 += CPW) {
+    int32_t cb[CPW];
+    int32_t rbk[kRbk];
+    uint32_t mbits[CPW];
+#pragma unroll
+    for (int j = 0; j < CPW; ++j) {
+      const int k = k0 + j;
+      const int c = wave + NW * k;
+      const int tb = start + c * kChunk;
+      cb[j] = 0;
+      mbits[j] = (1u << NR) - 1;
+      if (k >= my_chunks) continue;
+      if constexpr (kAligned) {
+        cb[j] = (k < 64 && c * kChunk < P) ? __builtin_amdgcn_readlane(tab, k)
+                                          : (int32_t)table_entry(p, table_row, tb / p.block_size);
+      } else {
+#pragma unroll
+        for (int r = 0; r < NR; ++r) {
+          const int tok = tb + rg + r * RPL;
+          rbk[j * NR + r] = tok < end ? (int32_t)table_entry(p, table_row, tok / p.block_size) : 0;
+        }
+      }
+      if (p.valid != nullptr) {
+#pragma unroll
+        for (int r = 0; r < NR; ++r) {
+          const int tok = tb + rg + r * RPL;
+          if (tok < end && tok < p.valid_len && p.valid[b * p.valid_sb + tok] == 0)
+            mbits[j] &= ~(1u << r);
+        }
+      }
+    }
     uint4 kr[CPW][NR], vr[CPW][NR];
     uint32_t valid[CPW];
 #pragma unroll
     for (int j = 0; j < CPW; ++j) {
       if (k0 + j < my_chunks) {
-        load_chunk(k0 + j, kr[j], vr[j], valid[j]);
+        load_chunk(k0 + j, cb[j], kAligned ? rbk : rbk + (kAligned ? 0 : j * NR), mbits[j], kr[j],
+                   vr[j], valid[j]);
       } else {
         valid[j] = 0;
 #pragma unroll
@@ -312,8 +361,13 @@ __global__ __launch_bounds__((DecodeShape<ET, D, G>::NW * 64)) void paged_decode
       }
     }
 #pragma unroll
-    for (int j = 0; j < CPW; ++j)
-      if (k0 + j < my_chunks) process_chunk(k0 + j, kr[j], vr[j], valid[j]);
+    for (int j = 0; j < CPW; ++j) {
+      if (k0 + j < my_chunks) {
+        process_chunk(k0 + j, kr[j], vr[j], valid[j]);
+        // After the chunk's reduction, so the store adds no wait in front of it.
+        if (new_tok >= 0) store_current_row(k0 + j, kr[j], vr[j]);
+      }
+    }
   }
 
   // Wave result: sum l and o over row groups (lanes sharing `col`).
@@ -364,35 +418,36 @@ __global__ __launch_bounds__((DecodeShape<ET, D, G>::NW * 64)) void paged_decode
       }
     } else {
       const int64_t slot = (pair * p.max_parts + part) * G + g;
-      __hip_atomic_store(p.part_o + slot * D + d, Ot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      p.part_o[slot * D + d] = Ot;
       if (d == 0) {
-        __hip_atomic_store(p.part_ml + slot * 2, M, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(p.part_ml + slot * 2 + 1, Lt, __ATOMIC_RELAXED,
-                           __HIP_MEMORY_SCOPE_AGENT);
+        p.part_ml[slot * 2] = M;
+        p.part_ml[slot * 2 + 1] = Lt;
       }
     }
   }
-  if (nparts == 1) return;
+}
 
-  // Cross-workgroup merge: the last partition to finish combines all of them.
-  // The partials above were written with device-scope stores, which write
-  // through the per-XCD L2 to the device coherence point, and the merge below
-  // reads them with device-scope loads, which do not hit stale L2 lines.  So
-  // publishing only needs this workgroup's stores to have completed before
-  // its counter increment (s_waitcnt 0 + barrier); a __threadfence() here
-  // would instead write back the whole L2 of the XCD in every merging
-  // workgroup, which measured ~6x slower on MI355X.
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-  if (tid == 0) {
-    const int prev = atomicAdd(p.counters + pair, 1);
-    s_last = prev == nparts - 1;
-  }
-  __syncthreads();
-  if (!s_last) return;
-
+// Merge of the partitions of one (sequence, kv head) pair: out = sum_q
+// 2^(m_q - M) o_q / sum_q 2^(m_q - M) l_q with M = max_q m_q.  Pairs that
+// fit one partition were written by the first kernel and are skipped.
+template <typename ET, int D, int G>
+__global__ __launch_bounds__(256) void paged_decode_merge_kernel(DecodeParams p) {
+  constexpr int E = ET::kPerVec;
+  const int h = blockIdx.x;
+  const int b = blockIdx.y;
+  int L;
+  if (p.lens_cum)
+    L = (int)(load_index(p.lens, b + 1, p.lens_i64) - load_index(p.lens, b, p.lens_i64));
+  else
+    L = (int)load_index(p.lens, b, p.lens_i64);
+  L = __builtin_amdgcn_readfirstlane(L);
+  if (L <= 0) return;
+  int nparts = (L + p.split_tokens - 1) / p.split_tokens;
+  if (nparts > p.max_parts) nparts = p.max_parts;
+  if (nparts <= 1) return;
+  const int64_t pair = (int64_t)b * p.num_kv_heads + h;
   constexpr int kBatch = 8;  // partials whose loads are in flight together
-  for (int idx = tid; idx < G * D; idx += NT) {
+  for (int idx = threadIdx.x; idx < G * D; idx += 256) {
     const int g = idx / D, d = idx % D;
     float M = kNegBig, Lt = 0.f, Ot = 0.f;
     for (int q0 = 0; q0 < nparts; q0 += kBatch) {
@@ -404,12 +459,9 @@ __global__ __launch_bounds__((DecodeShape<ET, D, G>::NW * 64)) void paged_decode
         oq[j] = 0.f;
         if (q0 + j < nparts) {
           const int64_t slot = (pair * p.max_parts + q0 + j) * G + g;
-          mq[j] = __hip_atomic_load(p.part_ml + slot * 2, __ATOMIC_RELAXED,
-                                    __HIP_MEMORY_SCOPE_AGENT);
-          lq[j] = __hip_atomic_load(p.part_ml + slot * 2 + 1, __ATOMIC_RELAXED,
-                                    __HIP_MEMORY_SCOPE_AGENT);
-          oq[j] = __hip_atomic_load(p.part_o + slot * D + d, __ATOMIC_RELAXED,
-                                    __HIP_MEMORY_SCOPE_AGENT);
+          mq[j] = p.part_ml[slot * 2];
+          lq[j] = p.part_ml[slot * 2 + 1];
+          oq[j] = p.part_o[slot * D + d];
         }
       }
 #pragma unroll
@@ -432,13 +484,13 @@ __global__ __launch_bounds__((DecodeShape<ET, D, G>::NW * 64)) void paged_decode
       *reinterpret_cast<uint16_t*>(dst) = (uint16_t)(u.x & 0xffffu);
     }
   }
-  if (tid == 0) __hip_atomic_store(p.counters + pair, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // ----------------------------------------------------------------- host side
-// Workgroups resident at once on the 256 CUs of an MI355X (one 16-wave
-// workgroup per CU); the split aims to give every CU one workgroup.
-constexpr int kDecodeTargetWorkgroups = 256;
+// Longest context a sequence may be split into without growing the
+// partition: beyond kMaxParts partitions the partition grows instead, which
+// bounds the merge kernel's loop.
+constexpr int kMaxParts = 256;
 
 struct DecodePlan {
   int split_tokens;
@@ -448,29 +500,60 @@ struct DecodePlan {
 
 template <typename ET, int D, int G>
 static int decode_unit() {
-  return DecodeShape<ET, D, G>::NW * kChunk;  // one chunk per wave
+  // one round of CPW chunks on every wave of a workgroup
+  return DecodeShape<ET, D, G>::NW * DecodeShape<ET, D, G>::CPW * kChunk;
 }
 
 static int decode_unit_for(int dtype, int D, int G);
+
+// Compute units of the current device (cached per device; 256, the MI355X
+// count, when no device is visible, e.g. when only the workspace size is
+// queried on a host without a GPU).
+static int current_device_cus() {
+  static std::atomic<int> cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0) {
+    (void)hipGetLastError();
+    return 256;
+  }
+  if (dev < 64) {
+    const int v = cache[dev].load(std::memory_order_relaxed);
+    if (v > 0) return v;
+  }
+  int n = 0;
+  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      n <= 0) {
+    (void)hipGetLastError();
+    n = 256;
+  }
+  if (dev < 64) cache[dev].store(n, std::memory_order_relaxed);
+  return n;
+}
 
 static DecodePlan plan_decode(const va_decode_args* a) {
   DecodePlan pl{};
   const int G = a->num_kv_heads > 0 ? a->num_heads / a->num_kv_heads : 1;
   int unit = decode_unit_for(a->dtype, a->head_dim, G);
-  if (unit <= 0) unit = 256;
+  if (unit <= 0) unit = 128;
   const int max_len = a->max_seq_len > 0 ? a->max_seq_len : 1;
   int P = a->split_tokens;
+  const int64_t pairs = (int64_t)a->num_seqs * a->num_kv_heads;
   if (P <= 0) {
-    const int64_t pairs = (int64_t)a->num_seqs * a->num_kv_heads;
-    int64_t want = (kDecodeTargetWorkgroups + pairs - 1) / (pairs > 0 ? pairs : 1);
-    if (want < 1) want = 1;
+    // Split contexts only as far as needed to give every CU one workgroup:
+    // with at least as many (sequence, kv head) pairs as CUs, one partition
+    // per pair.  Partitions are at least one round of in-flight chunks and
+    // at most kMaxParts per context.
+    const int64_t cus = current_device_cus();
+    const int64_t want = pairs >= cus ? 1 : cus / (pairs > 0 ? pairs : 1);
     P = (int)((max_len + want - 1) / want);
+    if (P < unit) P = unit;
+    const int cap = (max_len + kMaxParts - 1) / kMaxParts;
+    if (P < cap) P = cap;
   }
   P = ((P + unit - 1) / unit) * unit;
   if (P < unit) P = unit;
   pl.split_tokens = P;
   pl.max_parts = (max_len + P - 1) / P;
-  const int64_t pairs = (int64_t)a->num_seqs * a->num_kv_heads;
   if (pl.max_parts > 1) {
     pl.ml_bytes = ((size_t)pairs * pl.max_parts * G * 2 * 4 + 255) / 256 * 256;
     pl.o_bytes = (size_t)pairs * pl.max_parts * G * a->head_dim * 4;
@@ -481,8 +564,15 @@ static DecodePlan plan_decode(const va_decode_args* a) {
 
 template <typename ET, int D, int G>
 static void launch_decode(const DecodeParams& p, dim3 grid, hipStream_t s) {
-  hipLaunchKernelGGL((paged_decode_kernel<ET, D, G>), grid,
-                     dim3(DecodeShape<ET, D, G>::NW * 64), 0, s, p);
+  if (p.block_is_chunk_aligned)
+    hipLaunchKernelGGL((paged_decode_kernel<ET, D, G, true>), grid,
+                       dim3(DecodeShape<ET, D, G>::NW * 64), 0, s, p);
+  else
+    hipLaunchKernelGGL((paged_decode_kernel<ET, D, G, false>), grid,
+                       dim3(DecodeShape<ET, D, G>::NW * 64), 0, s, p);
+  if (p.max_parts > 1)
+    hipLaunchKernelGGL((paged_decode_merge_kernel<ET, D, G>), dim3(grid.y, grid.x), dim3(256), 0,
+                       s, p);
 }
 
 template <typename ET, int D>
@@ -555,7 +645,7 @@ extern "C" int va_paged_decode(const va_decode_args* a, void* stream) {
   VA_CHECK_ARG(eb != 0, "va_paged_decode: unknown dtype %d", a->dtype);
   VA_CHECK_ARG(a->num_seqs >= 0, "va_paged_decode: num_seqs < 0");
   if (a->num_seqs == 0) return VA_OK;
-  VA_CHECK_ARG(a->num_seqs <= 65535, "va_paged_decode: num_seqs > 65535");
+  VA_CHECK_ARG(a->num_seqs <= 65535, "va_paged_decode: num_seqs > 65535");  // merge grid.y
   VA_CHECK_ARG(a->q && a->out && a->pool.k && a->pool.v && a->block_tables && a->lens,
                "va_paged_decode: null pointer argument");
   VA_CHECK_ARG(a->num_kv_heads > 0 && a->num_heads > 0 && a->num_heads % a->num_kv_heads == 0,
@@ -594,12 +684,6 @@ extern "C" int va_paged_decode(const va_decode_args* a, void* stream) {
                 a->workspace_bytes);
       return VA_ERR_WORKSPACE;
     }
-    const int64_t pairs = (int64_t)a->num_seqs * a->num_kv_heads;
-    if (a->counters == nullptr || a->counters_len < pairs) {
-      set_error("va_paged_decode: %lld zero-initialised counters needed, %lld given",
-                (long long)pairs, (long long)a->counters_len);
-      return VA_ERR_WORKSPACE;
-    }
     VA_CHECK_ARG((uintptr_t)a->workspace % 16 == 0, "va_paged_decode: workspace alignment");
   }
   VA_CHECK_ARG(pl.max_parts <= 65535, "va_paged_decode: too many context partitions");
@@ -619,6 +703,16 @@ extern "C" int va_paged_decode(const va_decode_args* a, void* stream) {
   p.block_size = a->pool.block_size;
   p.num_blocks = a->pool.num_blocks;
   p.block_is_chunk_aligned = a->pool.block_size % kChunk == 0;
+  {
+    // Largest byte offset inside one pool: the last slot of the last head of
+    // the last block, plus a row.
+    const int64_t last = (int64_t)(a->pool.num_blocks > 0 ? a->pool.num_blocks - 1 : 0) *
+                             a->pool.stride_block +
+                         (int64_t)(a->pool.block_size - 1) * a->pool.stride_slot +
+                         (int64_t)(a->num_kv_heads - 1) * a->pool.stride_head + a->head_dim;
+    p.pool_off32 = last * eb < ((int64_t)1 << 32) && a->pool.stride_block >= 0 &&
+                   a->pool.stride_slot >= 0 && a->pool.stride_head >= 0;
+  }
   p.table = a->block_tables;
   p.t_sb = a->table_stride_seq;
   p.table_i64 = a->table_dtype == VA_I64;
@@ -640,11 +734,10 @@ extern "C" int va_paged_decode(const va_decode_args* a, void* stream) {
   p.max_parts = pl.max_parts;
   p.scale_log2 = a->scale * 1.4426950408889634f;
   char* ws = (char*)a->workspace;
-  p.counters = pl.total_bytes ? a->counters : nullptr;
   p.part_ml = pl.total_bytes ? (float*)ws : nullptr;
   p.part_o = pl.total_bytes ? (float*)(ws + pl.ml_bytes) : nullptr;
 
-  const dim3 grid(pl.max_parts, a->num_kv_heads, a->num_seqs);
+  const dim3 grid(a->num_seqs, a->num_kv_heads, pl.max_parts);
   const hipStream_t s = (hipStream_t)stream;
   bool ok = false;
   switch (a->dtype) {

@@ -130,7 +130,6 @@ def store_kvcache(
 
 # -------------------------------------------------------------------- decode
 _WORKSPACES: dict[int, torch.Tensor] = {}
-_COUNTERS: dict[int, torch.Tensor] = {}
 
 
 def _device_index(device: torch.device) -> int:
@@ -139,7 +138,8 @@ def _device_index(device: torch.device) -> int:
 
 def decode_workspace(device: torch.device, nbytes: int) -> torch.Tensor | None:
     """Partial-result workspace shared by decode launches on one device (no
-    initialisation needed; grows by doubling)."""
+    initialisation needed; grows by doubling; launches sharing it are
+    ordered on one stream)."""
     if nbytes == 0:
         return None
     key = _device_index(device)
@@ -151,26 +151,9 @@ def decode_workspace(device: torch.device, nbytes: int) -> torch.Tensor | None:
     return ws
 
 
-def decode_counters(device: torch.device, count: int) -> torch.Tensor:
-    """Zero-filled int32 arrival counters of the in-launch merge.
-
-    Every launch leaves the counters it used at zero, so the buffer is
-    zero-filled only when it is (re)allocated and holds nothing else.
-    """
-    key = _device_index(device)
-    cnt = _COUNTERS.get(key)
-    if cnt is None or cnt.numel() < count:
-        size = max(count, 1024, 0 if cnt is None else 2 * cnt.numel())
-        cnt = torch.zeros(size, dtype=torch.int32, device=device)
-        _COUNTERS[key] = cnt
-    return cnt
-
-
-def reserve_decode_workspace(device: torch.device, nbytes: int, pairs: int) -> None:
-    """Allocate the decode workspace and counters up front (before HIP graph capture)."""
-    device = torch.device(device)
-    decode_workspace(device, nbytes)
-    decode_counters(device, pairs)
+def reserve_decode_workspace(device: torch.device, nbytes: int) -> None:
+    """Allocate the decode workspace up front (before HIP graph capture)."""
+    decode_workspace(torch.device(device), nbytes)
 
 
 def paged_decode(
@@ -266,9 +249,6 @@ def paged_decode(
     if ws is not None:
         args.workspace = ws.data_ptr()
         args.workspace_bytes = ws.numel()
-        cnt = decode_counters(device, B * hkv)
-        args.counters = cnt.data_ptr()
-        args.counters_len = cnt.numel()
     N.call("va_paged_decode", args, device)
     return out
 
