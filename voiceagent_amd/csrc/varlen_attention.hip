@@ -59,6 +59,7 @@ struct VarlenParams {
   const void* slots;
   int32_t slot_i64;
   int32_t num_qblocks;
+  int32_t num_seqs, num_kv_heads;
 };
 
 template <bool kBF16>
@@ -71,10 +72,15 @@ struct Mma {
       return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a),
                                                     __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
   }
+  // Two floats to a packed 16-bit pair, round to nearest even (bf16 through
+  // gfx950's v_cvt_pk_bf16_f32).
   __device__ static inline uint32_t pack2(float lo, float hi) {
-    if constexpr (kBF16)
-      return (uint32_t)BF16::from_float(lo) | ((uint32_t)BF16::from_float(hi) << 16);
-    else
+    if constexpr (kBF16) {
+      bf16x2_t v;
+      v.x = (__bf16)lo;
+      v.y = (__bf16)hi;
+      return __builtin_bit_cast(uint32_t, v);
+    } else
       return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)lo) |
              ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)hi) << 16);
   }
@@ -83,6 +89,55 @@ struct Mma {
 constexpr int kVarlenThreads = 256;
 constexpr int kRowsPerWG = 128;
 constexpr int kKeyTile = 64;
+// MI355X hands workgroup i of a launch to XCD i % 8; each XCD has its own L2.
+constexpr int kXcds = 8;
+// Lazy-rescale slack of the online softmax, in log2 units (p <= 2^kLazy).
+constexpr float kLazy = 8.0f;
+
+// 16 zero bytes: the DMA source of every lane whose key row is past the end
+// of the visible keys or unmapped, so every tile takes the same number of
+// DMA instructions (the pipeline's vmcnt waits count them).
+__device__ __align__(16) const uint4 kZeroRow = {0u, 0u, 0u, 0u};
+
+// One 16-byte global -> LDS transfer per lane (global_load_lds_dwordx4):
+// lane l's bytes land at lds_base + 16 l.  Issued as inline asm so the
+// compiler does not wait on it before unrelated LDS reads; the kernel waits
+// for it explicitly with wait_vmcnt.
+__device__ inline void dma16(const void* src, uint32_t lds_base) {
+  asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(src), "{m0}"(lds_base) : "memory");
+}
+// The same from a wave-uniform base plus a 32-bit per-lane byte offset.
+__device__ inline void dma16(uint32_t off, const void* base, uint32_t lds_base) {
+  asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "{m0}"(lds_base)
+               : "memory");
+}
+
+__device__ inline const char* uniform_ptr(const char* ptr) {
+  const uint64_t u = (uint64_t)(uintptr_t)ptr;
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)u);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(u >> 32));
+  return (const char*)(uintptr_t)(((uint64_t)hi << 32) | lo);
+}
+
+// s_waitcnt vmcnt(N), no wait on the other counters (gfx9 encoding).
+template <int N>
+__device__ inline void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// LDS layout of a staged K or V tile: kKeyTile rows of 2 D bytes, unpadded;
+// the 16-byte chunk c of row r sits at chunk position c ^ swz(r).  The XOR
+// spreads the 16 rows of one K read (ds_read_b128, one chunk per row) and
+// the 8 rows x 2 chunks of half a V read (ds_read_b64_tr_b16) over distinct
+// banks.  swz depends on r % 16 only.
+template <int D>
+__device__ inline int swz(int row) {
+  if constexpr (D == 128)
+    return ((row & 7) << 1) | ((row >> 3) & 1);
+  else
+    return (((row >> 1) & 3) << 1) | ((row >> 3) & 1);
+}
 
 __device__ inline uint4 lds_read16(const char* base, int off) {
   return *reinterpret_cast<const uint4*>(base + off);
@@ -92,60 +147,194 @@ __device__ inline s16x4_t lds_read_tr(const char* base, int off) {
   return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)(base + off));
 }
 
-template <bool kBF16, int D, int G, bool kCausal>
+// kPaged: keys j < k_len - q_len come from the pool through the block table
+// (launches with a pool); otherwise every key comes from k/v.
+template <bool kBF16, int D, int G, bool kCausal, bool kPaged>
 __global__ __launch_bounds__(kVarlenThreads, 2) void varlen_attention_kernel(VarlenParams p) {
   constexpr int BQ = kRowsPerWG / G;       // query positions per workgroup
   constexpr int DS = D / 32;               // k-steps of the S^T MFMA
   constexpr int DT = D / 16;               // 16-wide d tiles of O^T
-  constexpr int CPR = D * 2 / 16;          // 16-byte chunks per K/V row
-  constexpr int LDS_ROW = D * 2 + 32;      // padded row pitch in bytes
+  constexpr int ROWB = D * 2;              // bytes per K/V row
+  constexpr int CPR = ROWB / 16;           // 16-byte chunks per row
+  constexpr int RPI = 64 / CPR;            // rows per DMA instruction (1 KiB)
+  constexpr int TILE_B = kKeyTile * ROWB;  // bytes of one K (or V) tile
+  constexpr int NI = TILE_B / 1024 / 4;    // DMA instructions per wave per tile, K or V
   constexpr int KT = kKeyTile / 16;        // 16-key tiles per key tile
   constexpr int KS = kKeyTile / 32;        // 32-key MFMA steps per key tile
-  constexpr int LOADS = kKeyTile * CPR / kVarlenThreads;
   static_assert(BQ % 16 == 0, "query block must hold whole 16-row tiles");
-  static_assert(LOADS * kVarlenThreads == kKeyTile * CPR, "tile load split");
+  static_assert(NI * 4 * 1024 == TILE_B, "tile DMA split");
   using M = Mma<kBF16>;
 
-  __shared__ __align__(16) char s_kv[2 * kKeyTile * LDS_ROW];
-  char* s_k = s_kv;
-  char* s_v = s_kv + kKeyTile * LDS_ROW;
+  // Two stages of (K tile, V tile): the next tile streams in while the
+  // current one is reduced.
+  __shared__ __align__(1024) char s_kv[2 * 2 * TILE_B];
 
-  const int qb = p.num_qblocks - 1 - (int)blockIdx.x;  // heavy (late) blocks first
-  const int h = blockIdx.y;
-  const int s = blockIdx.z;
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
   const int lane = tid & 63;
   const int r16 = lane & 15;
   const int g4 = lane >> 4;
 
-  const int q0 = p.cu_q[s];
-  const int ql = p.cu_q[s + 1] - q0;
-  const int k0 = p.cu_k[s];
-  const int kl = p.cu_k[s + 1] - k0;
+  // XCD-aware schedule: the query blocks of one (sequence, kv head) pair all
+  // go to one XCD, whose L2 then serves the K/V rows they share.  XCD x owns
+  // pairs x, x + 8, ... and works through a list of their live query blocks
+  // (blocks past a sequence's end are left out, so no slot is spent on
+  // them); workgroup 8 i + x takes item i of that list, and items past its
+  // end exit.  With at most 64 pairs per XCD, lane k of every wave reads
+  // pair k's lengths and the list is formed with wave ballots; otherwise
+  // the list holds every (pair, block) and dead blocks exit on arrival.
+  const int nqb = p.num_qblocks;
+  const int npairs = p.num_seqs * p.num_kv_heads;
+  const int xcd = (int)blockIdx.x % kXcds;
+  const int local = (int)blockIdx.x / kXcds;
+  const int ppx = (npairs - xcd + kXcds - 1) / kXcds;  // pairs on this XCD
+  int s, h, qb, q0, ql, k0, kl;
+  if (ppx <= 64) {
+    int nq = 0, lq0 = 0, lql = 0, lk0 = 0, lkl = 0;
+    if (lane < ppx) {
+      const int ls = (xcd + kXcds * lane) / p.num_kv_heads;
+      lq0 = p.cu_q[ls];
+      lql = p.cu_q[ls + 1] - lq0;
+      lk0 = p.cu_k[ls];
+      lkl = p.cu_k[ls + 1] - lk0;
+      nq = (lql + BQ - 1) / BQ;
+    }
+    int ksel;
+    // Level-major: every pair's last block, then every pair's second to
+    // last, ... (late blocks are the heavy ones under causal masking).
+    int rem = local;
+    ksel = -1;
+    qb = -1;
+    for (int lev = nqb - 1; lev >= 0; --lev) {
+      const uint64_t live = __builtin_amdgcn_ballot_w64(nq > lev);
+      const int cnt = __popcll(live);
+      if (rem < cnt) {
+        const int below = __builtin_amdgcn_mbcnt_hi((uint32_t)(live >> 32),
+                                                     __builtin_amdgcn_mbcnt_lo((uint32_t)live, 0));
+        ksel = __builtin_ctzll(__builtin_amdgcn_ballot_w64(nq > lev && below == rem));
+        qb = lev;
+        break;
+      }
+      rem -= cnt;
+    }
+    if (qb < 0) return;
+    const int pair = xcd + kXcds * ksel;
+    s = pair / p.num_kv_heads;
+    h = pair % p.num_kv_heads;
+    q0 = __shfl(lq0, ksel, 64);
+    ql = __shfl(lql, ksel, 64);
+    k0 = __shfl(lk0, ksel, 64);
+    kl = __shfl(lkl, ksel, 64);
+  } else {
+    if (local >= ppx * nqb) return;
+    qb = nqb - 1 - local / ppx;
+    const int pair = xcd + kXcds * (local % ppx);
+    s = pair / p.num_kv_heads;
+    h = pair % p.num_kv_heads;
+    q0 = p.cu_q[s];
+    ql = p.cu_q[s + 1] - q0;
+    k0 = p.cu_k[s];
+    kl = p.cu_k[s + 1] - k0;
+  }
   const int pos0 = qb * BQ;
   if (pos0 >= ql) return;
   const int pos_end = min(ql, pos0 + BQ);
   const int diag = kl - ql;  // bottom-right alignment offset
-  const int pool_prefix = p.has_pool ? (p.k != nullptr ? kl - ql : kl) : 0;
+  const int pool_prefix = kPaged ? (p.k != nullptr ? kl - ql : kl) : 0;
+  const int kend = kCausal ? max(0, min(kl, diag + pos_end)) : kl;
+  const int ntiles = (kend + kKeyTile - 1) / kKeyTile;
+  const int64_t table_row = (int64_t)s * p.t_sb;
+  const uint32_t lds_base = __builtin_amdgcn_readfirstlane(
+      (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)s_kv);
+
+  // ---- DMA of key tile [kb, kb + 64) into stage st ----
+  // Wave w fills 1 KiB blocks w NI .. w NI + NI - 1 of the K and V tiles;
+  // lane l of a block writes row RPI * block + l / CPR, chunk position l % CPR,
+  // so it reads logical chunk (l % CPR) ^ swz(row) of that key.  Every lane
+  // issues exactly 2 NI DMAs per tile.
+  // Keys from k/v: key j is row new_base + j of k and v.
+  const int64_t new_base = kPaged ? (int64_t)q0 - pool_prefix : (int64_t)k0;
+  uint32_t koff[NI], voff[NI];  // per-lane byte offsets inside a tile of k/v rows
+#pragma unroll
+  for (int i = 0; i < NI; ++i) {
+    const int row = (wave * NI + i) * RPI + lane / CPR;
+    const int chunk = (lane % CPR) ^ swz<D>(row);
+    koff[i] = (uint32_t)(row * p.k_st + chunk * 16);
+    voff[i] = (uint32_t)(row * p.v_st + chunk * 16);
+  }
+  const char* zero_row = reinterpret_cast<const char*>(&kZeroRow);
+  auto issue_tile = [&](int kb, int st) {
+    const uint32_t dst0 = lds_base + (uint32_t)(st * 2 * TILE_B + wave * NI * 1024);
+    if (kb >= pool_prefix && kb + kKeyTile <= kend) {
+      // Whole tile from k/v: uniform bases, constant lane offsets.
+      const char* kbase = uniform_ptr(p.k + (new_base + kb) * p.k_st + h * p.k_sh);
+      const char* vbase = uniform_ptr(p.v + (new_base + kb) * p.v_st + h * p.v_sh);
+#pragma unroll
+      for (int i = 0; i < NI; ++i) {
+        dma16(koff[i], kbase, dst0 + i * 1024);
+        dma16(voff[i], vbase, dst0 + TILE_B + i * 1024);
+      }
+      return;
+    }
+    // Tile with pool keys or past kend: per-lane addresses; rows past kend
+    // or with an unmapped block read kZeroRow.
+    int64_t bid[NI];
+    if (kPaged && kb < pool_prefix) {
+      // Read all block ids first, so the loads share one wait.
+#pragma unroll
+      for (int i = 0; i < NI; ++i) {
+        const int j = kb + (wave * NI + i) * RPI + lane / CPR;
+        const int col = j / p.block_size;
+        bid[i] = (j < pool_prefix && j < kend && col < p.table_width)
+                     ? load_index(p.table, table_row + col, p.table_i64)
+                     : 0;
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      const int row = (wave * NI + i) * RPI + lane / CPR;
+      const int chunk = (lane % CPR) ^ swz<D>(row);
+      const int j = kb + row;
+      const char* ka = zero_row;
+      const char* va_ = zero_row;
+      if (j < kend) {
+        if (kPaged && j < pool_prefix) {
+          if (bid[i] >= 0 && bid[i] < p.num_blocks) {
+            const int64_t off = bid[i] * p.s_blk + (int64_t)(j % p.block_size) * p.s_slot +
+                                h * p.s_head + chunk * 16;
+            ka = p.kp + off;
+            va_ = p.vp + off;
+          }
+        } else {
+          ka = p.k + (new_base + j) * p.k_st + h * p.k_sh + chunk * 16;
+          va_ = p.v + (new_base + j) * p.v_st + h * p.v_sh + chunk * 16;
+        }
+      }
+      dma16(ka, dst0 + i * 1024);
+      dma16(va_, dst0 + TILE_B + i * 1024);
+    }
+  };
+
+  if (ntiles > 0) issue_tile(0, 0);
+  if (ntiles > 1) issue_tile(kKeyTile, 1);
 
   // ---- fused store of this block's new K/V rows (kv head h) ----
-  if (p.slots != nullptr) {
-    const int nrows = pos_end - pos0;
-    const int64_t cap = (int64_t)p.num_blocks * p.block_size;
-    for (int c = tid; c < nrows * CPR * 2; c += kVarlenThreads) {
-      const int is_v = c >= nrows * CPR;
-      const int cc = is_v ? c - nrows * CPR : c;
-      const int row = cc / CPR, chunk = cc % CPR;
-      const int tok = q0 + pos0 + row;
-      const int64_t slot = load_index(p.slots, tok, p.slot_i64);
-      if (slot < 0 || slot >= cap) continue;
+  // The new rows are keys [pool_prefix + pos0, pool_prefix + pos_end), which
+  // the tile loop stages in LDS anyway: each is copied from there to its
+  // slot, so k/v are read once.  TPR threads share a row; thread `sub` of a
+  // row moves items sub, sub + TPR, ... of its 2 CPR chunks (K then V).
+  constexpr int TPR = kVarlenThreads / BQ;
+  constexpr int IPT = 2 * CPR / TPR;
+  static_assert(TPR * BQ == kVarlenThreads && IPT * TPR == 2 * CPR, "store split");
+  const bool fused_store = kPaged && p.slots != nullptr;
+  const int st_row = tid / TPR, st_sub = tid % TPR;
+  const int st_key = pool_prefix + pos0 + st_row;  // key index of this thread's row
+  int64_t st_dst = -1;                             // pool byte offset of the row's slot
+  if (fused_store && pos0 + st_row < pos_end) {
+    const int64_t slot = load_index(p.slots, q0 + pos0 + st_row, p.slot_i64);
+    if (slot >= 0 && slot < (int64_t)p.num_blocks * p.block_size) {
       const int64_t blk = slot / p.block_size;
-      const char* src = (is_v ? p.v + tok * p.v_st + h * p.v_sh : p.k + tok * p.k_st + h * p.k_sh) +
-                        chunk * 16;
-      char* dst = (is_v ? p.vp : p.kp) + blk * p.s_blk + (slot - blk * p.block_size) * p.s_slot +
-                  h * p.s_head + chunk * 16;
-      st16(dst, ld16(src));
+      st_dst = blk * p.s_blk + (slot - blk * p.block_size) * p.s_slot + h * p.s_head;
     }
   }
 
@@ -170,6 +359,17 @@ __global__ __launch_bounds__(kVarlenThreads, 2) void varlen_attention_kernel(Var
         qreg[tt][ds] = make_uint4(0, 0, 0, 0);
     }
 
+  // Wait for the query (and, in order, everything issued before it) here, so
+  // the compiler has no load of its own pending inside the tile loop, where
+  // its wait would also stall on the next tile's DMA.
+#pragma unroll
+  for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+    for (int ds = 0; ds < DS; ++ds)
+      asm volatile("" ::"v"(qreg[tt][ds].x), "v"(qreg[tt][ds].y), "v"(qreg[tt][ds].z),
+                   "v"(qreg[tt][ds].w));
+  asm volatile("" ::"v"((uint32_t)st_dst), "v"((uint32_t)(st_dst >> 32)));
+
   float m[2] = {-1.0e30f, -1.0e30f};
   float l[2] = {0.f, 0.f};
   f32x4_t o[2][DT];
@@ -178,51 +378,40 @@ __global__ __launch_bounds__(kVarlenThreads, 2) void varlen_attention_kernel(Var
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) o[tt][dt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-  const int kend = kCausal ? max(0, min(kl, diag + pos_end)) : kl;
-  const int64_t table_row = (int64_t)s * p.t_sb;
-
-  for (int kb = 0; kb < kend; kb += kKeyTile) {
-    // ---- stage K/V tile [kb, kb + 64) into LDS ----
-    uint4 kbuf[LOADS], vbuf[LOADS];
+  // Visible keys per row: j < lim[tt]; tiles ending at or below lim_lo (the
+  // smallest limit in the workgroup) need no mask.  Rows past the end of the
+  // sequence have zero queries; their outputs are never written.
+  int lim[2];
 #pragma unroll
-    for (int i = 0; i < LOADS; ++i) {
-      const int c = tid + i * kVarlenThreads;
-      const int key = c / CPR, chunk = c % CPR;
-      const int j = kb + key;
-      kbuf[i] = make_uint4(0, 0, 0, 0);
-      vbuf[i] = make_uint4(0, 0, 0, 0);
-      if (j < kend) {
-        const char* ka = nullptr;
-        const char* va_ = nullptr;
-        if (j < pool_prefix) {
-          const int col = j / p.block_size;
-          const int64_t blk =
-              col < p.table_width ? load_index(p.table, table_row + col, p.table_i64) : 0;
-          if (blk >= 0 && blk < p.num_blocks) {
-            const int64_t off = blk * p.s_blk + (int64_t)(j % p.block_size) * p.s_slot +
-                                h * p.s_head + chunk * 16;
-            ka = p.kp + off;
-            va_ = p.vp + off;
-          }
-        } else {
-          const int64_t row = p.has_pool ? (int64_t)q0 + (j - pool_prefix) : (int64_t)k0 + j;
-          ka = p.k + row * p.k_st + h * p.k_sh + chunk * 16;
-          va_ = p.v + row * p.v_st + h * p.v_sh + chunk * 16;
-        }
-        if (ka != nullptr) {
-          kbuf[i] = ld16(ka);
-          vbuf[i] = ld16(va_);
-        }
+  for (int tt = 0; tt < 2; ++tt) lim[tt] = kCausal ? min(kend, diag + qpos[tt] + 1) : kend;
+  const int lim_lo = kCausal ? min(kend, diag + pos0 + 1) : kend;
+
+  // Swizzled chunk positions of this lane's reads (row % 16 is fixed per lane).
+  const int kswz = swz<D>(r16);
+  const int vswz = swz<D>(4 * g4 + (r16 >> 2));
+
+  for (int t = 0; t < ntiles; ++t) {
+    const int kb = t * kKeyTile;
+    // Tile t has landed once at most the 2 NI DMAs of tile t + 1 are pending;
+    // the barrier makes every wave's part of it visible.
+    if (t + 1 < ntiles)
+      wait_vmcnt<2 * NI>();
+    else
+      wait_vmcnt<0>();
+    __syncthreads();
+    const char* s_k = s_kv + (t & 1) * 2 * TILE_B;
+    const char* s_v = s_k + TILE_B;
+
+    if (fused_store && st_dst >= 0 && st_key >= kb && st_key < kb + kKeyTile) {
+      const int r = st_key - kb;
+#pragma unroll
+      for (int k = 0; k < IPT; ++k) {
+        const int e = st_sub + TPR * k;
+        const int c = e % CPR;
+        const uint4 w = lds_read16(e < CPR ? s_k : s_v, r * ROWB + ((c ^ swz<D>(r)) << 4));
+        st16((e < CPR ? p.kp : p.vp) + st_dst + c * 16, w);
       }
     }
-#pragma unroll
-    for (int i = 0; i < LOADS; ++i) {
-      const int c = tid + i * kVarlenThreads;
-      const int key = c / CPR, chunk = c % CPR;
-      *reinterpret_cast<uint4*>(s_k + key * LDS_ROW + chunk * 16) = kbuf[i];
-      *reinterpret_cast<uint4*>(s_v + key * LDS_ROW + chunk * 16) = vbuf[i];
-    }
-    __syncthreads();
 
     // ---- S^T = K Q^T for both row tiles ----
     f32x4_t sacc[2][KT];
@@ -232,42 +421,58 @@ __global__ __launch_bounds__(kVarlenThreads, 2) void varlen_attention_kernel(Var
       sacc[1][kt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int ds = 0; ds < DS; ++ds) {
-        const uint4 a = lds_read16(s_k, (16 * kt + r16) * LDS_ROW + (32 * ds + 8 * g4) * 2);
+        const uint4 a = lds_read16(s_k, (16 * kt + r16) * ROWB + (((4 * ds + g4) ^ kswz) << 4));
         sacc[0][kt] = M::mfma(a, qreg[0][ds], sacc[0][kt]);
         sacc[1][kt] = M::mfma(a, qreg[1][ds], sacc[1][kt]);
       }
     }
 
     // ---- online softmax (exp2 domain) and P^T packing ----
+    // Scores stay unscaled until the exponent: p = 2^(s c - m) with
+    // c = scale log2 e > 0 and m the row's running max of s c.  The max used
+    // as reference is raised only when a row's new max exceeds it by more
+    // than kLazy (or on the first scores); in between, p <= 2^kLazy, which
+    // the fp32 sums and 16-bit P hold exactly as well.  Key masking is
+    // applied only on tiles that cross a row's limit.
+    const bool need_mask = kb + kKeyTile > lim_lo;
     uint4 pb[2][KS];
 #pragma unroll
     for (int tt = 0; tt < 2; ++tt) {
       float sv[KT][4];
+      if (need_mask) {
+        const int rel = lim[tt] - kb - 4 * g4;  // key 16 kt + i of this lane is visible iff < rel
+#pragma unroll
+        for (int kt = 0; kt < KT; ++kt)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) sv[kt][i] = 16 * kt + i < rel ? sacc[tt][kt][i] : -INFINITY;
+      } else {
+#pragma unroll
+        for (int kt = 0; kt < KT; ++kt)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) sv[kt][i] = sacc[tt][kt][i];
+      }
       float mx = -INFINITY;
-      const int lim = kCausal ? min(kend, diag + qpos[tt] + 1) : kend;
 #pragma unroll
       for (int kt = 0; kt < KT; ++kt)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int j = kb + 16 * kt + 4 * g4 + i;
-          const float x = sacc[tt][kt][i] * p.scale_log2;
-          sv[kt][i] = (j < lim && qpos[tt] < ql) ? x : -INFINITY;
-          mx = fmaxf(mx, sv[kt][i]);
-        }
+        for (int i = 0; i < 4; ++i) mx = fmaxf(mx, sv[kt][i]);
       mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
       mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-      const float mnew = fmaxf(m[tt], mx);
-      const float alpha = fast_exp2(m[tt] - mnew);
-      m[tt] = mnew;
-      l[tt] *= alpha;
+      const float mxs = mx * p.scale_log2;
+      if (__builtin_amdgcn_ballot_w64(mxs > m[tt] + kLazy) != 0) {
+        const float mnew = fmaxf(m[tt], mxs);
+        const float alpha = fast_exp2(m[tt] - mnew);
+        m[tt] = mnew;
+        l[tt] *= alpha;
 #pragma unroll
-      for (int dt = 0; dt < DT; ++dt) o[tt][dt] *= alpha;
+        for (int dt = 0; dt < DT; ++dt) o[tt][dt] *= alpha;
+      }
       float pr[KT][4];
 #pragma unroll
       for (int kt = 0; kt < KT; ++kt)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          pr[kt][i] = fast_exp2(sv[kt][i] - mnew);
+          pr[kt][i] = fast_exp2(fmaf(sv[kt][i], p.scale_log2, -m[tt]));
           l[tt] += pr[kt][i];
         }
 #pragma unroll
@@ -284,9 +489,10 @@ __global__ __launch_bounds__(kVarlenThreads, 2) void varlen_attention_kernel(Var
     for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt) {
-        const int off = (32 * ks + 4 * g4 + (r16 >> 2)) * LDS_ROW + (16 * dt + 4 * (r16 & 3)) * 2;
+        const int off = (32 * ks + 4 * g4 + (r16 >> 2)) * ROWB +
+                        (((2 * dt + ((r16 >> 1) & 1)) ^ vswz) << 4) + ((r16 & 1) << 3);
         const s16x4_t lo = lds_read_tr(s_v, off);
-        const s16x4_t hi = lds_read_tr(s_v, off + 16 * LDS_ROW);
+        const s16x4_t hi = lds_read_tr(s_v, off + 16 * ROWB);
         uint4 a;
         a.x = (uint32_t)(uint16_t)lo[0] | ((uint32_t)(uint16_t)lo[1] << 16);
         a.y = (uint32_t)(uint16_t)lo[2] | ((uint32_t)(uint16_t)lo[3] << 16);
@@ -295,7 +501,9 @@ __global__ __launch_bounds__(kVarlenThreads, 2) void varlen_attention_kernel(Var
         o[0][dt] = M::mfma(a, pb[0][ks], o[0][dt]);
         o[1][dt] = M::mfma(a, pb[1][ks], o[1][dt]);
       }
+    // Every wave is done with stage t & 1 before tile t + 2 overwrites it.
     __syncthreads();
+    if (t + 2 < ntiles) issue_tile(kb + 2 * kKeyTile, t & 1);
   }
 
   // ---- normalise and write: lane holds O[row r16][16 dt + 4 g4 + i] ----
@@ -317,14 +525,22 @@ __global__ __launch_bounds__(kVarlenThreads, 2) void varlen_attention_kernel(Var
   }
 }
 
+template <bool kBF16, int D, int G, bool kCausal>
+static void launch_varlen_c(const VarlenParams& p, dim3 grid, hipStream_t st) {
+  if (p.has_pool)
+    hipLaunchKernelGGL((varlen_attention_kernel<kBF16, D, G, kCausal, true>), grid,
+                       dim3(kVarlenThreads), 0, st, p);
+  else
+    hipLaunchKernelGGL((varlen_attention_kernel<kBF16, D, G, kCausal, false>), grid,
+                       dim3(kVarlenThreads), 0, st, p);
+}
+
 template <bool kBF16, int D, int G>
 static void launch_varlen(const VarlenParams& p, bool causal, dim3 grid, hipStream_t st) {
   if (causal)
-    hipLaunchKernelGGL((varlen_attention_kernel<kBF16, D, G, true>), grid, dim3(kVarlenThreads), 0,
-                       st, p);
+    launch_varlen_c<kBF16, D, G, true>(p, grid, st);
   else
-    hipLaunchKernelGGL((varlen_attention_kernel<kBF16, D, G, false>), grid, dim3(kVarlenThreads),
-                       0, st, p);
+    launch_varlen_c<kBF16, D, G, false>(p, grid, st);
 }
 
 template <bool kBF16, int D>
@@ -393,6 +609,16 @@ extern "C" int va_varlen_attention(const va_varlen_args* a, void* stream) {
                             (uintptr_t)a->pool.k, (uintptr_t)a->pool.v};
   for (uintptr_t p : ptrs)
     VA_CHECK_ARG(p % 16 == 0, "va_varlen_attention: pointers must be 16-byte aligned");
+  VA_CHECK_ARG(a->scale > 0.f && a->scale < INFINITY, "va_varlen_attention: scale must be > 0");
+  if (a->k != nullptr) {
+    // Per-lane DMA offsets inside a 64-key tile are 32-bit.
+    const int64_t span = (int64_t)(kKeyTile - 1) * (a->k_stride_tok > a->v_stride_tok
+                                                        ? a->k_stride_tok
+                                                        : a->v_stride_tok) * 2 +
+                         (int64_t)a->head_dim * 2;
+    VA_CHECK_ARG(a->k_stride_tok >= 0 && a->v_stride_tok >= 0 && span < ((int64_t)1 << 32),
+                 "va_varlen_attention: k/v token strides must be non-negative and below 64 MiB");
+  }
   const int G = a->num_heads / a->num_kv_heads;
   if (!((a->head_dim == 64 || a->head_dim == 128) && (G == 1 || G == 2 || G == 4 || G == 8))) {
     set_error("va_varlen_attention: unsupported head_dim %d / group size %d (head_dim 64|128, "
@@ -436,8 +662,14 @@ extern "C" int va_varlen_attention(const va_varlen_args* a, void* stream) {
   p.slots = a->slot_mapping;
   p.slot_i64 = a->slot_dtype == VA_I64;
   p.num_qblocks = nqb;
+  p.num_seqs = a->num_seqs;
+  p.num_kv_heads = a->num_kv_heads;
 
-  const dim3 grid(nqb, a->num_kv_heads, a->num_seqs);
+  // 1-D grid: kXcds interleaved lists of (pair, query block); see the kernel.
+  const int64_t npairs = (int64_t)a->num_seqs * a->num_kv_heads;
+  const int64_t nwg = (npairs + kXcds - 1) / kXcds * kXcds * nqb;
+  VA_CHECK_ARG(npairs <= INT32_MAX / 2 && nwg <= INT32_MAX, "va_varlen_attention: grid too large");
+  const dim3 grid((unsigned)nwg);
   const hipStream_t st = (hipStream_t)stream;
   const bool ok = a->dtype == VA_BF16
                       ? dispatch_varlen<true>(a->head_dim, G, p, a->causal != 0, grid, st)
