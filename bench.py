@@ -130,6 +130,51 @@ def bench_decode(args, dev, stream):
                 batch=batch, qs=qs)
 
 
+def bench_longform(args, dev, stream):
+    """Config 5: long-form decode, (i) one 16384-token context, (ii) 8 contexts
+    U[4096, 16384]; 28 layers with their own pools, fused store, contexts split
+    into partitions and merged (the split the library picks by default)."""
+    res = {}
+    layers = workloads.LAYERS
+    for variant in ("single", "batch8"):
+        lens = workloads.cfg5_lens(variant, 0)
+        nb = sum(math.ceil(n / workloads.BLOCK) for n in lens) + 64
+        batch = workloads.make_decode_batch(lens, num_blocks=nb, num_layers=layers,
+                                            dtype=torch.bfloat16, kv_std=0.5, device=dev,
+                                            seed=5, device_rng=True)
+        g = torch.Generator(device=dev).manual_seed(9)
+        B = batch.num_seqs
+        qs = torch.randn(layers, B, workloads.HQ, workloads.HEAD_DIM, generator=g, device=dev
+                         ).to(torch.bfloat16)
+        nks = (torch.randn(layers, B, workloads.HKV, workloads.HEAD_DIM, generator=g,
+                           device=dev) * 0.5).to(torch.bfloat16)
+        nvs = (torch.randn(layers, B, workloads.HKV, workloads.HEAD_DIM, generator=g,
+                           device=dev) * 0.5).to(torch.bfloat16)
+        outs = torch.empty_like(qs)
+
+        def step():
+            for i in range(layers):
+                ops.paged_decode(qs[i], batch.k_pools[i], batch.v_pools[i], batch.block_tables,
+                                 batch.cu_seqlens_k, lens_cumulative=True,
+                                 max_seq_len=batch.max_seq_len, scale=batch.scale,
+                                 new_k=nks[i], new_v=nvs[i], new_slots=batch.slot_mapping,
+                                 out=outs[i], split_tokens=args.split)
+
+        ms, _ = timed_graph(step, args.steps, args.warmup, stream)
+        nbytes = workloads.decode_bytes(lens) + 2 * B * workloads.HKV * workloads.HEAD_DIM * 2 \
+            + 4 * B
+        us = ms * 1000.0 / layers
+        gbs = nbytes / (us * 1e-6) / 1e9
+        log(f"[longform {variant}] B={B} ctx sum {sum(lens)}: {us:.2f} us/layer, {gbs:.0f} GB/s "
+            f"({nbytes / 1e6:.1f} MB/layer, {gbs / HBM_PEAK_GBS:.3f} of HBM peak)")
+        res[variant] = {"us_per_layer": round(us, 2), "gbs": round(gbs, 1),
+                        "frac": round(gbs / HBM_PEAK_GBS, 4), "bytes_per_layer": nbytes,
+                        "batch": B, "context_tokens": sum(lens)}
+        del batch, qs, nks, nvs, outs
+        torch.cuda.empty_cache()
+    return res
+
+
 def bench_store(args, dev, stream, dec):
     """store_kvcache alone: 32 rows per layer over the 28 pools (latency-bound)."""
     batch = dec["batch"]
@@ -189,7 +234,8 @@ def bench_prefill(args, dev, stream):
     nbytes = workloads.varlen_bytes(lens, 16, 8, 128) + total * 2 * 8 * 128 * 2
     log(f"[prefill] {us:.2f} us/layer, {tflops:.1f} TFLOP/s ({flops / 1e9:.2f} GFLOP), "
         f"{nbytes / (us * 1e-6) / 1e9:.0f} GB/s")
-    return dict(us_layer=us, tflops=tflops, flops=flops, bytes=nbytes)
+    return dict(us_layer=us, tflops=tflops, flops=flops, bytes=nbytes,
+                inputs=(q[0], k[0], v[0], cu, scale, True))
 
 
 def bench_encoder(args, dev, stream):
@@ -217,7 +263,31 @@ def bench_encoder(args, dev, stream):
     log(f"[encoder] {len(wins)} windows, {total} tokens: {us:.2f} us/layer, "
         f"{flops / (us * 1e-6) / 1e12:.1f} TFLOP/s, {nbytes / (us * 1e-6) / 1e9:.0f} GB/s")
     return dict(us_layer=us, tflops=flops / (us * 1e-6) / 1e12,
-                gbs=nbytes / (us * 1e-6) / 1e9, windows=len(wins), tokens=total)
+                gbs=nbytes / (us * 1e-6) / 1e9, windows=len(wins), tokens=total, flops=flops,
+                inputs=(q[0], k[0], v[0], cu, 0.125, False))
+
+
+def cpu_varlen_baseline(inputs, budget_s: float, label: str):
+    """The oracle's per-sequence fp32 attention (bf16 inputs upcast) for one
+    layer of config 3 or 4 on the host's cores; median seconds per layer."""
+    from oracle import attention as oracle
+
+    torch.set_num_threads(os.cpu_count() or 1)
+    q, k, v, cu, scale, causal = inputs
+    q, k, v, cu = q.cpu(), k.cpu(), v.cpu(), cu.cpu()
+    oracle.varlen_attention(q, k, v, cu, cu, scale, causal)  # warm-up
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while len(times) < 3 or time.perf_counter() < t_end:
+        t0 = time.perf_counter()
+        oracle.varlen_attention(q, k, v, cu, cu, scale, causal)
+        times.append(time.perf_counter() - t0)
+        if len(times) >= 500:
+            break
+    times.sort()
+    med = times[len(times) // 2]
+    log(f"[cpu {label}] {med * 1e6:.0f} us/layer median of {len(times)} reps")
+    return med, len(times)
 
 
 def cpu_baseline(dec, budget_s: float):
@@ -266,7 +336,8 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--split", type=int, default=0, help="decode split_tokens (0 = auto)")
-    ap.add_argument("--only", choices=["decode", "prefill", "encoder", "store", "all"],
+    ap.add_argument("--only", choices=["decode", "prefill", "encoder", "store", "longform",
+                                       "all"],
                     default="all")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
@@ -295,6 +366,9 @@ def main():
     if args.only in ("encoder",):
         print(json.dumps({"encoder": bench_encoder(args, dev, stream)}))
         return
+    if args.only == "longform":
+        print(json.dumps({"longform": bench_longform(args, dev, stream)}))
+        return
     dec = bench_decode(args, dev, stream)
     if args.only == "store":
         print(json.dumps({"store": bench_store(args, dev, stream, dec)}))
@@ -310,6 +384,7 @@ def main():
                             "hbm_gbs": round(pre["bytes"] / (pre["us_layer"] * 1e-6) / 1e9, 1),
                             "config": "cfg3: 32 prompts U[50,450], GQA 16/8, D128, fused store, "
                                       "28 rotating input sets (cold)"}
+        extra["longform"] = bench_longform(args, dev, stream)
         extra["encoder"] = {"us_per_layer": round(enc["us_layer"], 2),
                             "tflops": round(enc["tflops"], 2),
                             "hbm_gbs": round(enc["gbs"], 1),
@@ -318,6 +393,14 @@ def main():
     cpu = None
     if not args.no_cpu and args.only == "all":
         cpu = cpu_baseline(dec, args.cpu_seconds)
+        threads = os.cpu_count() or 1
+        for key, res, label in (("prefill", pre, "cfg3"), ("encoder", enc, "cfg4")):
+            med, reps = cpu_varlen_baseline(res["inputs"], args.cpu_seconds / 2, label)
+            extra[key]["cpu_baseline"] = {
+                "us_per_layer": round(med * 1e6, 1), "tflops": round(res["flops"] / med / 1e12, 4),
+                "cores": threads, "kind": "port",
+                "sample": f"one layer of {label} through the oracle's per-sequence fp32 "
+                          f"masked softmax (bf16 inputs upcast), {reps} reps, median"}
     line = {
         "metric": METRIC,
         "value": round(dec["gbs"], 2),
