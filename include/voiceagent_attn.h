@@ -23,6 +23,11 @@
  *                            qwen_asr_vllm/layers/attention.py:92-107, and
  *                            flash_attn_varlen_func(causal=False),
  *                            qwen_asr_vllm/layers/attention.py:121-139
+ *   va_qk_norm_rope       <- q_norm / k_norm + rotary_emb of Qwen3Attention.forward,
+ *                            qwen_asr_vllm/models/qwen3.py:42-48 (RMSNorm._norm,
+ *                            layers/layernorm.py:19-25; apply_rotary_emb and
+ *                            RotaryEmbedding.forward, layers/rotary_embedding.py:9-32);
+ *                            also fused into va_paged_decode (va_decode_args.prologue)
  */
 #ifndef VOICEAGENT_ATTN_H
 #define VOICEAGENT_ATTN_H
@@ -34,7 +39,7 @@
 extern "C" {
 #endif
 
-#define VA_ATTN_ABI_VERSION 1
+#define VA_ATTN_ABI_VERSION 2
 
 /* status codes */
 #define VA_OK 0
@@ -97,6 +102,47 @@ typedef struct va_store_args {
  * Replaces store_kvcache, qwen_asr_vllm/layers/attention.py:52-67. */
 int va_store_kvcache(const va_store_args* args, void* stream);
 
+/* ------------------------------------------------------ q/k prologue */
+/* Qwen3's per-head query/key prologue: RMSNorm over head_dim,
+ *   n = to_dtype(x * 1/sqrt(mean(x^2) + eps)),  y = to_dtype(n * weight)
+ * (layers/layernorm.py:19-25), then rotary embedding in the half-split
+ * convention with the fp32 cache [max_position, head_dim] = [cos | sin],
+ *   out[i]       = to_dtype(y[i] cos[i] - y[i + D/2] sin[i]),
+ *   out[i + D/2] = to_dtype(y[i + D/2] cos[i] + y[i] sin[i]),    i < D/2
+ * at the token's position (layers/rotary_embedding.py:9-32).  Products and
+ * sums are rounded separately (no fused multiply-add), as torch evaluates
+ * them. */
+typedef struct va_qk_prologue {
+  const void* q_norm_weight;  /* [head_dim] in weight_dtype                 */
+  const void* k_norm_weight;  /* [head_dim] in weight_dtype                 */
+  int32_t weight_dtype;       /* VA_BF16 / VA_F16 / VA_F32                  */
+  float eps;
+  const float* cos_sin_cache; /* [max_position, head_dim]: cos | sin halves */
+  int64_t cos_sin_stride;     /* elements between consecutive positions     */
+  int32_t max_position;       /* positions are clamped to [0, max_position) */
+  int32_t positions_dtype;    /* VA_I32 / VA_I64                            */
+  const void* positions;      /* decode: [num_seqs]; va_qk_norm_rope: [num_tokens] */
+} va_qk_prologue;
+
+typedef struct va_qk_norm_rope_args {
+  uint32_t struct_size;   /* sizeof(va_qk_norm_rope_args)                 */
+  int32_t dtype;          /* q, k and the outputs share it                */
+  const void* q;          /* [num_tokens, Hq, D]                          */
+  int64_t q_stride_tok, q_stride_head;
+  const void* k;          /* [num_tokens, Hkv, D]                         */
+  int64_t k_stride_tok, k_stride_head;
+  void* q_out;            /* [num_tokens, Hq, D]; may equal q (in place)  */
+  int64_t q_out_stride_tok, q_out_stride_head;
+  void* k_out;            /* [num_tokens, Hkv, D]; may equal k            */
+  int64_t k_out_stride_tok, k_out_stride_head;
+  int32_t num_tokens, num_heads, num_kv_heads, head_dim;
+  va_qk_prologue prologue; /* positions: one per token                    */
+} va_qk_norm_rope_args;
+
+/* Apply the prologue to every query and key row (prefill and any batch the
+ * fused decode path does not take). */
+int va_qk_norm_rope(const va_qk_norm_rope_args* args, void* stream);
+
 /* --------------------------------------------------------------- decode */
 typedef struct va_decode_args {
   uint32_t struct_size;   /* sizeof(va_decode_args)                       */
@@ -120,8 +166,9 @@ typedef struct va_decode_args {
    * for that position in the same launch (the TTS fused write,
    * qwen_tts_paged_attention.py:181-221).  [num_seqs, Hkv, D]. */
   const void* new_k;
+  int64_t new_k_stride_seq, new_k_stride_head;
   const void* new_v;
-  int64_t new_stride_seq, new_stride_head;
+  int64_t new_v_stride_seq, new_v_stride_head;
   /* Optional destination slots for the current row ([num_seqs], slot < 0
    * skips the write and the substitution).  NULL: the slot of position len-1
    * through the block table. */
@@ -133,7 +180,13 @@ typedef struct va_decode_args {
   float scale;            /* softmax scale                                */
   void* workspace;        /* partial results; see va_paged_decode_workspace_bytes */
   size_t workspace_bytes; /* (no initialisation needed; launches sharing one   */
-} va_decode_args;         /*  workspace must be ordered on one stream)         */
+                          /*  workspace must be ordered on one stream)         */
+  /* Optional Qwen3 prologue (NULL: q and new_k are used as given).  When set,
+   * q (and new_k, if given) are the raw projections: q is normalised and
+   * rotated at positions[b] before attention, and new_k likewise before it
+   * is written and attended (its position is also positions[b]). */
+  const va_qk_prologue* prologue;
+} va_decode_args;
 
 /* Bytes of workspace va_paged_decode needs for these arguments (the
  * struct's workspace fields are ignored); 0 when no sequence can span more

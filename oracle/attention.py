@@ -17,6 +17,12 @@ in plain PyTorch on the CPU, evaluated in float32 (or float64 when asked):
   92-107), non-causal block-diagonal windows (:121-139); equal to upstream
   eager_attention_forward + the causal or _prepare_attention_mask masks
   (reference/modeling_qwen3_asr.py:90-113, 649-667).
+* :func:`rms_norm`, :func:`rope_cache`, :func:`apply_rope`, :func:`qk_norm_rope` —
+  Qwen3's q/k prologue: RMSNorm._norm (qwen_asr_vllm/layers/layernorm.py:19-25),
+  RotaryEmbedding's cache and apply_rotary_emb
+  (qwen_asr_vllm/layers/rotary_embedding.py:9-32), in the order
+  Qwen3Attention.forward applies them (qwen_asr_vllm/models/qwen3.py:42-48),
+  evaluated by eager torch ops with the reference's dtype conversions.
 
 Masking convention: masked scores are -inf; a query row with no attended key
 returns 0 (the Triton kernel's result, qwen_tts_paged_attention.py:223-279).
@@ -28,6 +34,10 @@ force written with scalar loops; the reference's known-answer tests (exact
 scaled_dot_product_attention with independently built masks; closed forms
 (single key, constant V, zero query, block-table permutation); and planted
 mistakes (GQA mapping, causal alignment, block indexing) that must fail.
+The prologue functions are pinned by closed forms (a constant row normalises
+to +-1/sqrt(1 + eps/c^2); position 0 is the identity), by an independent
+float64 complex-number rotation with the reference's frequency formula, and
+by planted mistakes (swapped halves, flipped sign, a missing weight).
 """
 
 from __future__ import annotations
@@ -186,3 +196,42 @@ def varlen_attention(q, k, v, cu_seqlens_q, cu_seqlens_k, scale, causal, *, k_ca
             keep = (j <= kl - ql + i).view(1, ql, kl)
         out[q0:q1] = _masked_softmax_av(scores, values, keep).permute(1, 0, 2)
     return out
+
+
+# ------------------------------------------------------------ q/k prologue
+def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
+    """RMSNorm._norm (layers/layernorm.py:19-25): fp32 mean of squares and
+    rsqrt, back to x's dtype, then an in-place product with the weight (the
+    result keeps x's dtype)."""
+    orig = x.dtype
+    xf = x.float()
+    variance = xf.pow(2).mean(dim=-1, keepdim=True)
+    xf = xf * torch.rsqrt(variance + eps)
+    y = xf.to(orig)
+    y.mul_(weight)
+    return y
+
+
+def rope_cache(head_dim: int, max_position: int, base: float) -> torch.Tensor:
+    """The rotary table [max_position, head_dim] = cos | sin in fp32
+    (RotaryEmbedding.__init__, layers/rotary_embedding.py:18-26, without the
+    singleton head axis)."""
+    inv_freq = 1.0 / (base ** (torch.arange(0, head_dim, 2, dtype=torch.float) / head_dim))
+    positions = torch.arange(max_position, dtype=torch.float)
+    freqs = torch.einsum("i,j->ij", positions, inv_freq)
+    return torch.cat((freqs.cos(), freqs.sin()), dim=-1)
+
+
+def apply_rope(x: torch.Tensor, cos_sin: torch.Tensor, positions: torch.Tensor) -> torch.Tensor:
+    """apply_rotary_emb at per-token positions (layers/rotary_embedding.py:9-15,
+    28-32): x [T, H, D], first half paired with the second, fp32 math, result
+    in x's dtype."""
+    cos, sin = cos_sin[positions.long()].unsqueeze(1).chunk(2, dim=-1)
+    first, second = torch.chunk(x.float(), 2, dim=-1)
+    return torch.cat((first * cos - second * sin, second * cos + first * sin), dim=-1).to(x.dtype)
+
+
+def qk_norm_rope(q, k, positions, q_norm_weight, k_norm_weight, eps, cos_sin):
+    """Qwen3Attention.forward's prologue (models/qwen3.py:44-48)."""
+    return (apply_rope(rms_norm(q, q_norm_weight, eps), cos_sin, positions),
+            apply_rope(rms_norm(k, k_norm_weight, eps), cos_sin, positions))

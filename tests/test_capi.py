@@ -27,14 +27,15 @@ def test_header_functions_are_exported():
     assert declared == set(N.SIGNATURES), declared ^ set(N.SIGNATURES)
     for name in declared:
         assert hasattr(lib, name), name
-    assert lib.va_abi_version() == 1
+    assert lib.va_abi_version() == 2
 
 
 @pytest.mark.parametrize(
     "fn, cls, count_field",
     [("va_store_kvcache", N.StoreArgs, "num_tokens"),
      ("va_paged_decode", N.DecodeArgs, "num_seqs"),
-     ("va_varlen_attention", N.VarlenArgs, "num_seqs")],
+     ("va_varlen_attention", N.VarlenArgs, "num_seqs"),
+     ("va_qk_norm_rope", N.QkNormRopeArgs, "num_tokens")],
 )
 def test_struct_size_contract(fn, cls, count_field):
     lib = N.lib()

@@ -179,6 +179,30 @@ def test_engine_fused_store_matches_store_then_attend(dev):
     assert changed == expected_blocks
 
 
+def test_engine_fused_store_with_contiguous_k_and_strided_v(dev):
+    # The engine's decode inputs: k comes out of k_norm (contiguous) while v
+    # stays a view of the fused qkv row (row stride (Hq + 2 Hkv) D,
+    # models/qwen3.py:44-48).
+    lens = workloads.cfg2_lens(2)
+    b = workloads.make_decode_batch(lens, num_blocks=2048, dtype=torch.bfloat16, kv_std=0.5,
+                                    device=dev, seed=12)
+    B = len(lens)
+    qkv = torch.zeros(B, (16 + 2 * 8) * 128, dtype=torch.bfloat16, device=dev)
+    v_view = qkv[:, (16 + 8) * 128:].view(B, 8, 128)
+    v_view.copy_(b.new_v)
+    k0, v0 = b.k_pools[0].cpu(), b.v_pools[0].cpu()
+    out = ops.paged_decode(b.q, b.k_pools[0], b.v_pools[0], b.block_tables, b.cu_seqlens_k,
+                           lens_cumulative=True, max_seq_len=b.max_seq_len, scale=b.scale,
+                           new_k=b.new_k.contiguous(), new_v=v_view, new_slots=b.slot_mapping)
+    ek, ev = oracle.store_kvcache(b.new_k.cpu(), b.new_v.cpu(), k0, v0, b.slot_mapping.cpu())
+    torch.cuda.synchronize()
+    assert v_view.stride(0) == 4096 and b.new_k.contiguous().stride(0) == 1024
+    assert torch.equal(b.k_pools[0].cpu(), ek) and torch.equal(b.v_pools[0].cpu(), ev)
+    ref = oracle.paged_decode(b.q.cpu(), ek, ev, b.block_tables.cpu(), b.context_lens.cpu(),
+                              b.scale)
+    assert _err(out, ref) <= 2e-2
+
+
 def _tts_case(dev, d=128, hq=16, hkv=8, page=2, dtype=torch.float32, seed=17):
     # The reference fixture's structure (tests/test_qwen_tts_paged_attention_kernel.py:16-35),
     # scaled to a head_dim the kernel supports: two requests on disjoint pages with

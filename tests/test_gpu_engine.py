@@ -15,6 +15,7 @@ from torch import nn
 from voiceagent_amd.engine import DecodeGraphMetadata, prepare_batch
 from voiceagent_amd.layers.attention import PagedAttention
 from voiceagent_amd.layers.context import attention_context
+from voiceagent_amd.layers.qwen3 import Qwen3AttentionCore
 
 pytestmark = pytest.mark.gpu
 
@@ -35,16 +36,28 @@ class Seq:
 
 class TinyDecoder(nn.Module):
     """Attention-only decoder: x += o_proj(attn(split(x @ Wqkv))) per layer, with
-    the engine's fused-qkv views (v strided by (Hq + 2 Hkv) D)."""
+    the engine's fused-qkv views (v strided by (Hq + 2 Hkv) D).  ``kind``
+    "paged" uses PagedAttention on the raw q/k; "qwen3" uses
+    Qwen3AttentionCore (q/k RMSNorm + RoPE at the token positions first)."""
 
-    def __init__(self, dev, seed):
+    def __init__(self, dev, seed, kind="paged"):
         super().__init__()
         g = torch.Generator().manual_seed(seed)
         self.wqkv = [(torch.randn(HID, (HQ + 2 * HKV) * D, generator=g) * HID ** -0.5)
                      .to(torch.bfloat16).to(dev) for _ in range(L)]
         self.wo = [(torch.randn(HQ * D, HID, generator=g) * (HQ * D) ** -0.5)
                    .to(torch.bfloat16).to(dev) for _ in range(L)]
-        self.attn = nn.ModuleList(PagedAttention(HQ, D, D ** -0.5, HKV) for _ in range(L))
+        self.kind = kind
+        if kind == "paged":
+            self.attn = nn.ModuleList(PagedAttention(HQ, D, D ** -0.5, HKV) for _ in range(L))
+        else:
+            self.attn = nn.ModuleList(
+                Qwen3AttentionCore(HQ, D, HKV, eps=1e-6, max_position=MAX_MODEL_LEN)
+                for _ in range(L))
+            for layer in self.attn:
+                layer.q_norm_weight.data = (torch.rand(D, generator=g) + 0.5).to(torch.bfloat16)
+                layer.k_norm_weight.data = (torch.rand(D, generator=g) + 0.5).to(torch.bfloat16)
+            self.attn.to(dev)
         kv = torch.zeros(2, L, NB, BS, HKV, D, dtype=torch.bfloat16, device=dev)
         self.kv = kv
         for i, layer in enumerate(self.attn):  # model_runner.py:116-131
@@ -52,13 +65,17 @@ class TinyDecoder(nn.Module):
             layer.v_cache = kv[1, i]
         self.record = None  # list collecting layer 0's (k, v) rows when set
 
-    def forward(self, x):
+    def forward(self, x, positions):
         for i in range(L):
             qkv = x @ self.wqkv[i]
             q, k, v = qkv.split([HQ * D, HKV * D, HKV * D], dim=-1)
             if i == 0 and self.record is not None:
                 self.record.append((k.reshape(-1, HKV, D).clone(), v.reshape(-1, HKV, D).clone()))
-            a = self.attn[i](q.view(-1, HQ, D), k.view(-1, HKV, D), v.view(-1, HKV, D))
+            q, k, v = q.view(-1, HQ, D), k.view(-1, HKV, D), v.view(-1, HKV, D)
+            if self.kind == "paged":
+                a = self.attn[i](q, k, v)
+            else:
+                a = self.attn[i](positions, q, k, v)
             x = x + a.flatten(1) @ self.wo[i]
         return x
 
@@ -73,21 +90,26 @@ def _sequences(prompts, seed):
     return seqs
 
 
-def test_eager_and_graph_decode_match(dev):
+@pytest.mark.parametrize("kind", ["paged", "qwen3"])
+def test_eager_and_graph_decode_match(dev, kind):
     prompts = [37, 5, 64, 17, 100, 1]
     steps = 3
     g = torch.Generator().manual_seed(3)
     emb = [torch.randn(MAX_MODEL_LEN, HID, generator=g).to(torch.bfloat16).to(dev)
            for _ in prompts]
     engines = {}
-    for mode in ("eager", "graph"):
-        model = TinyDecoder(dev, seed=1)
+    modes = ("eager", "graph") + (("unfused",) if kind == "qwen3" else ())
+    for mode in modes:
+        model = TinyDecoder(dev, seed=1, kind=kind)
         if mode == "eager":
             model.record = []
+        if mode == "unfused":  # prologue kernel + decode: two launches per layer
+            for layer in model.attn:
+                layer.fuse_prologue = False
         seqs = _sequences(prompts, seed=2)
-        _, ctx = prepare_batch(seqs, BS, dev)
+        positions, ctx = prepare_batch(seqs, BS, dev)
         with attention_context(ctx):
-            model(torch.cat([emb[i][: len(s)] for i, s in enumerate(seqs)]))
+            model(torch.cat([emb[i][: len(s)] for i, s in enumerate(seqs)]), positions)
         for s in seqs:
             s.num_computed_tokens = len(s)
         engines[mode] = (model, seqs)
@@ -99,27 +121,34 @@ def test_eager_and_graph_decode_match(dev):
     x_static = torch.zeros(8, HID, dtype=torch.bfloat16, device=dev)
     meta.warmup_state()
     ctx_g = meta.context(8)
+    pos_g = meta.positions[:8]
     with attention_context(ctx_g):
         for _ in range(2):
-            model_g(x_static)
+            model_g(x_static, pos_g)
         torch.cuda.synchronize()
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(graph):
-            out_static = model_g(x_static)
+            out_static = model_g(x_static, pos_g)
     torch.cuda.synchronize()
     # The warm-up and the capture wrote nothing (every slot was -1).
     model_e, seqs_e = engines["eager"]
     assert torch.equal(model_g.kv, model_e.kv)
 
     for step in range(steps):
-        for seqs in (seqs_e, seqs_g):
+        for _, seqs in engines.values():
             for s in seqs:
                 s.length += 1
                 s.num_computed_tokens = s.length - 1
         x = torch.stack([emb[i][len(s) - 1] for i, s in enumerate(seqs_e)])
-        _, ctx = prepare_batch(seqs_e, BS, dev)
+        positions, ctx = prepare_batch(seqs_e, BS, dev)
         with attention_context(ctx):
-            out_e = model_e(x)
+            out_e = model_e(x, positions)
+        if "unfused" in engines:
+            model_u, seqs_u = engines["unfused"]
+            positions_u, ctx_u = prepare_batch(seqs_u, BS, dev)
+            with attention_context(ctx_u):
+                out_u = model_u(x, positions_u)
+            assert torch.equal(out_e, out_u), step
         bucket = meta.stage(seqs_g)
         assert bucket == 8
         x_static.zero_()
@@ -132,6 +161,10 @@ def test_eager_and_graph_decode_match(dev):
         assert torch.equal(out_e, out_g), step
 
     assert torch.equal(model_g.kv, model_e.kv)
+    if "unfused" in engines:
+        assert torch.equal(engines["unfused"][0].kv, model_e.kv)
+    if kind == "qwen3":
+        return  # layer 0's cache holds normalised, rotated keys: covered by test_gpu_prologue
 
     # Every slot written in layer 0 holds exactly the k/v row the layer
     # produced for that (sequence, position), bit for bit.

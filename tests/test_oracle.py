@@ -353,3 +353,75 @@ def test_planted_mistakes_are_caught(monkeypatch):
     assert run() > 1e-3
     monkeypatch.setattr(torch.Tensor, "repeat_interleave", orig)
     assert run() < 1e-12
+
+
+# ------------------------------------------------------------ q/k prologue
+def _rope_complex(x, positions, base):
+    """Independent float64 restatement: pair (x_i, x_{i+D/2}) as the complex
+    number x_i + j x_{i+D/2}, multiplied by exp(j p base^(-2i/D))."""
+    d = x.shape[-1]
+    i = torch.arange(d // 2, dtype=torch.float64)
+    theta = positions.double()[:, None] * base ** (-2.0 * i / d)[None, :]
+    z = torch.complex(x[..., : d // 2].double(), x[..., d // 2:].double())
+    r = z * torch.polar(torch.ones_like(theta), theta)[:, None, :]
+    return torch.cat((r.real, r.imag), dim=-1)
+
+
+def test_rms_norm_closed_forms():
+    eps = 1e-6
+    for c in (0.5, -3.0, 40.0):
+        x = torch.full((2, 3, 128), c)
+        y = oracle.rms_norm(x, torch.ones(128), eps)
+        want = (1.0 if c > 0 else -1.0) / (1.0 + eps / c ** 2) ** 0.5
+        assert torch.allclose(y, torch.full_like(y, want), atol=1e-6)
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(5, 4, 64, generator=g, dtype=torch.float64)
+    w = torch.rand(64, generator=g, dtype=torch.float64) + 0.5
+    ref = x / torch.sqrt((x * x).mean(-1, keepdim=True) + eps) * w
+    assert torch.allclose(oracle.rms_norm(x.float(), w.float(), eps).double(), ref, atol=1e-5)
+    # bf16 input: the normalised value is rounded before the weight, as the reference does
+    xb = x.to(torch.bfloat16)
+    wb = w.to(torch.bfloat16)
+    y = oracle.rms_norm(xb, wb, eps)
+    n = (xb.float() * torch.rsqrt(xb.float().pow(2).mean(-1, keepdim=True) + eps)).to(torch.bfloat16)
+    assert y.dtype == torch.bfloat16 and torch.equal(y, n * wb)
+    # an fp32 weight on bf16 activations keeps the activation dtype (in-place product)
+    assert oracle.rms_norm(xb, w.float(), eps).dtype == torch.bfloat16
+
+
+def test_rope_matches_complex_rotation_and_identity_at_zero():
+    base, d = 1_000_000.0, 128
+    cs = oracle.rope_cache(d, 4096, base)
+    assert cs.shape == (4096, d) and cs.dtype == torch.float32
+    g = torch.Generator().manual_seed(1)
+    x = torch.randn(64, 3, d, generator=g)
+    pos = torch.randint(0, 4096, (64,), generator=g)
+    got = oracle.apply_rope(x, cs, pos).double()
+    want = _rope_complex(x, pos, base)
+    # fp32 angles of up to ~4096 rad: absolute error of a few 1e-4 at most
+    assert (got - want).abs().max() < 2e-3
+    zero = torch.zeros(64, dtype=torch.long)
+    assert torch.equal(oracle.apply_rope(x, cs, zero), x)
+    # rotation preserves the norm of every (i, i + D/2) pair
+    pn = lambda t: t[..., : d // 2] ** 2 + t[..., d // 2:] ** 2  # noqa: E731
+    assert torch.allclose(pn(got), pn(x.double()), rtol=1e-5, atol=1e-5)
+
+
+def test_prologue_planted_mistakes_fail():
+    base, d = 10000.0, 64
+    cs = oracle.rope_cache(d, 512, base)
+    g = torch.Generator().manual_seed(2)
+    x = torch.randn(32, 2, d, generator=g)
+    pos = torch.randint(1, 512, (32,), generator=g)
+    want = _rope_complex(x, pos, base)
+    cos, sin = cs[pos].unsqueeze(1).chunk(2, dim=-1)
+    a, b = x.chunk(2, dim=-1)
+    flipped = torch.cat((a * cos + b * sin, b * cos - a * sin), -1)   # wrong sign
+    swapped = torch.cat((b * cos - a * sin, a * cos + b * sin), -1)   # halves swapped
+    for bad in (flipped, swapped):
+        assert (bad.double() - want).abs().max() > 0.1
+    w = torch.rand(d, generator=g) + 0.5
+    assert (oracle.rms_norm(x, w, 1e-6) - oracle.rms_norm(x, torch.ones(d), 1e-6)).abs().max() > 0.1
+    qn, kn = oracle.qk_norm_rope(x, x[:, :1], pos, w, w, 1e-6, cs)
+    assert torch.allclose(qn.double(), _rope_complex(oracle.rms_norm(x, w, 1e-6), pos, base),
+                          atol=2e-3)

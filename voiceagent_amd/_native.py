@@ -20,6 +20,7 @@ VA_OK = 0
 VA_BF16, VA_F16, VA_F32 = 0, 1, 2
 VA_I32, VA_I64 = 0, 1
 VA_LENS_PER_SEQ, VA_LENS_CUMULATIVE = 0, 1
+ABI_VERSION = 2  # VA_ATTN_ABI_VERSION of the header these structs mirror
 
 DTYPE_CODES = {torch.bfloat16: VA_BF16, torch.float16: VA_F16, torch.float32: VA_F32}
 INDEX_CODES = {torch.int32: VA_I32, torch.int64: VA_I64}
@@ -64,6 +65,44 @@ class StoreArgs(ctypes.Structure):
     ]
 
 
+class QkPrologue(ctypes.Structure):
+    _fields_ = [
+        ("q_norm_weight", c_void_p),
+        ("k_norm_weight", c_void_p),
+        ("weight_dtype", c_int32),
+        ("eps", c_float),
+        ("cos_sin_cache", c_void_p),
+        ("cos_sin_stride", c_int64),
+        ("max_position", c_int32),
+        ("positions_dtype", c_int32),
+        ("positions", c_void_p),
+    ]
+
+
+class QkNormRopeArgs(ctypes.Structure):
+    _fields_ = [
+        ("struct_size", c_uint32),
+        ("dtype", c_int32),
+        ("q", c_void_p),
+        ("q_stride_tok", c_int64),
+        ("q_stride_head", c_int64),
+        ("k", c_void_p),
+        ("k_stride_tok", c_int64),
+        ("k_stride_head", c_int64),
+        ("q_out", c_void_p),
+        ("q_out_stride_tok", c_int64),
+        ("q_out_stride_head", c_int64),
+        ("k_out", c_void_p),
+        ("k_out_stride_tok", c_int64),
+        ("k_out_stride_head", c_int64),
+        ("num_tokens", c_int32),
+        ("num_heads", c_int32),
+        ("num_kv_heads", c_int32),
+        ("head_dim", c_int32),
+        ("prologue", QkPrologue),
+    ]
+
+
 class DecodeArgs(ctypes.Structure):
     _fields_ = [
         ("struct_size", c_uint32),
@@ -86,9 +125,11 @@ class DecodeArgs(ctypes.Structure):
         ("valid_stride_seq", c_int64),
         ("valid_len", c_int32),
         ("new_k", c_void_p),
+        ("new_k_stride_seq", c_int64),
+        ("new_k_stride_head", c_int64),
         ("new_v", c_void_p),
-        ("new_stride_seq", c_int64),
-        ("new_stride_head", c_int64),
+        ("new_v_stride_seq", c_int64),
+        ("new_v_stride_head", c_int64),
         ("new_slots", c_void_p),
         ("new_slots_dtype", c_int32),
         ("num_seqs", c_int32),
@@ -100,6 +141,7 @@ class DecodeArgs(ctypes.Structure):
         ("scale", c_float),
         ("workspace", c_void_p),
         ("workspace_bytes", c_size_t),
+        ("prologue", ctypes.POINTER(QkPrologue)),
     ]
 
 
@@ -146,6 +188,7 @@ SIGNATURES = {
     "va_paged_decode_workspace_bytes": (c_size_t, [ctypes.POINTER(DecodeArgs)]),
     "va_paged_decode": (c_int32, [ctypes.POINTER(DecodeArgs), c_void_p]),
     "va_varlen_attention": (c_int32, [ctypes.POINTER(VarlenArgs), c_void_p]),
+    "va_qk_norm_rope": (c_int32, [ctypes.POINTER(QkNormRopeArgs), c_void_p]),
     "va_last_error": (ctypes.c_char_p, []),
     "va_abi_version": (c_int32, []),
 }
@@ -171,8 +214,9 @@ def lib() -> ctypes.CDLL:
             fn = getattr(handle, name)
             fn.restype = restype
             fn.argtypes = argtypes
-        if handle.va_abi_version() != 1:
-            raise RuntimeError("libvoiceagent_attn ABI version mismatch")
+        if handle.va_abi_version() != ABI_VERSION:
+            raise RuntimeError(f"libvoiceagent_attn ABI version {handle.va_abi_version()} != "
+                               f"{ABI_VERSION} (rebuild the library)")
         _LIB = handle
     return _LIB
 

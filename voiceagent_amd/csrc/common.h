@@ -36,6 +36,7 @@ typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
 struct BF16 {
   static constexpr int kBytes = 2;
   static constexpr int kPerVec = 8;
+  static constexpr bool kIsBF16 = true;
   __device__ static inline float dot(const uint4 q, const uint4 k, float acc) {
     acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, q.x),
                                           __builtin_bit_cast(bf16x2_t, k.x), acc, false);
@@ -73,6 +74,7 @@ struct BF16 {
 struct F16 {
   static constexpr int kBytes = 2;
   static constexpr int kPerVec = 8;
+  static constexpr bool kIsBF16 = false;
   typedef _Float16 h2 __attribute__((ext_vector_type(2)));
   __device__ static inline float dot(const uint4 q, const uint4 k, float acc) {
     acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, q.x), __builtin_bit_cast(f16x2_t, k.x),
@@ -110,6 +112,7 @@ struct F16 {
 struct F32 {
   static constexpr int kBytes = 4;
   static constexpr int kPerVec = 4;
+  static constexpr bool kIsBF16 = false;
   __device__ static inline float dot(const uint4 q, const uint4 k, float acc) {
     acc = fmaf(__uint_as_float(q.x), __uint_as_float(k.x), acc);
     acc = fmaf(__uint_as_float(q.y), __uint_as_float(k.y), acc);

@@ -35,7 +35,7 @@
 // than the imbalance between long and short contexts.
 #include <atomic>
 
-#include "common.h"
+#include "prologue.h"
 
 namespace va {
 
@@ -61,7 +61,7 @@ struct DecodeParams {
   int32_t valid_len;
   const char* new_k;
   const char* new_v;
-  int64_t n_sb, n_sh;  // bytes
+  int64_t nk_sb, nk_sh, nv_sb, nv_sh;  // bytes
   const void* new_slots;
   int32_t new_slots_i64;
   int32_t num_kv_heads;
@@ -70,6 +70,8 @@ struct DecodeParams {
   float scale_log2;
   float* part_ml;
   float* part_o;
+  int32_t has_pro;  // apply the Qwen3 q/k prologue to q and the current row
+  PrologueParams pro;
 };
 
 constexpr int kChunk = 16;
@@ -170,17 +172,6 @@ __global__ __launch_bounds__((DecodeShape<ET, D, G>::NW * 64),
   if (nparts > p.max_parts) nparts = p.max_parts;  // the last partition absorbs the rest
   const int end = last_grid_part ? L : min(start + P, L);
 
-  constexpr bool kScaleAfter = ET::kBytes == 2;
-  if constexpr (!kScaleAfter) {
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      qv[g].x = __float_as_uint(__uint_as_float(qv[g].x) * p.scale_log2);
-      qv[g].y = __float_as_uint(__uint_as_float(qv[g].y) * p.scale_log2);
-      qv[g].z = __float_as_uint(__uint_as_float(qv[g].z) * p.scale_log2);
-      qv[g].w = __float_as_uint(__uint_as_float(qv[g].w) * p.scale_log2);
-    }
-  }
-
   // Current-row substitution / write (TTS fused write, engine fused store).
   int64_t new_dst = -1;  // byte offset of the destination slot (block/slot part)
   int new_tok = -1;
@@ -199,6 +190,50 @@ __global__ __launch_bounds__((DecodeShape<ET, D, G>::NW * 64),
       new_tok = L - 1;
     }
   }
+  // This lane's slice of the current row (attended at new_tok and written to
+  // new_dst); loaded up front, so no K/V load waits on it.
+  uint4 kcur = make_uint4(0, 0, 0, 0), vcur = make_uint4(0, 0, 0, 0);
+  if (new_tok >= 0) {
+    kcur = ld16(p.new_k + b * p.nk_sb + h * p.nk_sh + col * 16);
+    vcur = ld16(p.new_v + b * p.nv_sb + h * p.nv_sh + col * 16);
+  }
+
+  // Qwen3 prologue: q and the current key are raw projections; normalise and
+  // rotate them at the sequence's position (one head row per LPR lanes).
+  if (p.has_pro) {
+    int64_t pos = load_index(p.pro.pos, b, p.pro.pos_i64);
+    pos = pos < 0 ? 0 : (pos >= p.pro.max_pos ? p.pro.max_pos - 1 : pos);
+    float c[E], sn[E], w[E];
+    load_rotary<E, LPR>(p.pro, pos, col, D, c, sn);
+    load_weights<E>(p.pro.q_w, p.pro.w_dtype, col * E, w);
+    const bool first_half = col < LPR / 2;
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      float x[E];
+      ET::unpack(qv[g], x);
+      qk_prologue<ET, LPR, E>(x, w, p.pro.eps, D, c, sn, first_half);
+      qv[g] = ET::pack(x);
+    }
+    if (new_tok >= 0) {
+      load_weights<E>(p.pro.k_w, p.pro.w_dtype, col * E, w);
+      float x[E];
+      ET::unpack(kcur, x);
+      qk_prologue<ET, LPR, E>(x, w, p.pro.eps, D, c, sn, first_half);
+      kcur = ET::pack(x);
+    }
+  }
+
+  constexpr bool kScaleAfter = ET::kBytes == 2;
+  if constexpr (!kScaleAfter) {
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      qv[g].x = __float_as_uint(__uint_as_float(qv[g].x) * p.scale_log2);
+      qv[g].y = __float_as_uint(__uint_as_float(qv[g].y) * p.scale_log2);
+      qv[g].z = __float_as_uint(__uint_as_float(qv[g].z) * p.scale_log2);
+      qv[g].w = __float_as_uint(__uint_as_float(qv[g].w) * p.scale_log2);
+    }
+  }
+
 
   float m[G], l[G], o[G][E];
 #pragma unroll
@@ -243,17 +278,16 @@ __global__ __launch_bounds__((DecodeShape<ET, D, G>::NW * 64),
           kr[r] = ld16(p.kp + off);
           vr[r] = ld16(p.vp + off);
         }
-      } else {
-        const bool cur = tok == new_tok;
-        // The current row is loaded (from new_k/new_v) even when it is masked.
-        if (ok || cur) {
-          const int64_t off =
-              (int64_t)blk * p.s_blk + (int64_t)(tok % p.block_size) * p.s_slot + head_off;
-          const char* kaddr = cur ? p.new_k + b * p.n_sb + h * p.n_sh + col * 16 : p.kp + off;
-          const char* vaddr = cur ? p.new_v + b * p.n_sb + h * p.n_sh + col * 16 : p.vp + off;
-          kr[r] = ld16(kaddr);
-          vr[r] = ld16(vaddr);
-        }
+      } else if (tok == new_tok) {
+        // The current row comes from registers (also when it is masked, so
+        // the store below always has it).
+        kr[r] = kcur;
+        vr[r] = vcur;
+      } else if (ok) {
+        const int64_t off =
+            (int64_t)blk * p.s_blk + (int64_t)(tok % p.block_size) * p.s_slot + head_off;
+        kr[r] = ld16(p.kp + off);
+        vr[r] = ld16(p.vp + off);
       }
     }
   };
@@ -669,7 +703,8 @@ extern "C" int va_paged_decode(const va_decode_args* a, void* stream) {
   VA_CHECK_ARG(a->table_width >= 0, "va_paged_decode: table_width < 0");
   const int64_t strides[] = {a->q_stride_seq,        a->q_stride_head,        a->out_stride_seq,
                              a->out_stride_head,     a->pool.stride_block,    a->pool.stride_slot,
-                             a->pool.stride_head,    a->new_stride_seq,       a->new_stride_head};
+                             a->pool.stride_head,    a->new_k_stride_seq,     a->new_k_stride_head,
+                             a->new_v_stride_seq,    a->new_v_stride_head};
   for (int64_t s : strides)
     VA_CHECK_ARG((s * eb) % 16 == 0, "va_paged_decode: strides must be 16-byte multiples");
   const uintptr_t ptrs[] = {(uintptr_t)a->q, (uintptr_t)a->out, (uintptr_t)a->pool.k,
@@ -725,14 +760,40 @@ extern "C" int va_paged_decode(const va_decode_args* a, void* stream) {
   p.valid_len = a->valid_mask ? a->valid_len : 0;
   p.new_k = (const char*)a->new_k;
   p.new_v = (const char*)a->new_v;
-  p.n_sb = a->new_stride_seq * eb;
-  p.n_sh = a->new_stride_head * eb;
+  p.nk_sb = a->new_k_stride_seq * eb;
+  p.nk_sh = a->new_k_stride_head * eb;
+  p.nv_sb = a->new_v_stride_seq * eb;
+  p.nv_sh = a->new_v_stride_head * eb;
   p.new_slots = a->new_slots;
   p.new_slots_i64 = a->new_slots_dtype == VA_I64;
   p.num_kv_heads = a->num_kv_heads;
   p.split_tokens = pl.split_tokens;
   p.max_parts = pl.max_parts;
   p.scale_log2 = a->scale * 1.4426950408889634f;
+  p.has_pro = a->prologue != nullptr;
+  p.pro = PrologueParams{};
+  if (a->prologue != nullptr) {
+    const va_qk_prologue& pr = *a->prologue;
+    VA_CHECK_ARG(pr.cos_sin_cache && pr.positions && pr.max_position > 0 &&
+                     pr.cos_sin_stride >= a->head_dim,
+                 "va_paged_decode: prologue rotary cache / positions");
+    VA_CHECK_ARG(pr.q_norm_weight && (a->new_k == nullptr || pr.k_norm_weight),
+                 "va_paged_decode: prologue norm weights missing");
+    VA_CHECK_ARG(pr.weight_dtype == VA_BF16 || pr.weight_dtype == VA_F16 ||
+                     pr.weight_dtype == VA_F32,
+                 "va_paged_decode: prologue weight_dtype");
+    VA_CHECK_ARG(pr.positions_dtype == VA_I32 || pr.positions_dtype == VA_I64,
+                 "va_paged_decode: prologue positions_dtype");
+    p.pro.q_w = pr.q_norm_weight;
+    p.pro.k_w = pr.k_norm_weight;
+    p.pro.w_dtype = pr.weight_dtype;
+    p.pro.eps = pr.eps;
+    p.pro.cs = pr.cos_sin_cache;
+    p.pro.cs_stride = pr.cos_sin_stride;
+    p.pro.max_pos = pr.max_position;
+    p.pro.pos_i64 = pr.positions_dtype == VA_I64;
+    p.pro.pos = pr.positions;
+  }
   char* ws = (char*)a->workspace;
   p.part_ml = pl.total_bytes ? (float*)ws : nullptr;
   p.part_o = pl.total_bytes ? (float*)(ws + pl.ml_bytes) : nullptr;

@@ -1,0 +1,148 @@
+// Standalone Qwen3 q/k prologue: RMSNorm + half-split rotary embedding of
+// every query and key head row of a batch of tokens (the prefill side of
+// Qwen3Attention.forward, qwen_asr_vllm/models/qwen3.py:42-48; the decode side
+// is fused into the paged decode kernel).  One group of LPR lanes per head
+// row; the per-row math lives in prologue.h.
+#include "prologue.h"
+
+namespace va {
+
+struct QkParams {
+  const char* q;
+  int64_t q_st, q_sh;  // bytes
+  const char* k;
+  int64_t k_st, k_sh;
+  char* qo;
+  int64_t qo_st, qo_sh;
+  char* ko;
+  int64_t ko_st, ko_sh;
+  int32_t num_tokens, hq, hkv;
+  PrologueParams pp;
+};
+
+constexpr int kQkThreads = 256;
+
+template <typename ET, int D>
+__global__ __launch_bounds__(kQkThreads) void qk_norm_rope_kernel(QkParams p) {
+  constexpr int E = ET::kPerVec;
+  constexpr int LPR = D / E;     // lanes per head row
+  constexpr int RPW = 64 / LPR;  // rows per wave
+  static_assert(LPR >= 2 && LPR <= 64 && 64 % LPR == 0, "unsupported head_dim");
+  const int lane = threadIdx.x & 63;
+  const int col = lane % LPR;
+  const int64_t wave = (int64_t)blockIdx.x * (kQkThreads / 64) + threadIdx.x / 64;
+  const int64_t row = wave * RPW + lane / LPR;
+  const int heads = p.hq + p.hkv;
+  // Rows are whole lane groups, so a group is either in range or not.
+  if (row >= (int64_t)p.num_tokens * heads) return;
+  const int64_t tok = row / heads;
+  const int hh = (int)(row % heads);
+  const bool isq = hh < p.hq;
+  const char* src = isq ? p.q + tok * p.q_st + hh * p.q_sh
+                        : p.k + tok * p.k_st + (int64_t)(hh - p.hq) * p.k_sh;
+  char* dst = isq ? p.qo + tok * p.qo_st + hh * p.qo_sh
+                  : p.ko + tok * p.ko_st + (int64_t)(hh - p.hq) * p.ko_sh;
+  const uint4 raw = ld16(src + col * 16);
+  int64_t pos = load_index(p.pp.pos, tok, p.pp.pos_i64);
+  pos = pos < 0 ? 0 : (pos >= p.pp.max_pos ? p.pp.max_pos - 1 : pos);
+  float x[E], w[E], c[E], s[E];
+  ET::unpack(raw, x);
+  load_weights<E>(isq ? p.pp.q_w : p.pp.k_w, p.pp.w_dtype, col * E, w);
+  load_rotary<E, LPR>(p.pp, pos, col, D, c, s);
+  qk_prologue<ET, LPR, E>(x, w, p.pp.eps, D, c, s, col < LPR / 2);
+  st16(dst + col * 16, ET::pack(x));
+}
+
+template <typename ET>
+static bool launch_qk(int D, const QkParams& p, dim3 grid, hipStream_t st) {
+  switch (D) {
+    case 64: hipLaunchKernelGGL((qk_norm_rope_kernel<ET, 64>), grid, dim3(kQkThreads), 0, st, p); return true;
+    case 128: hipLaunchKernelGGL((qk_norm_rope_kernel<ET, 128>), grid, dim3(kQkThreads), 0, st, p); return true;
+    case 256: hipLaunchKernelGGL((qk_norm_rope_kernel<ET, 256>), grid, dim3(kQkThreads), 0, st, p); return true;
+    default: return false;
+  }
+}
+
+}  // namespace va
+
+extern "C" int va_qk_norm_rope(const va_qk_norm_rope_args* a, void* stream) {
+  using namespace va;
+  VA_CHECK_ARG(a != nullptr, "va_qk_norm_rope: null args");
+  VA_CHECK_ARG(a->struct_size == sizeof(va_qk_norm_rope_args),
+               "va_qk_norm_rope: struct_size %u != %zu (header/library mismatch)", a->struct_size,
+               sizeof(va_qk_norm_rope_args));
+  VA_CHECK_ARG(a->num_tokens >= 0, "va_qk_norm_rope: num_tokens < 0");
+  if (a->num_tokens == 0) return VA_OK;
+  const int eb = a->dtype == VA_F32 ? 4 : (a->dtype == VA_BF16 || a->dtype == VA_F16) ? 2 : 0;
+  VA_CHECK_ARG(eb != 0, "va_qk_norm_rope: unknown dtype %d", a->dtype);
+  VA_CHECK_ARG(a->head_dim == 64 || a->head_dim == 128 || a->head_dim == 256,
+               "va_qk_norm_rope: head_dim %d (64, 128 or 256)", a->head_dim);
+  VA_CHECK_ARG(a->num_heads >= 0 && a->num_kv_heads >= 0 && a->num_heads + a->num_kv_heads > 0,
+               "va_qk_norm_rope: head counts");
+  VA_CHECK_ARG(a->num_heads == 0 || (a->q && a->q_out), "va_qk_norm_rope: q / q_out missing");
+  VA_CHECK_ARG(a->num_kv_heads == 0 || (a->k && a->k_out), "va_qk_norm_rope: k / k_out missing");
+  const va_qk_prologue& pr = a->prologue;
+  VA_CHECK_ARG(pr.cos_sin_cache && pr.positions && pr.max_position > 0 && pr.cos_sin_stride >= a->head_dim,
+               "va_qk_norm_rope: rotary cache / positions");
+  VA_CHECK_ARG((a->num_heads == 0 || pr.q_norm_weight) && (a->num_kv_heads == 0 || pr.k_norm_weight),
+               "va_qk_norm_rope: norm weights missing");
+  VA_CHECK_ARG(pr.weight_dtype == VA_BF16 || pr.weight_dtype == VA_F16 || pr.weight_dtype == VA_F32,
+               "va_qk_norm_rope: weight_dtype");
+  VA_CHECK_ARG(pr.positions_dtype == VA_I32 || pr.positions_dtype == VA_I64,
+               "va_qk_norm_rope: positions_dtype");
+  const int64_t strides[] = {a->q_stride_tok,     a->q_stride_head,     a->k_stride_tok,
+                             a->k_stride_head,    a->q_out_stride_tok,  a->q_out_stride_head,
+                             a->k_out_stride_tok, a->k_out_stride_head};
+  for (int64_t s : strides)
+    VA_CHECK_ARG((s * eb) % 16 == 0, "va_qk_norm_rope: strides must be 16-byte multiples");
+  const uintptr_t ptrs[] = {(uintptr_t)a->q, (uintptr_t)a->k, (uintptr_t)a->q_out,
+                            (uintptr_t)a->k_out};
+  for (uintptr_t p : ptrs)
+    VA_CHECK_ARG(p % 16 == 0, "va_qk_norm_rope: pointers must be 16-byte aligned");
+
+  QkParams p;
+  p.q = (const char*)a->q;
+  p.q_st = a->q_stride_tok * eb;
+  p.q_sh = a->q_stride_head * eb;
+  p.k = (const char*)a->k;
+  p.k_st = a->k_stride_tok * eb;
+  p.k_sh = a->k_stride_head * eb;
+  p.qo = (char*)a->q_out;
+  p.qo_st = a->q_out_stride_tok * eb;
+  p.qo_sh = a->q_out_stride_head * eb;
+  p.ko = (char*)a->k_out;
+  p.ko_st = a->k_out_stride_tok * eb;
+  p.ko_sh = a->k_out_stride_head * eb;
+  p.num_tokens = a->num_tokens;
+  p.hq = a->num_heads;
+  p.hkv = a->num_kv_heads;
+  p.pp.q_w = pr.q_norm_weight;
+  p.pp.k_w = pr.k_norm_weight;
+  p.pp.w_dtype = pr.weight_dtype;
+  p.pp.eps = pr.eps;
+  p.pp.cs = pr.cos_sin_cache;
+  p.pp.cs_stride = pr.cos_sin_stride;
+  p.pp.max_pos = pr.max_position;
+  p.pp.pos_i64 = pr.positions_dtype == VA_I64;
+  p.pp.pos = pr.positions;
+
+  const int E = 16 / eb;
+  const int rpw = 64 / (a->head_dim / E);
+  const int64_t rows = (int64_t)a->num_tokens * (a->num_heads + a->num_kv_heads);
+  const int64_t waves = (rows + rpw - 1) / rpw;
+  const int64_t blocks = (waves + kQkThreads / 64 - 1) / (kQkThreads / 64);
+  VA_CHECK_ARG(blocks <= INT32_MAX, "va_qk_norm_rope: too many rows");
+  const dim3 grid((unsigned)blocks);
+  const hipStream_t st = (hipStream_t)stream;
+  bool ok = false;
+  switch (a->dtype) {
+    case VA_BF16: ok = launch_qk<BF16>(a->head_dim, p, grid, st); break;
+    case VA_F16: ok = launch_qk<F16>(a->head_dim, p, grid, st); break;
+    case VA_F32: ok = launch_qk<F32>(a->head_dim, p, grid, st); break;
+  }
+  if (!ok) {
+    set_error("va_qk_norm_rope: unsupported configuration");
+    return VA_ERR_UNSUPPORTED;
+  }
+  return check_launch("va_qk_norm_rope");
+}

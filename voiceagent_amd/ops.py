@@ -10,6 +10,7 @@ from __future__ import annotations
 
 import ctypes
 import math
+from dataclasses import dataclass
 
 import torch
 
@@ -128,6 +129,93 @@ def store_kvcache(
     N.call("va_store_kvcache", args, device)
 
 
+# ---------------------------------------------------------- q/k prologue
+@dataclass(frozen=True)
+class QKPrologue:
+    """Qwen3's per-head q/k prologue (qwen_asr_vllm/models/qwen3.py:42-48):
+    RMSNorm with ``q_norm_weight`` / ``k_norm_weight`` and ``eps``
+    (layers/layernorm.py:19-25), then the half-split rotary embedding read from
+    the fp32 ``cos_sin_cache`` ([max_position, D] or the reference's
+    [max_position, 1, D] buffer) at ``positions`` (layers/rotary_embedding.py:9-32)."""
+
+    q_norm_weight: torch.Tensor
+    k_norm_weight: torch.Tensor
+    eps: float
+    cos_sin_cache: torch.Tensor
+    positions: torch.Tensor
+
+
+def _prologue_struct(pro: QKPrologue, head_dim: int, n_positions: int) -> N.QkPrologue:
+    for name, w in (("q_norm_weight", pro.q_norm_weight), ("k_norm_weight", pro.k_norm_weight)):
+        _require(w.dim() == 1 and w.numel() == head_dim and w.is_contiguous(),
+                 f"{name} must be a contiguous [head_dim] vector")
+    _require(pro.q_norm_weight.dtype == pro.k_norm_weight.dtype,
+             "q_norm_weight and k_norm_weight must share a dtype")
+    cs = pro.cos_sin_cache
+    if cs.dim() == 3:
+        _require(cs.shape[1] == 1, "cos_sin_cache must be [max_position, (1,) head_dim]")
+        cs = cs[:, 0]
+    _require(cs.dim() == 2 and cs.shape[1] == head_dim and cs.dtype == torch.float32
+             and cs.stride(-1) == 1,
+             "cos_sin_cache must be an fp32 [max_position, head_dim] table (cos | sin)")
+    pos = pro.positions
+    _require(pos.dim() == 1 and pos.numel() >= n_positions and pos.is_contiguous(),
+             f"positions must be a contiguous vector of at least {n_positions} entries")
+    st = N.QkPrologue()
+    st.q_norm_weight = pro.q_norm_weight.data_ptr()
+    st.k_norm_weight = pro.k_norm_weight.data_ptr()
+    st.weight_dtype = _dtype_code(pro.q_norm_weight)
+    st.eps = float(pro.eps)
+    st.cos_sin_cache = cs.data_ptr()
+    st.cos_sin_stride = cs.stride(0)
+    st.max_position = int(cs.shape[0])
+    st.positions_dtype = _index_code(pos, "positions")
+    st.positions = pos.data_ptr()
+    return st
+
+
+def qk_norm_rope(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    prologue: QKPrologue,
+    *,
+    q_out: torch.Tensor | None = None,
+    k_out: torch.Tensor | None = None,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """Apply the Qwen3 q/k prologue to q [T, Hq, D] and k [T, Hkv, D] (one
+    position per token).  Outputs are allocated contiguous when not given and
+    may be q / k themselves (in place)."""
+    device = _check_gpu(q, k, q_out, k_out, prologue.q_norm_weight, prologue.k_norm_weight,
+                        prologue.cos_sin_cache, prologue.positions)
+    _require(q.dim() == 3 and k.dim() == 3 and q.shape[0] == k.shape[0] and
+             q.shape[2] == k.shape[2], "q must be [T, Hq, D] and k [T, Hkv, D]")
+    _require(q.dtype == k.dtype, "q and k must share a dtype")
+    _rows(q, "q")
+    _rows(k, "k")
+    T, hq, d = (int(x) for x in q.shape)
+    hkv = int(k.shape[1])
+    if q_out is None:
+        q_out = torch.empty(q.shape, dtype=q.dtype, device=device)
+    if k_out is None:
+        k_out = torch.empty(k.shape, dtype=k.dtype, device=device)
+    _require(q_out.shape == q.shape and q_out.dtype == q.dtype, "q_out must match q")
+    _require(k_out.shape == k.shape and k_out.dtype == k.dtype, "k_out must match k")
+    _rows(q_out, "q_out")
+    _rows(k_out, "k_out")
+    args = N.new_args(N.QkNormRopeArgs)
+    args.dtype = _dtype_code(q)
+    args.q, args.q_stride_tok, args.q_stride_head = q.data_ptr(), q.stride(0), q.stride(1)
+    args.k, args.k_stride_tok, args.k_stride_head = k.data_ptr(), k.stride(0), k.stride(1)
+    args.q_out = q_out.data_ptr()
+    args.q_out_stride_tok, args.q_out_stride_head = q_out.stride(0), q_out.stride(1)
+    args.k_out = k_out.data_ptr()
+    args.k_out_stride_tok, args.k_out_stride_head = k_out.stride(0), k_out.stride(1)
+    args.num_tokens, args.num_heads, args.num_kv_heads, args.head_dim = T, hq, hkv, d
+    args.prologue = _prologue_struct(prologue, d, T)
+    N.call("va_qk_norm_rope", args, device)
+    return q_out, k_out
+
+
 # -------------------------------------------------------------------- decode
 _WORKSPACES: dict[int, torch.Tensor] = {}
 
@@ -173,16 +261,22 @@ def paged_decode(
     new_slots: torch.Tensor | None = None,
     out: torch.Tensor | None = None,
     split_tokens: int = 0,
+    prologue: QKPrologue | None = None,
 ) -> torch.Tensor:
     """One-token paged GQA attention.
 
     q: [B, Hq, D]; out: [B, Hq, D] (allocated if None); lens: per-sequence
     context lengths [B], or cu_seqlens_k [B + 1] with ``lens_cumulative``.
     ``new_k``/``new_v`` ([B, Hkv, D]) are written at position len-1 (or at
-    ``new_slots[b]``) and used for that position in the same launch.
+    ``new_slots[b]``) and used for that position in the same launch.  With a
+    ``prologue``, q and new_k are raw projections, normalised and rotated at
+    ``prologue.positions[b]`` inside the launch.
     """
     device = _check_gpu(q, k_cache, v_cache, block_tables, lens, valid_mask, new_k, new_v,
                         new_slots, out)
+    if prologue is not None:
+        _check_gpu(q, prologue.q_norm_weight, prologue.k_norm_weight, prologue.cos_sin_cache,
+                   prologue.positions)
     _require(q.dim() == 3, "q must be [num_seqs, num_heads, head_dim]")
     _rows(q, "q")
     B, hq, d = (int(x) for x in q.shape)
@@ -225,12 +319,13 @@ def paged_decode(
     if new_k is not None:
         _require(new_k.shape == (B, hkv, d) and new_v.shape == new_k.shape,
                  "new_k/new_v must be [num_seqs, num_kv_heads, head_dim]")
-        _require(new_v.stride() == new_k.stride(), "new_k and new_v must share strides")
         _require(new_k.dtype == new_v.dtype == q.dtype, "new_k/new_v must match q's dtype")
         _rows(new_k, "new_k")
+        _rows(new_v, "new_v")
         args.new_k = new_k.data_ptr()
+        args.new_k_stride_seq, args.new_k_stride_head = new_k.stride(0), new_k.stride(1)
         args.new_v = new_v.data_ptr()
-        args.new_stride_seq, args.new_stride_head = new_k.stride(0), new_k.stride(1)
+        args.new_v_stride_seq, args.new_v_stride_head = new_v.stride(0), new_v.stride(1)
     if new_slots is not None:
         _require(new_k is not None, "new_slots requires new_k/new_v")
         _require(new_slots.dim() == 1 and new_slots.numel() >= B and new_slots.is_contiguous(),
@@ -244,6 +339,9 @@ def paged_decode(
     args.max_seq_len = int(max_seq_len)
     args.split_tokens = int(split_tokens)
     args.scale = float(scale)
+    if prologue is not None:
+        pro_struct = _prologue_struct(prologue, d, B)  # kept alive through the call
+        args.prologue = ctypes.pointer(pro_struct)
     nbytes = N.lib().va_paged_decode_workspace_bytes(ctypes.byref(args))
     ws = decode_workspace(device, nbytes)
     if ws is not None:
