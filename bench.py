@@ -127,7 +127,52 @@ def bench_decode(args, dev, stream):
     log(f"[decode] {ms:.3f} ms/step, {us_layer:.2f} us/layer, {gbs:.0f} GB/s "
         f"({per_layer_bytes / 1e6:.2f} MB/layer)")
     return dict(ms=ms, us_layer=us_layer, gbs=gbs, bytes_layer=per_layer_bytes, lens=lens,
-                batch=batch, qs=qs)
+                batch=batch, qs=qs, nks=nks, nvs=nvs)
+
+
+def bench_prologue(args, dev, stream, dec):
+    """Config 2's decode step with Qwen3's q/k RMSNorm + RoPE in front
+    (models/qwen3.py:44-49): fused into the decode launch vs the standalone
+    prologue kernel followed by the decode launch."""
+    from voiceagent_amd.layers.qwen3 import rotary_cos_sin_cache
+
+    batch, qs, nks, nvs = dec["batch"], dec["qs"], dec["nks"], dec["nvs"]
+    layers = workloads.LAYERS
+    g = torch.Generator(device=dev).manual_seed(17)
+    wq = (torch.rand(layers, workloads.HEAD_DIM, generator=g, device=dev) + 0.5).to(torch.bfloat16)
+    wk = (torch.rand(layers, workloads.HEAD_DIM, generator=g, device=dev) + 0.5).to(torch.bfloat16)
+    cs = rotary_cos_sin_cache(workloads.HEAD_DIM, 4096, 1_000_000.0).to(dev)
+    pos = (batch.context_lens.long() - 1).to(dev)
+    pros = [ops.QKPrologue(wq[i], wk[i], 1e-6, cs, pos) for i in range(layers)]
+    outs = torch.empty_like(qs)
+    common = dict(lens_cumulative=True, max_seq_len=batch.max_seq_len, scale=batch.scale,
+                  new_slots=batch.slot_mapping)
+
+    def fused():
+        for i in range(layers):
+            ops.paged_decode(qs[i], batch.k_pools[i], batch.v_pools[i], batch.block_tables,
+                             batch.cu_seqlens_k, new_k=nks[i], new_v=nvs[i], out=outs[i],
+                             prologue=pros[i], **common)
+
+    qn = torch.empty_like(qs[0])
+    kn = torch.empty_like(nks[0])
+
+    def two_launch():
+        for i in range(layers):
+            ops.qk_norm_rope(qs[i], nks[i], pros[i], q_out=qn, k_out=kn)
+            ops.paged_decode(qn, batch.k_pools[i], batch.v_pools[i], batch.block_tables,
+                             batch.cu_seqlens_k, new_k=kn, new_v=nvs[i], out=outs[i], **common)
+
+    res = {}
+    for name, fn in (("fused", fused), ("two_launch", two_launch)):
+        ms, _ = timed_graph(fn, args.steps, args.warmup, stream)
+        res[name] = ms * 1000.0 / layers
+    log(f"[prologue] decode + q/k norm + rope: fused {res['fused']:.2f} us/layer, "
+        f"two launches {res['two_launch']:.2f} us/layer")
+    return {"fused_us_per_layer": round(res["fused"], 2),
+            "two_launch_us_per_layer": round(res["two_launch"], 2),
+            "config": "cfg2 decode step (B=32, 28 layers) with Qwen3 q/k RMSNorm + RoPE "
+                      "applied to the raw projections"}
 
 
 def bench_longform(args, dev, stream):
@@ -337,7 +382,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--split", type=int, default=0, help="decode split_tokens (0 = auto)")
     ap.add_argument("--only", choices=["decode", "prefill", "encoder", "store", "longform",
-                                       "all"],
+                                       "prologue", "all"],
                     default="all")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
@@ -373,9 +418,13 @@ def main():
     if args.only == "store":
         print(json.dumps({"store": bench_store(args, dev, stream, dec)}))
         return
+    if args.only == "prologue":
+        print(json.dumps({"qwen3_prologue": bench_prologue(args, dev, stream, dec)}))
+        return
     extra = {}
     if args.only == "all":
         extra["store"] = bench_store(args, dev, stream, dec)
+        extra["qwen3_prologue"] = bench_prologue(args, dev, stream, dec)
         pre = bench_prefill(args, dev, stream)
         enc = bench_encoder(args, dev, stream)
         extra["prefill"] = {"us_per_layer": round(pre["us_layer"], 2),

@@ -26,7 +26,7 @@ int check_launch(const char* what);
 // ------------------------------------------------------------ element types
 // Each type describes how 16 bytes (one dwordx4 lane load) unpack to floats
 // and how floats pack back.  bf16 -> f32 is exact (bit shift); f32 -> bf16
-// rounds to nearest even, as torch does.
+// rounds to nearest even, as torch does (hardware conversion on gfx950).
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
 
@@ -56,17 +56,19 @@ struct BF16 {
       f[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
     }
   }
+  // Round to nearest even (NaN stays NaN) with gfx950's v_cvt_pk_bf16_f32.
   __device__ static inline uint16_t from_float(float x) {
-    uint32_t u = __float_as_uint(x);
-    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);  // quiet NaN
-    u += 0x7fffu + ((u >> 16) & 1u);
-    return (uint16_t)(u >> 16);
+    return __builtin_bit_cast(uint16_t, (__bf16)x);
   }
   __device__ static inline uint4 pack(const float* f) {
     uint32_t w[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      w[i] = (uint32_t)from_float(f[2 * i]) | ((uint32_t)from_float(f[2 * i + 1]) << 16);
+    for (int i = 0; i < 4; ++i) {
+      bf16x2_t v;
+      v.x = (__bf16)f[2 * i];
+      v.y = (__bf16)f[2 * i + 1];
+      w[i] = __builtin_bit_cast(uint32_t, v);
+    }
     return make_uint4(w[0], w[1], w[2], w[3]);
   }
 };

@@ -11,6 +11,8 @@
 // after the rotation), and products and sums are rounded separately.
 #pragma once
 
+#include <type_traits>
+
 #include "common.h"
 
 namespace va {
@@ -27,28 +29,77 @@ struct PrologueParams {
   const void* pos;
 };
 
+// x rounded to the element type (nearest even) and widened back to float.
+// bf16 uses gfx950's v_cvt_pk_bf16_f32.
 template <typename ET>
 __device__ inline float round_to(float x) {
   if constexpr (ET::kBytes == 4) {
     return x;
   } else if constexpr (ET::kIsBF16) {
-    return __uint_as_float((uint32_t)BF16::from_float(x) << 16);
+    return (float)(__bf16)x;
   } else {
     return (float)(_Float16)x;
   }
 }
 
-// E weights starting at element `start`, as floats.
+// The value held by lane (lane ^ (LPR / 2)) of the same LPR-lane row: the
+// rotary partner.  A 16-lane row (D = 128 in 16-bit types) is one DPP row,
+// rotated by 8; other widths use a cross-lane permute.
+template <int LPR>
+__device__ inline float rotary_partner(float x) {
+  if constexpr (LPR == 16) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x128 /* row_ror:8 */,
+                                                      0xF, 0xF, false));
+  } else {
+    return __shfl_xor(x, LPR / 2, 64);
+  }
+}
+
+// The E norm weights from element `start`, as raw bytes: two loads of E * 2
+// bytes each, issued without a branch (a loaded value that meets a branch
+// join makes the compiler wait for every outstanding load).  16-bit weights
+// sit in `a` (`b` repeats it); fp32 weights are `a` then `b`.  The weight
+// array must be aligned to 2 E bytes.
 template <int E>
-__device__ inline void load_weights(const void* w, int dtype, int start, float (&out)[E]) {
+struct WeightRaw {
+  using V = typename std::conditional<E == 8, uint4, uint2>::type;
+  V a, b;
+};
+
+template <int E>
+__device__ inline WeightRaw<E> load_weights_raw(const void* w, int dtype, int start) {
+  using V = typename WeightRaw<E>::V;
+  const int wb = dtype == VA_F32 ? 4 : 2;
+  const char* ptr = reinterpret_cast<const char*>(w) + (int64_t)start * wb;
+  WeightRaw<E> r;
+  r.a = *reinterpret_cast<const V*>(ptr);
+  r.b = *reinterpret_cast<const V*>(ptr + (wb == 4 ? E * 2 : 0));
+  return r;
+}
+
+template <int E>
+__device__ inline void convert_weights(const WeightRaw<E>& r, int dtype, float (&out)[E]) {
+  uint32_t wa[E / 2], wbv[E / 2];
+  __builtin_memcpy(wa, &r.a, sizeof(wa));
+  __builtin_memcpy(wbv, &r.b, sizeof(wbv));
+  if (dtype == VA_F32) {
 #pragma unroll
-  for (int e = 0; e < E; ++e) {
-    if (dtype == VA_F32) {
-      out[e] = reinterpret_cast<const float*>(w)[start + e];
-    } else if (dtype == VA_BF16) {
-      out[e] = __uint_as_float((uint32_t)reinterpret_cast<const uint16_t*>(w)[start + e] << 16);
-    } else {
-      out[e] = (float)reinterpret_cast<const _Float16*>(w)[start + e];
+    for (int e = 0; e < E / 2; ++e) {
+      out[e] = __uint_as_float(wa[e]);
+      out[E / 2 + e] = __uint_as_float(wbv[e]);
+    }
+  } else if (dtype == VA_BF16) {
+#pragma unroll
+    for (int e = 0; e < E / 2; ++e) {
+      out[2 * e] = __uint_as_float(wa[e] << 16);
+      out[2 * e + 1] = __uint_as_float(wa[e] & 0xffff0000u);
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < E / 2; ++e) {
+      const f16x2_t hv = __builtin_bit_cast(f16x2_t, wa[e]);
+      out[2 * e] = (float)hv.x;
+      out[2 * e + 1] = (float)hv.y;
     }
   }
 }
@@ -80,7 +131,7 @@ __device__ inline void qk_prologue(float (&x)[E], const float (&w)[E], float eps
   for (int e = 0; e < E; ++e) x[e] = round_to<ET>(__fmul_rn(round_to<ET>(__fmul_rn(x[e], r)), w[e]));
   float pt[E];
 #pragma unroll
-  for (int e = 0; e < E; ++e) pt[e] = __shfl_xor(x[e], LPR / 2, 64);
+  for (int e = 0; e < E; ++e) pt[e] = rotary_partner<LPR>(x[e]);
 #pragma unroll
   for (int e = 0; e < E; ++e) {
     const float a = __fmul_rn(x[e], c[e]), b = __fmul_rn(pt[e], s[e]);

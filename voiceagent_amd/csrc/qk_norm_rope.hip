@@ -45,10 +45,11 @@ __global__ __launch_bounds__(kQkThreads) void qk_norm_rope_kernel(QkParams p) {
   const uint4 raw = ld16(src + col * 16);
   int64_t pos = load_index(p.pp.pos, tok, p.pp.pos_i64);
   pos = pos < 0 ? 0 : (pos >= p.pp.max_pos ? p.pp.max_pos - 1 : pos);
+  const WeightRaw<E> wr = load_weights_raw<E>(isq ? p.pp.q_w : p.pp.k_w, p.pp.w_dtype, col * E);
   float x[E], w[E], c[E], s[E];
-  ET::unpack(raw, x);
-  load_weights<E>(isq ? p.pp.q_w : p.pp.k_w, p.pp.w_dtype, col * E, w);
   load_rotary<E, LPR>(p.pp, pos, col, D, c, s);
+  ET::unpack(raw, x);
+  convert_weights<E>(wr, p.pp.w_dtype, w);
   qk_prologue<ET, LPR, E>(x, w, p.pp.eps, D, c, s, col < LPR / 2);
   st16(dst + col * 16, ET::pack(x));
 }
@@ -99,6 +100,8 @@ extern "C" int va_qk_norm_rope(const va_qk_norm_rope_args* a, void* stream) {
                             (uintptr_t)a->k_out};
   for (uintptr_t p : ptrs)
     VA_CHECK_ARG(p % 16 == 0, "va_qk_norm_rope: pointers must be 16-byte aligned");
+  VA_CHECK_ARG((uintptr_t)pr.q_norm_weight % 16 == 0 && (uintptr_t)pr.k_norm_weight % 16 == 0,
+               "va_qk_norm_rope: norm weights must be 16-byte aligned");
 
   QkParams p;
   p.q = (const char*)a->q;
