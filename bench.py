@@ -406,10 +406,12 @@ def main():
     result = {}
     if args.only in ("prefill",):
         result["prefill"] = bench_prefill(args, dev, stream)
-        print(json.dumps({"prefill": {k: v for k, v in result["prefill"].items()}}))
+        print(json.dumps({"prefill": {k: v for k, v in result["prefill"].items()
+                                      if k != "inputs"}}))
         return
     if args.only in ("encoder",):
-        print(json.dumps({"encoder": bench_encoder(args, dev, stream)}))
+        enc = bench_encoder(args, dev, stream)
+        print(json.dumps({"encoder": {k: v for k, v in enc.items() if k != "inputs"}}))
         return
     if args.only == "longform":
         print(json.dumps({"longform": bench_longform(args, dev, stream)}))

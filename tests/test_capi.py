@@ -83,6 +83,10 @@ def test_decode_workspace_sizing():
     args.split_tokens = 1  # an explicit split is honoured (rounded up to a workgroup round)
     args.num_seqs, args.max_seq_len = 32, 600
     assert lib.va_paged_decode_workspace_bytes(ctypes.byref(args)) > 0
+    # a tiny explicit split on a long context is capped at 256 partitions
+    args.num_seqs, args.split_tokens, args.max_seq_len = 2, 16, 1 << 20
+    per_part = 2 * 8 * 2 * (2 * 4 + 128 * 4)  # pairs * G * (m, l + o) bytes
+    assert lib.va_paged_decode_workspace_bytes(ctypes.byref(args)) <= 256 * per_part + 256
     bad = N.DecodeArgs()
     assert lib.va_paged_decode_workspace_bytes(ctypes.byref(bad)) == 0
 

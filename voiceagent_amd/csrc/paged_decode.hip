@@ -8,10 +8,8 @@
 namespace va {
 
 // ----------------------------------------------------------------- host side
-// Longest context a sequence may be split into without growing the
-// partition: beyond kMaxParts partitions the partition grows instead, which
-// bounds the merge kernel's loop.
-constexpr int kMaxParts = 256;
+// A context is split into at most kMaxParts partitions (the partition grows
+// instead), which bounds the merge kernel's LDS and loops.
 
 struct DecodePlan {
   int split_tokens;
@@ -62,15 +60,15 @@ static DecodePlan plan_decode(const va_decode_args* a) {
   if (P <= 0) {
     // Split contexts only as far as needed to give every CU one workgroup:
     // with at least as many (sequence, kv head) pairs as CUs, one partition
-    // per pair.  Partitions are at least one round of in-flight chunks and
-    // at most kMaxParts per context.
+    // per pair.  Partitions are at least one round of in-flight chunks.
     const int64_t cus = current_device_cus();
     const int64_t want = pairs >= cus ? 1 : cus / (pairs > 0 ? pairs : 1);
     P = (int)((max_len + want - 1) / want);
     if (P < unit) P = unit;
-    const int cap = (max_len + kMaxParts - 1) / kMaxParts;
-    if (P < cap) P = cap;
   }
+  // Any split (automatic or requested) keeps at most kMaxParts partitions.
+  const int cap = (max_len + kMaxParts - 1) / kMaxParts;
+  if (P < cap) P = cap;
   P = ((P + unit - 1) / unit) * unit;
   if (P < unit) P = unit;
   pl.split_tokens = P;
@@ -174,7 +172,7 @@ extern "C" int va_paged_decode(const va_decode_args* a, void* stream) {
     }
     VA_CHECK_ARG((uintptr_t)a->workspace % 16 == 0, "va_paged_decode: workspace alignment");
   }
-  VA_CHECK_ARG(pl.max_parts <= 65535, "va_paged_decode: too many context partitions");
+  VA_CHECK_ARG(pl.max_parts <= kMaxParts, "va_paged_decode: too many context partitions");
 
   DecodeParams p;
   p.q = (const char*)a->q;

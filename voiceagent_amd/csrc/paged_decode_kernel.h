@@ -493,14 +493,30 @@ __global__ __launch_bounds__((DecodeShape<ET, D, G>::NW * 64),
   }
 }
 
+// Most partitions one context is split into (the host grows the partition
+// beyond this), which bounds the merge kernel's LDS.
+constexpr int kMaxParts = 256;
+
 // Merge of the partitions of one (sequence, kv head) pair: out = sum_q
 // 2^(m_q - M) o_q / sum_q 2^(m_q - M) l_q with M = max_q m_q.  Pairs that
 // fit one partition were written by the first kernel and are skipped.
+// Phase 1: wave w reduces (m, l) of every partition for query heads
+// g = w, w + 4, ... (lanes over partitions) into LDS weights 2^(m_q - M) and
+// 1 / sum.  Phase 2: each thread sums o_q[d] for its (g, d) in batches of
+// 32 partitions whose loads are all in flight together.  Loads use clamped
+// indices and are masked afterwards, so no load sits behind a branch.
 template <typename ET, int D, int G>
 __global__ __launch_bounds__(256) void paged_decode_merge_kernel(DecodeParams p) {
   constexpr int E = ET::kPerVec;
+  constexpr int kPerLane = kMaxParts / 64;
+  constexpr int kBatch = 32;
+  __shared__ float s_w[kMaxParts][G];
+  __shared__ float s_inv[G];
   const int h = blockIdx.x;
   const int b = blockIdx.y;
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6;
+  const int lane = tid & 63;
   int L;
   if (p.lens_cum)
     L = (int)(load_index(p.lens, b + 1, p.lens_i64) - load_index(p.lens, b, p.lens_i64));
@@ -511,35 +527,53 @@ __global__ __launch_bounds__(256) void paged_decode_merge_kernel(DecodeParams p)
   int nparts = (L + p.split_tokens - 1) / p.split_tokens;
   if (nparts > p.max_parts) nparts = p.max_parts;
   if (nparts <= 1) return;
-  const int64_t pair = (int64_t)b * p.num_kv_heads + h;
-  constexpr int kBatch = 8;  // partials whose loads are in flight together
-  for (int idx = threadIdx.x; idx < G * D; idx += 256) {
-    const int g = idx / D, d = idx % D;
-    float M = kNegBig, Lt = 0.f, Ot = 0.f;
-    for (int q0 = 0; q0 < nparts; q0 += kBatch) {
-      float mq[kBatch], lq[kBatch], oq[kBatch];
+  const int64_t base = (int64_t)b * p.num_kv_heads + h;  // pair index
+  const int64_t pair_slot0 = base * p.max_parts;
+
+  for (int g = wave; g < G; g += 4) {
+    float mq[kPerLane], lq[kPerLane];
 #pragma unroll
-      for (int j = 0; j < kBatch; ++j) {
-        mq[j] = kNegBig;
-        lq[j] = 0.f;
-        oq[j] = 0.f;
-        if (q0 + j < nparts) {
-          const int64_t slot = (pair * p.max_parts + q0 + j) * G + g;
-          mq[j] = p.part_ml[slot * 2];
-          lq[j] = p.part_ml[slot * 2 + 1];
-          oq[j] = p.part_o[slot * D + d];
-        }
-      }
+    for (int i = 0; i < kPerLane; ++i) {
+      const int q = lane + 64 * i;
+      const int64_t slot = (pair_slot0 + (q < nparts ? q : nparts - 1)) * G + g;
+      mq[i] = p.part_ml[slot * 2];
+      lq[i] = p.part_ml[slot * 2 + 1];
+    }
+    float M = kNegBig;
 #pragma unroll
-      for (int j = 0; j < kBatch; ++j) {
-        const float Mn = fmaxf(M, mq[j]);
-        const float a = fast_exp2(M - Mn), bq = fast_exp2(mq[j] - Mn);
-        Lt = Lt * a + lq[j] * bq;
-        Ot = Ot * a + oq[j] * bq;
-        M = Mn;
+    for (int i = 0; i < kPerLane; ++i)
+      if (lane + 64 * i < nparts) M = fmaxf(M, mq[i]);
+    M = group_max<64>(M);
+    float Lt = 0.f;
+#pragma unroll
+    for (int i = 0; i < kPerLane; ++i) {
+      const int q = lane + 64 * i;
+      if (q < nparts) {
+        const float w = fast_exp2(mq[i] - M);
+        s_w[q][g] = w;
+        Lt += w * lq[i];
       }
     }
-    const float val = Lt > 0.f ? Ot / Lt : 0.f;
+    Lt = group_sum<64>(Lt);
+    if (lane == 0) s_inv[g] = Lt > 0.f ? 1.f / Lt : 0.f;
+  }
+  __syncthreads();
+
+  for (int idx = tid; idx < G * D; idx += 256) {
+    const int g = idx / D, d = idx % D;
+    float acc = 0.f;
+    for (int q0 = 0; q0 < nparts; q0 += kBatch) {
+      float oq[kBatch];
+#pragma unroll
+      for (int j = 0; j < kBatch; ++j) {
+        const int q = q0 + j < nparts ? q0 + j : nparts - 1;
+        oq[j] = p.part_o[((pair_slot0 + q) * G + g) * D + d];
+      }
+#pragma unroll
+      for (int j = 0; j < kBatch; ++j)
+        if (q0 + j < nparts) acc = fmaf(s_w[q0 + j][g], oq[j], acc);
+    }
+    const float val = acc * s_inv[g];
     char* dst = p.out + b * p.o_sb + (int64_t)(h * G + g) * p.o_sh + d * ET::kBytes;
     if constexpr (ET::kBytes == 4) {
       *reinterpret_cast<float*>(dst) = val;
