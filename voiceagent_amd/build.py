@@ -39,6 +39,16 @@ HIPCC_FLAGS = [
 ]
 
 
+# Per-source extra flags.  The decode translation units keep matrix-core
+# accumulators in ordinary VGPRs: the online-softmax rescale of the output
+# accumulators is VALU work, and AGPR accumulators would be copied out and
+# back on every tile.
+EXTRA_FLAGS = {
+    "paged_decode_bf16.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=true"],
+    "paged_decode_f16.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=true"],
+}
+
+
 def _hipcc() -> str:
     path = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
     if not Path(path).exists():
@@ -47,7 +57,7 @@ def _hipcc() -> str:
 
 
 def _compile(hipcc: str, src: Path, obj: Path) -> tuple[Path, str]:
-    cmd = [hipcc, *HIPCC_FLAGS, "-c", str(src), "-o", str(obj)]
+    cmd = [hipcc, *HIPCC_FLAGS, *EXTRA_FLAGS.get(src.name, []), "-c", str(src), "-o", str(obj)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     noise = "is not a recognized feature for this target"
     log = "\n".join(

@@ -136,6 +136,14 @@ struct F32 {
 
 // ------------------------------------------------------------ memory access
 __device__ inline uint4 ld16(const void* p) { return *reinterpret_cast<const uint4*>(p); }
+// Non-temporal 16-byte load (the nt cache policy): for data read exactly once,
+// such as the K/V rows of a decode step.  One CU streams ~80 GB/s with it and
+// ~60 GB/s without it on MI355X.
+typedef unsigned va_u32x4 __attribute__((ext_vector_type(4)));
+__device__ inline uint4 ld16_nt(const void* p) {
+  const va_u32x4 t = __builtin_nontemporal_load(reinterpret_cast<const va_u32x4*>(p));
+  return make_uint4(t.x, t.y, t.z, t.w);
+}
 __device__ inline void st16(void* p, uint4 v) { *reinterpret_cast<uint4*>(p) = v; }
 
 __device__ inline int64_t load_index(const void* p, int64_t i, int is_i64) {
@@ -197,5 +205,45 @@ __device__ inline float strided_max(float x) {
 }
 
 __device__ inline float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// ------------------------------------------------------- global -> LDS DMA
+// One 16-byte global -> LDS copy per lane (global_load_lds_dwordx4): lane l's
+// bytes land at lds + 16 l.  Inline asm, so the compiler neither waits on it
+// nor moves memory accesses across it; callers wait with wait_vmcnt.
+// The compiler's hazard recognizer does not look inside inline asm, so each
+// asm pads the wait states the ISA requires before the load itself: five
+// after a VALU write of an SGPR the load reads (uniform bases come from
+// v_readfirstlane) and one after the SALU write of M0.
+__device__ inline void dma16(uint32_t off, const void* base, uint32_t lds) {
+  asm volatile("s_nop 4\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "{m0}"(lds)
+               : "memory");
+}
+// The same with the non-temporal cache policy (data read exactly once).
+__device__ inline void dma16_nt(uint32_t off, const void* base, uint32_t lds) {
+  asm volatile("s_nop 4\n\tglobal_load_lds_dwordx4 %0, %1 nt" ::"v"(off), "s"(base), "{m0}"(lds)
+               : "memory");
+}
+// The same from a per-lane 64-bit address.
+__device__ inline void dma16(const void* src, uint32_t lds) {
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "{m0}"(lds) : "memory");
+}
+
+// s_waitcnt vmcnt(N) / lgkmcnt(0) as inline asm with a memory clobber: no
+// memory access moves across the wait (the waitcnt builtin is not a memory
+// barrier for the compiler).
+template <int N>
+__device__ inline void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+__device__ inline void wait_lgkmcnt0() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+
+// A wave-uniform pointer in SGPRs (readfirstlane of both halves).
+__device__ inline const char* uniform_ptr(const char* ptr) {
+  const uint64_t u = (uint64_t)(uintptr_t)ptr;
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)u);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(u >> 32));
+  return (const char*)(uintptr_t)(((uint64_t)hi << 32) | lo);
+}
 
 }  // namespace va

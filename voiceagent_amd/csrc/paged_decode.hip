@@ -1,9 +1,11 @@
 // Host side of the paged decode: argument checks, the context split and
-// launch dispatch (kernels in paged_decode_kernel.h, instantiated per
-// element type in paged_decode_{bf16,f16,f32}.hip).
+// launch dispatch (kernels in paged_decode_kernel.h and paged_decode_mfma.h,
+// instantiated per element type in paged_decode_{bf16,f16,f32}.hip).
 #include <atomic>
+#include <cstdlib>
+#include <cstring>
 
-#include "paged_decode_kernel.h"
+#include "paged_decode_mfma.h"
 
 namespace va {
 
@@ -24,6 +26,42 @@ static int decode_unit() {
 }
 
 static int decode_unit_for(int dtype, int D, int G);
+
+// The matrix-core kernel serves 16-bit K/V with block sizes that are
+// multiples of 16 and no key_valid_mask; every other call takes the general
+// kernel.  VA_DECODE_KERNEL=general in the environment forces the general
+// kernel (for comparisons).
+static bool general_kernel_forced() {
+  static const int forced = [] {
+    const char* e = std::getenv("VA_DECODE_KERNEL");
+    return (e != nullptr && std::strcmp(e, "general") == 0) ? 1 : 0;
+  }();
+  return forced != 0;
+}
+
+static bool use_mfma_decode(const va_decode_args* a) {
+  if (a->dtype != VA_BF16 && a->dtype != VA_F16) return false;
+  if (a->pool.block_size <= 0 || a->pool.block_size % kChunk != 0) return false;
+  if (a->valid_mask != nullptr && a->valid_len > 0) return false;
+  if (a->head_dim != 64 && a->head_dim != 128 && a->head_dim != 256) return false;
+  if (a->num_kv_heads <= 0 || a->num_heads % a->num_kv_heads != 0) return false;
+  const int G = a->num_heads / a->num_kv_heads;
+  if (G != 1 && G != 2 && G != 4 && G != 8) return false;
+  // Per-lane DMA offsets inside a 16-row tile are 32-bit.
+  if (a->pool.stride_slot < 0 ||
+      (kChunk - 1) * a->pool.stride_slot * 2 + (int64_t)a->head_dim * 2 >= ((int64_t)1 << 31))
+    return false;
+  return !general_kernel_forced();
+}
+
+static int mfma_unit_for(int D) {
+  switch (D) {
+    case 64: return mfma_decode_unit<64>();
+    case 128: return mfma_decode_unit<128>();
+    case 256: return mfma_decode_unit<256>();
+    default: return 0;
+  }
+}
 
 // Compute units of the current device (cached per device; 256, the MI355X
 // count, when no device is visible, e.g. when only the workspace size is
@@ -52,7 +90,8 @@ static int current_device_cus() {
 static DecodePlan plan_decode(const va_decode_args* a) {
   DecodePlan pl{};
   const int G = a->num_kv_heads > 0 ? a->num_heads / a->num_kv_heads : 1;
-  int unit = decode_unit_for(a->dtype, a->head_dim, G);
+  int unit = use_mfma_decode(a) ? mfma_unit_for(a->head_dim)
+                                : decode_unit_for(a->dtype, a->head_dim, G);
   if (unit <= 0) unit = 128;
   const int max_len = a->max_seq_len > 0 ? a->max_seq_len : 1;
   int P = a->split_tokens;
@@ -254,10 +293,15 @@ extern "C" int va_paged_decode(const va_decode_args* a, void* stream) {
   const dim3 grid(a->num_seqs, a->num_kv_heads, pl.max_parts);
   const hipStream_t s = (hipStream_t)stream;
   bool ok = false;
-  switch (a->dtype) {
-    case VA_BF16: ok = launch_paged_decode<BF16>(a->head_dim, G, p, grid, s); break;
-    case VA_F16: ok = launch_paged_decode<F16>(a->head_dim, G, p, grid, s); break;
-    case VA_F32: ok = launch_paged_decode<F32>(a->head_dim, G, p, grid, s); break;
+  if (use_mfma_decode(a)) {
+    ok = a->dtype == VA_BF16 ? launch_paged_decode_mfma<BF16>(a->head_dim, G, p, grid, s)
+                             : launch_paged_decode_mfma<F16>(a->head_dim, G, p, grid, s);
+  } else {
+    switch (a->dtype) {
+      case VA_BF16: ok = launch_paged_decode<BF16>(a->head_dim, G, p, grid, s); break;
+      case VA_F16: ok = launch_paged_decode<F16>(a->head_dim, G, p, grid, s); break;
+      case VA_F32: ok = launch_paged_decode<F32>(a->head_dim, G, p, grid, s); break;
+    }
   }
   if (!ok) {
     set_error("va_paged_decode: unsupported head_dim %d / group size %d (head_dim 64|128|256, "

@@ -249,14 +249,14 @@ __global__ __launch_bounds__((DecodeShape<ET, D, G>::NW * 64),
           const uint32_t off = (uint32_t)blk * (uint32_t)p.s_blk +
                                (uint32_t)(tok % p.block_size) * (uint32_t)p.s_slot +
                                (uint32_t)head_off;
-          kr[r] = ld16(p.kp + off);
-          vr[r] = ld16(p.vp + off);
+          kr[r] = ld16_nt(p.kp + off);
+          vr[r] = ld16_nt(p.vp + off);
         }
       } else if (ok) {
         const int64_t off =
             (int64_t)blk * p.s_blk + (int64_t)(tok % p.block_size) * p.s_slot + head_off;
-        kr[r] = ld16(p.kp + off);
-        vr[r] = ld16(p.vp + off);
+        kr[r] = ld16_nt(p.kp + off);
+        vr[r] = ld16_nt(p.vp + off);
       }
     }
   };

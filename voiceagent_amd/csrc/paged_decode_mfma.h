@@ -1,0 +1,477 @@
+// Paged-KV decode attention on CDNA4 matrix cores, for 16-bit K/V whose
+// block size is a multiple of 16 and without a key_valid_mask (the engine's
+// decode; the general kernel in paged_decode_kernel.h covers the rest).
+//
+// Same semantics, grid and partial/merge protocol as paged_decode_kernel:
+// the grid is (sequence, kv head, partition); a workgroup owns P consecutive
+// tokens of one (sequence, kv head) pair and all G query heads of its group.
+//
+// Work decomposition.  A workgroup is W = 4 wave64s (one per SIMD).  The
+// partition's 16-token tiles go round robin to the waves (tile c to wave
+// c % W), and each wave runs its own pipeline with no workgroup barrier:
+//   * the K and V rows of a tile (16 rows of one block) are copied from HBM
+//     straight into the wave's LDS ring of S stages with
+//     global_load_lds_dwordx4 (1 KiB per instruction, 16-byte chunks stored
+//     XOR-swizzled by row so the matrix-core reads below are conflict-free);
+//     S - 1 tiles are in flight while one is reduced;
+//   * S^T = K Q^T  (16 tokens x 16 columns, G of them real query heads) with
+//     v_mfma_f32_16x16x32: A = K rows from LDS (ds_read_b128), B = Q^T held
+//     in registers for the whole loop;
+//   * online softmax in the exp2 domain on the four scores each lane holds
+//     (tokens 4 (lane / 16) + i of column lane % 16); the reference maximum is
+//     raised only when a column's new maximum exceeds it by more than kLazy;
+//   * O^T += V^T P^T with v_mfma_f32_16x16x16: P^T is the S^T accumulator
+//     packed to 16 bits in place (its layout is already the B operand's),
+//     V^T comes from the row-major V tile through ds_read_b64_tr_b16.
+// Nearly all arithmetic runs on the matrix cores, so one wave per SIMD keeps
+// HBM busy and a workgroup can pull several times its fair share of
+// bandwidth once shorter contexts have finished.  The waves merge through
+// LDS at the end; partitioned contexts write (m, l, o) partials that
+// paged_decode_merge_kernel combines.
+#pragma once
+
+#include "paged_decode_kernel.h"
+
+namespace va {
+
+typedef __bf16 mf_bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 mf_f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 mf_f16x4 __attribute__((ext_vector_type(4)));
+typedef short mf_s16x4 __attribute__((ext_vector_type(4)));
+typedef float mf_f32x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) mf_s16x4 mf_lds_s16x4;
+
+template <typename ET>
+struct DecodeMma;
+
+template <>
+struct DecodeMma<BF16> {
+  __device__ static inline mf_f32x4 qk(uint4 a, uint4 b, mf_f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(mf_bf16x8, a),
+                                                   __builtin_bit_cast(mf_bf16x8, b), c, 0, 0, 0);
+  }
+  __device__ static inline mf_f32x4 pv(mf_s16x4 a, uint2 b, mf_f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, __builtin_bit_cast(mf_s16x4, b), c, 0, 0,
+                                                     0);
+  }
+  __device__ static inline uint32_t pack2(float lo, float hi) {
+    bf16x2_t v;
+    v.x = (__bf16)lo;
+    v.y = (__bf16)hi;
+    return __builtin_bit_cast(uint32_t, v);
+  }
+};
+
+template <>
+struct DecodeMma<F16> {
+  __device__ static inline mf_f32x4 qk(uint4 a, uint4 b, mf_f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(mf_f16x8, a),
+                                                  __builtin_bit_cast(mf_f16x8, b), c, 0, 0, 0);
+  }
+  __device__ static inline mf_f32x4 pv(mf_s16x4 a, uint2 b, mf_f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(mf_f16x4, a),
+                                                 __builtin_bit_cast(mf_f16x4, b), c, 0, 0, 0);
+  }
+  __device__ static inline uint32_t pack2(float lo, float hi) {
+    f16x2_t v;
+    v.x = (_Float16)lo;
+    v.y = (_Float16)hi;
+    return __builtin_bit_cast(uint32_t, v);
+  }
+};
+
+// Geometry of the matrix-core decode for head_dim D (16-bit elements).
+template <int D>
+struct MfmaDecodeShape {
+  static constexpr int ROWB = D * 2;           // bytes per K/V row
+  static constexpr int CPR = ROWB / 16;        // 16-byte chunks per row
+  static constexpr int RPI = 64 / CPR;         // rows per DMA instruction (1 KiB)
+  static constexpr int NI = kChunk / RPI;      // DMA instructions per tile, K or V
+  static constexpr int TILE_B = kChunk * ROWB; // bytes of one K (or V) tile
+  // Two waves per SIMD with two stages each (128 KiB of LDS) where the tiles
+  // allow; head_dim 256 keeps one wave per SIMD.
+  static constexpr int W = 8 * 2 * 2 * TILE_B <= 131072 ? 8 : 4;  // waves per workgroup
+  static constexpr int S = 131072 / (W * 2 * TILE_B) < 2 ? 2 : 131072 / (W * 2 * TILE_B);
+  static constexpr int WAVE_B = S * 2 * TILE_B;  // LDS bytes per wave
+  static constexpr int DS = D / 32;            // k-steps of S^T = K Q^T
+  static constexpr int DT = D / 16;            // 16-row d tiles of O^T
+  static constexpr int LPR = D / 8;            // lanes per row in the row layout
+  static constexpr int RPL = 64 / LPR;         // rows per wave in the row layout
+};
+
+// Tokens per partition unit of the matrix-core kernel: one round of S tiles
+// on every wave.
+template <int D>
+constexpr int mfma_decode_unit() {
+  return MfmaDecodeShape<D>::W * MfmaDecodeShape<D>::S * kChunk;
+}
+
+// LDS position of 16-byte chunk c of row r in a staged tile: c ^ swz(r).
+// The XOR spreads the 16 rows of a K read (one chunk per row) and the four
+// rows x four half-chunks of a transposed V read over distinct banks.
+template <int D>
+__device__ inline int dec_swz(int row) {
+  if constexpr (D == 64)
+    return (((row >> 1) & 3) << 1) | ((row >> 3) & 1);
+  else
+    return ((row & 7) << 1) | ((row >> 3) & 1);
+}
+
+__device__ __align__(16) const uint4 kDecZeroRow = {0u, 0u, 0u, 0u};
+
+// Lazy-rescale slack of the online softmax in log2 units (p <= 2^kDecLazy).
+constexpr float kDecLazy = 8.0f;
+
+template <typename ET, int D, int G, bool kProlog>
+__global__ __launch_bounds__(MfmaDecodeShape<D>::W * 64, 1) void paged_decode_mfma_kernel(
+    DecodeParams p) {
+  using Sh = MfmaDecodeShape<D>;
+  using M = DecodeMma<ET>;
+  constexpr int W = Sh::W, S = Sh::S, NI = Sh::NI, ROWB = Sh::ROWB, CPR = Sh::CPR;
+  constexpr int RPI = Sh::RPI, TILE_B = Sh::TILE_B, DS = Sh::DS, DT = Sh::DT;
+  constexpr int LPR = Sh::LPR, RPL = Sh::RPL, E = 8;
+  constexpr int NT = W * 64;
+  constexpr int QROWS = (G + RPL - 1) / RPL;  // query rows per lane in the row layout
+  static_assert(G <= 16, "at most 16 query heads per kv head");
+  static_assert(W * G * D * 4 + 2 * W * G * 4 <= W * Sh::WAVE_B, "merge scratch");
+
+  __shared__ __align__(1024) char s_buf[W * Sh::WAVE_B];
+
+  const int b = blockIdx.x;
+  const int h = blockIdx.y;
+  const int part = blockIdx.z;
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6;
+  const int lane = tid & 63;
+  const int r16 = lane & 15;   // MFMA row / column index of this lane
+  const int c4 = lane >> 4;    // MFMA k-group of this lane
+  const int rg = lane / LPR;   // row-layout row of this lane
+  const int col = lane % LPR;  // row-layout 16-byte column of this lane
+  const int P = p.split_tokens;
+  const int start = part * P;
+  const int64_t table_row = (int64_t)b * p.t_sb;
+
+  // ---- independent loads: length, this wave's block ids, the query rows,
+  // the current K/V row and its slot, the prologue inputs ----
+  int L;
+  if (p.lens_cum)
+    L = (int)(load_index(p.lens, b + 1, p.lens_i64) - load_index(p.lens, b, p.lens_i64));
+  else
+    L = (int)load_index(p.lens, b, p.lens_i64);
+  // Block of the wave's tile `lane` (tile 64 i + lane after refills): `tab`
+  // serves the DMA issue, which runs S tiles ahead; `tab_proc` is the copy
+  // the tile being reduced reads (refreshed when it reaches the refill).
+  int tab = 0;
+  {
+    const int c = wave + W * lane;
+    if (c * kChunk < P || part == p.max_parts - 1)
+      tab = (int)table_entry(p, table_row, (start + c * kChunk) / p.block_size);
+  }
+  uint4 qrow[QROWS];
+#pragma unroll
+  for (int k = 0; k < QROWS; ++k) {
+    const int g = rg + RPL * k;
+    qrow[k] = g < G ? ld16(p.q + b * p.q_sb + (int64_t)(h * G + g) * p.q_sh + col * 16)
+                    : make_uint4(0, 0, 0, 0);
+  }
+  uint4 kcur = make_uint4(0, 0, 0, 0), vcur = make_uint4(0, 0, 0, 0);
+  if (p.new_k != nullptr) {
+    kcur = ld16(p.new_k + b * p.nk_sb + h * p.nk_sh + col * 16);
+    vcur = ld16(p.new_v + b * p.nv_sb + h * p.nv_sh + col * 16);
+  }
+  int64_t new_slot = -1;
+  if (p.new_slots != nullptr) new_slot = load_index(p.new_slots, b, p.new_slots_i64);
+  float pro_c[E], pro_s[E];
+  WeightRaw<E> pro_wq{}, pro_wk{};
+  int64_t pos = 0;
+  if constexpr (kProlog) {
+    pos = load_index(p.pro.pos, b, p.pro.pos_i64);
+    pos = pos < 0 ? 0 : (pos >= p.pro.max_pos ? p.pro.max_pos - 1 : pos);
+    pro_wq = load_weights_raw<E>(p.pro.q_w, p.pro.w_dtype, col * E);
+    pro_wk = load_weights_raw<E>(p.pro.k_w != nullptr ? p.pro.k_w : p.pro.q_w, p.pro.w_dtype,
+                                 col * E);
+    load_rotary<E, LPR>(p.pro, pos, col, D, pro_c, pro_s);
+  }
+  L = __builtin_amdgcn_readfirstlane(L);
+
+  if (L <= 0) {
+    // Nothing to attend: the output is defined as 0.
+    if (part == 0) {
+      for (int idx = tid; idx < G * D / E; idx += NT) {
+        const int g = idx / (D / E), d = (idx % (D / E)) * E;
+        st16(p.out + b * p.o_sb + (int64_t)(h * G + g) * p.o_sh + d * 2, make_uint4(0, 0, 0, 0));
+      }
+    }
+    return;
+  }
+  if (start >= L) return;
+  int nparts = (L + P - 1) / P;
+  const bool last_grid_part = part == p.max_parts - 1;
+  if (nparts > p.max_parts) nparts = p.max_parts;  // the last partition absorbs the rest
+  const int end = last_grid_part ? L : min(start + P, L);
+  const int nch = (end - start + kChunk - 1) / kChunk;
+  const int ntw = nch > wave ? (nch - wave + W - 1) / W : 0;  // tiles of this wave
+
+  // The current row is position L - 1 when this partition holds it: it is
+  // stored to its slot and replaces the pool row in the staged tile.
+  const int new_tok = (p.new_k != nullptr && L - 1 >= start && L - 1 < end) ? L - 1 : -1;
+  const int new_tile = new_tok >= 0 ? (new_tok - start) / kChunk : -1;  // partition chunk
+  const int64_t cap = (int64_t)p.num_blocks * p.block_size;
+
+  char* const s_wave = s_buf + wave * Sh::WAVE_B;
+  const uint32_t lds_wave = __builtin_amdgcn_readfirstlane(
+      (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)s_wave);
+
+  // ---- prologue (Qwen3 q/k RMSNorm + RoPE) in the row layout, then the
+  // query rows go through LDS into the B-operand layout ----
+  if constexpr (kProlog) {
+    const bool first_half = col < LPR / 2;
+    float w[E];
+    convert_weights<E>(pro_wq, p.pro.w_dtype, w);
+#pragma unroll
+    for (int k = 0; k < QROWS; ++k) {
+      float x[E];
+      ET::unpack(qrow[k], x);
+      qk_prologue<ET, LPR, E>(x, w, p.pro.eps, D, pro_c, pro_s, first_half);
+      qrow[k] = ET::pack(x);
+    }
+    if (new_tok >= 0) {
+      convert_weights<E>(pro_wk, p.pro.w_dtype, w);
+      float x[E];
+      ET::unpack(kcur, x);
+      qk_prologue<ET, LPR, E>(x, w, p.pro.eps, D, pro_c, pro_s, first_half);
+      kcur = ET::pack(x);
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < QROWS; ++k) {
+    const int g = rg + RPL * k;
+    if (g < G) st16(s_wave + g * ROWB + col * 16, qrow[k]);
+  }
+  uint4 qb[DS];  // Q^T: lane holds q[head r16][32 j + 8 c4, +8)
+#pragma unroll
+  for (int j = 0; j < DS; ++j)
+    qb[j] = r16 < G ? *reinterpret_cast<const uint4*>(s_wave + r16 * ROWB + (4 * j + c4) * 16)
+                    : make_uint4(0, 0, 0, 0);
+  // Every wave has its q before any DMA may overwrite the scratch rows.
+  wait_lgkmcnt0();
+
+  // ---- tile DMA: instruction i of a tile moves rows RPI i .. RPI i + RPI - 1;
+  // lane l writes row RPI i + l / CPR at chunk position l % CPR, i.e. reads
+  // logical chunk (l % CPR) ^ swz(row) of that row ----
+  uint32_t loff[NI];
+#pragma unroll
+  for (int i = 0; i < NI; ++i) {
+    const int row = RPI * i + lane / CPR;
+    loff[i] = (uint32_t)(row * p.s_slot) + (uint32_t)(((lane % CPR) ^ dec_swz<D>(row)) << 4);
+  }
+  const char* zero_row = reinterpret_cast<const char*>(&kDecZeroRow);
+  const int64_t head_off = (int64_t)h * p.s_head;
+  // Issue tile k of this wave into stage k % S.  Tiles whose block id is
+  // outside [0, num_blocks) read zeros (their scores are masked).
+  auto issue = [&](int k) {
+    if (k > 0 && (k & 63) == 0) {
+      // Next 64 tiles of this wave: refill the block-id prefetch.
+      const int c = wave + W * (k + lane);
+      tab = c * kChunk < end - start
+                ? (int)table_entry(p, table_row, (start + c * kChunk) / p.block_size)
+                : 0;
+    }
+    const int tb = start + (wave + W * k) * kChunk;
+    const int32_t blk = __builtin_amdgcn_readlane(tab, k & 63);
+    const uint32_t dst = lds_wave + (uint32_t)((k % S) * 2 * TILE_B);
+    if (blk >= 0 && blk < p.num_blocks) {
+      const int64_t off = (int64_t)blk * p.s_blk + (int64_t)(tb % p.block_size) * p.s_slot +
+                          head_off;
+      const char* kb = uniform_ptr(p.kp + off);
+      const char* vb = uniform_ptr(p.vp + off);
+#pragma unroll
+      for (int i = 0; i < NI; ++i) dma16_nt(loff[i], kb, dst + i * 1024);
+#pragma unroll
+      for (int i = 0; i < NI; ++i) dma16_nt(loff[i], vb, dst + TILE_B + i * 1024);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 2 * NI; ++i) dma16(zero_row, dst + i * 1024);
+    }
+  };
+
+  for (int k = 0; k < S; ++k)
+    if (k < ntw) issue(k);
+  int tab_proc = tab;
+
+  float m = kNegBig, l = 0.f;  // running max (scaled, log2) and sum of this lane's column
+  mf_f32x4 o[DT];
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) o[dt] = mf_f32x4{0.f, 0.f, 0.f, 0.f};
+  const int kswz = dec_swz<D>(r16);
+  const int vrow = 4 * c4 + (r16 >> 2);
+  const int vswz = dec_swz<D>(vrow);
+
+  for (int k = 0; k < ntw; ++k) {
+    if (k + S - 1 < ntw)
+      wait_vmcnt<2 * NI * (S - 1)>();  // tiles k + 1 .. k + S - 1 may stay in flight
+    else
+      wait_vmcnt<0>();
+    char* sK = s_wave + (k % S) * 2 * TILE_B;
+    char* sV = sK + TILE_B;
+    const int c = wave + W * k;  // partition chunk of this tile
+    const int tb = start + c * kChunk;
+    if (k > 0 && (k & 63) == 0) tab_proc = tab;
+    const int32_t blk = __builtin_amdgcn_readlane(tab_proc, k & 63);
+    const bool blk_ok = blk >= 0 && blk < p.num_blocks;
+
+    if (c == new_tile) {
+      // The current row: write it to its slot (new_slots[b], or the table
+      // slot of L - 1) and put it in place of the staged pool row.
+      int64_t slot = new_slot;
+      if (p.new_slots == nullptr)
+        slot = blk_ok ? (int64_t)blk * p.block_size + new_tok % p.block_size : -1;
+      if (slot >= 0 && slot < cap && rg == 0) {
+        const int r = new_tok - tb;
+        const int pos16 = (col ^ dec_swz<D>(r)) << 4;
+        *reinterpret_cast<uint4*>(sK + r * ROWB + pos16) = kcur;
+        *reinterpret_cast<uint4*>(sV + r * ROWB + pos16) = vcur;
+        const int64_t sb = slot / p.block_size;
+        const int64_t dst = sb * p.s_blk + (slot - sb * p.block_size) * p.s_slot + head_off +
+                            col * 16;
+        st16(p.kp + dst, kcur);
+        st16(p.vp + dst, vcur);
+      }
+    }
+
+    // S^T = K Q^T: lane holds scores of tokens tb + 4 c4 + i for head r16.
+    mf_f32x4 sacc = mf_f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < DS; ++j) {
+      const uint4 a =
+          *reinterpret_cast<const uint4*>(sK + r16 * ROWB + (((4 * j + c4) ^ kswz) << 4));
+      sacc = M::qk(a, qb[j], sacc);
+    }
+    float sv[4];
+    const int rel = blk_ok ? end - tb - 4 * c4 : 0;  // token 4 c4 + i is live iff i < rel
+#pragma unroll
+    for (int i = 0; i < 4; ++i) sv[i] = i < rel ? sacc[i] : -INFINITY;
+    float mx = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
+    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float mxs = mx * p.scale_log2;
+    if (__builtin_amdgcn_ballot_w64(mxs > m + kDecLazy) != 0) {
+      const float mnew = fmaxf(m, mxs);
+      const float alpha = fast_exp2(m - mnew);
+      m = mnew;
+      l *= alpha;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) o[dt] *= alpha;
+    }
+    float pr[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      pr[i] = fast_exp2(fmaf(sv[i], p.scale_log2, -m));
+      l += pr[i];
+    }
+    uint2 pb;
+    pb.x = M::pack2(pr[0], pr[1]);
+    pb.y = M::pack2(pr[2], pr[3]);
+
+    // O^T += V^T P^T over this tile's 16 tokens.
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+      const int off = vrow * ROWB + (((2 * dt + ((r16 >> 1) & 1)) ^ vswz) << 4) + ((r16 & 1) << 3);
+      const mf_s16x4 a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((mf_lds_s16x4*)(sV + off));
+      o[dt] = M::pv(a, pb, o[dt]);
+    }
+    // The stage is free once its LDS reads have returned.
+    wait_lgkmcnt0();
+    if (k + S < ntw) issue(k + S);
+  }
+
+  // ---- merge the waves through LDS ----
+  l += __shfl_xor(l, 16, 64);
+  l += __shfl_xor(l, 32, 64);
+  __syncthreads();  // every wave is done with its stages
+  float* s_o = reinterpret_cast<float*>(s_buf);              // [W][G][D]
+  float* s_m = s_o + W * G * D;                               // [W][G]
+  float* s_l = s_m + W * G;                                   // [W][G]
+  if (r16 < G) {
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) s_o[(wave * G + r16) * D + 16 * dt + 4 * c4 + i] = o[dt][i];
+    if (c4 == 0) {
+      s_m[wave * G + r16] = ntw > 0 ? m : kNegBig;
+      s_l[wave * G + r16] = ntw > 0 ? l : 0.f;
+    }
+  }
+  __syncthreads();
+
+  const int64_t pair = (int64_t)b * p.num_kv_heads + h;
+  for (int idx = tid; idx < G * D; idx += NT) {
+    const int g = idx / D, d = idx % D;
+    float Mx = kNegBig;
+#pragma unroll
+    for (int w = 0; w < W; ++w) Mx = fmaxf(Mx, s_m[w * G + g]);
+    float Lt = 0.f, Ot = 0.f;
+#pragma unroll
+    for (int w = 0; w < W; ++w) {
+      const float f = fast_exp2(s_m[w * G + g] - Mx);
+      Lt += s_l[w * G + g] * f;
+      Ot += s_o[(w * G + g) * D + d] * f;
+    }
+    if (nparts == 1) {
+      const float val = Lt > 0.f ? Ot / Lt : 0.f;
+      char* dst = p.out + b * p.o_sb + (int64_t)(h * G + g) * p.o_sh + d * 2;
+      float tmp[E] = {};
+      tmp[0] = val;
+      const uint4 u = ET::pack(tmp);
+      *reinterpret_cast<uint16_t*>(dst) = (uint16_t)(u.x & 0xffffu);
+    } else {
+      const int64_t slot = (pair * p.max_parts + part) * G + g;
+      p.part_o[slot * D + d] = Ot;
+      if (d == 0) {
+        p.part_ml[slot * 2] = Mx;
+        p.part_ml[slot * 2 + 1] = Lt;
+      }
+    }
+  }
+}
+
+// ------------------------------------------------------------- launching
+template <typename ET, int D, int G>
+static void launch_decode_mfma(const DecodeParams& p, dim3 grid, hipStream_t s) {
+  constexpr int NT = MfmaDecodeShape<D>::W * 64;
+  if (p.has_pro)
+    hipLaunchKernelGGL((paged_decode_mfma_kernel<ET, D, G, true>), grid, dim3(NT), 0, s, p);
+  else
+    hipLaunchKernelGGL((paged_decode_mfma_kernel<ET, D, G, false>), grid, dim3(NT), 0, s, p);
+  if (p.max_parts > 1)
+    hipLaunchKernelGGL((paged_decode_merge_kernel<ET, D, G>), dim3(grid.y, grid.x), dim3(256), 0,
+                       s, p);
+}
+
+template <typename ET, int D>
+static bool dispatch_mfma_g(int G, const DecodeParams& p, dim3 grid, hipStream_t s) {
+  switch (G) {
+    case 1: launch_decode_mfma<ET, D, 1>(p, grid, s); return true;
+    case 2: launch_decode_mfma<ET, D, 2>(p, grid, s); return true;
+    case 4: launch_decode_mfma<ET, D, 4>(p, grid, s); return true;
+    case 8: launch_decode_mfma<ET, D, 8>(p, grid, s); return true;
+    default: return false;
+  }
+}
+
+template <typename ET>
+static bool dispatch_mfma_d(int D, int G, const DecodeParams& p, dim3 grid, hipStream_t s) {
+  switch (D) {
+    case 64: return dispatch_mfma_g<ET, 64>(G, p, grid, s);
+    case 128: return dispatch_mfma_g<ET, 128>(G, p, grid, s);
+    case 256: return dispatch_mfma_g<ET, 256>(G, p, grid, s);
+    default: return false;
+  }
+}
+
+// Launch the matrix-core decode (and, when partitioned, the merge) for one
+// 16-bit element type; false for an unsupported (head_dim, group) pair.
+template <typename ET>
+bool launch_paged_decode_mfma(int D, int G, const DecodeParams& p, dim3 grid, hipStream_t s);
+
+}  // namespace va

@@ -14,7 +14,9 @@
 // (sequence, kv head, query block) and serves all G query heads of the kv
 // group, so its 128 MFMA rows are BQ = 128 / G query positions x G heads.
 // Each wave owns two 16-row tiles.  Keys stream through LDS in 64-key tiles
-// (K and V row-major, rows padded to avoid bank conflicts).  Per tile:
+// (K and V row-major, 16-byte chunks XOR-swizzled by row against bank
+// conflicts) over a ring of kStages stages filled by global_load_lds DMA, so
+// kStages - 1 tiles are in flight while one is reduced.  Per tile:
 //   S^T = K Q^T  with v_mfma_f32_16x16x32 (A = K rows from LDS via
 //                ds_read_b128, B = Q^T held in registers for the whole loop);
 //   online softmax in the exp2 domain on the S^T accumulators: each lane
@@ -89,6 +91,8 @@ struct Mma {
 constexpr int kVarlenThreads = 256;
 constexpr int kRowsPerWG = 128;
 constexpr int kKeyTile = 64;
+// Stages of the K/V ring: kStages - 1 tiles stream in while one is reduced.
+constexpr int kStages = 2;
 // MI355X hands workgroup i of a launch to XCD i % 8; each XCD has its own L2.
 constexpr int kXcds = 8;
 // Lazy-rescale slack of the online softmax, in log2 units (p <= 2^kLazy).
@@ -98,33 +102,6 @@ constexpr float kLazy = 8.0f;
 // of the visible keys or unmapped, so every tile takes the same number of
 // DMA instructions (the pipeline's vmcnt waits count them).
 __device__ __align__(16) const uint4 kZeroRow = {0u, 0u, 0u, 0u};
-
-// One 16-byte global -> LDS transfer per lane (global_load_lds_dwordx4):
-// lane l's bytes land at lds_base + 16 l.  Issued as inline asm so the
-// compiler does not wait on it before unrelated LDS reads; the kernel waits
-// for it explicitly with wait_vmcnt.
-__device__ inline void dma16(const void* src, uint32_t lds_base) {
-  asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(src), "{m0}"(lds_base) : "memory");
-}
-// The same from a wave-uniform base plus a 32-bit per-lane byte offset.
-__device__ inline void dma16(uint32_t off, const void* base, uint32_t lds_base) {
-  asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "{m0}"(lds_base)
-               : "memory");
-}
-
-__device__ inline const char* uniform_ptr(const char* ptr) {
-  const uint64_t u = (uint64_t)(uintptr_t)ptr;
-  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)u);
-  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(u >> 32));
-  return (const char*)(uintptr_t)(((uint64_t)hi << 32) | lo);
-}
-
-// s_waitcnt vmcnt(N), no wait on the other counters (gfx9 encoding).
-template <int N>
-__device__ inline void wait_vmcnt() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
-}
 
 // LDS layout of a staged K or V tile: kKeyTile rows of 2 D bytes, unpadded;
 // the 16-byte chunk c of row r sits at chunk position c ^ swz(r).  The XOR
@@ -165,9 +142,9 @@ __global__ __launch_bounds__(kVarlenThreads, 2) void varlen_attention_kernel(Var
   static_assert(NI * 4 * 1024 == TILE_B, "tile DMA split");
   using M = Mma<kBF16>;
 
-  // Two stages of (K tile, V tile): the next tile streams in while the
-  // current one is reduced.
-  __shared__ __align__(1024) char s_kv[2 * 2 * TILE_B];
+  // kStages stages of (K tile, V tile): kStages - 1 tiles stream in while
+  // the current one is reduced.
+  __shared__ __align__(1024) char s_kv[kStages * 2 * TILE_B];
 
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
@@ -315,8 +292,9 @@ __global__ __launch_bounds__(kVarlenThreads, 2) void varlen_attention_kernel(Var
     }
   };
 
-  if (ntiles > 0) issue_tile(0, 0);
-  if (ntiles > 1) issue_tile(kKeyTile, 1);
+#pragma unroll
+  for (int st = 0; st < kStages - 1; ++st)
+    if (st < ntiles) issue_tile(st * kKeyTile, st);
 
   // ---- fused store of this block's new K/V rows (kv head h) ----
   // The new rows are keys [pool_prefix + pos0, pool_prefix + pos_end), which
@@ -392,14 +370,18 @@ __global__ __launch_bounds__(kVarlenThreads, 2) void varlen_attention_kernel(Var
 
   for (int t = 0; t < ntiles; ++t) {
     const int kb = t * kKeyTile;
-    // Tile t has landed once at most the 2 NI DMAs of tile t + 1 are pending;
-    // the barrier makes every wave's part of it visible.
-    if (t + 1 < ntiles)
-      wait_vmcnt<2 * NI>();
+    // Tile t has landed once at most the 2 NI DMAs of each of tiles
+    // t + 1 .. t + kStages - 2 are pending; the barrier makes every wave's part
+    // of it visible and tells that every wave is done with tile t - 1, whose
+    // stage then takes tile t + kStages - 1.
+    if (t + kStages - 2 < ntiles)
+      wait_vmcnt<2 * NI * (kStages - 2)>();
     else
       wait_vmcnt<0>();
     __syncthreads();
-    const char* s_k = s_kv + (t & 1) * 2 * TILE_B;
+    if (t + kStages - 1 < ntiles)
+      issue_tile(kb + (kStages - 1) * kKeyTile, (t + kStages - 1) % kStages);
+    const char* s_k = s_kv + (t % kStages) * 2 * TILE_B;
     const char* s_v = s_k + TILE_B;
 
     if (fused_store && st_dst >= 0 && st_key >= kb && st_key < kb + kKeyTile) {
@@ -501,9 +483,6 @@ __global__ __launch_bounds__(kVarlenThreads, 2) void varlen_attention_kernel(Var
         o[0][dt] = M::mfma(a, pb[0][ks], o[0][dt]);
         o[1][dt] = M::mfma(a, pb[1][ks], o[1][dt]);
       }
-    // Every wave is done with stage t & 1 before tile t + 2 overwrites it.
-    __syncthreads();
-    if (t + 2 < ntiles) issue_tile(kb + 2 * kKeyTile, t & 1);
   }
 
   // ---- normalise and write: lane holds O[row r16][16 dt + 4 g4 + i] ----
