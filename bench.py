@@ -54,6 +54,14 @@ def profiled_traffic(summary: str = "paged_decode_cfg2.md") -> int | None:
     return None
 
 
+def decode_kernel_name() -> str:
+    """The decode kernel config 2 runs: the matrix-core kernel unless
+    VA_DECODE_KERNEL=general selects the general one."""
+    if os.environ.get("VA_DECODE_KERNEL") == "general":
+        return "paged_decode_kernel<BF16,128,2,aligned>"
+    return "paged_decode_mfma_kernel<BF16,128,2>"
+
+
 def timed_graph(fn, steps: int, warmup: int, stream: torch.cuda.Stream):
     """Capture fn() in a graph, replay warmup + steps times; return ms per replay.
 
@@ -474,7 +482,7 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(dec["gbs"], 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(dec["gbs"] / HBM_PEAK_GBS, 4),
                      "traffic": profiled_traffic(),
-                     "kernel": "paged_decode_kernel<BF16,128,2,true>",
+                     "kernel": decode_kernel_name(),
                      "bytes_per_launch": dec["bytes_layer"]},
         "cpu_baseline": cpu,
     }
