@@ -206,6 +206,22 @@ __device__ inline float strided_max(float x) {
 
 __device__ inline float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// The value of lane (lane ^ 16) / (lane ^ 32) through gfx950's
+// v_permlane16_swap / v_permlane32_swap (VALU, no LDS round trip).
+// permlane32_swap(a, a) leaves lanes 32..63 of its first result and lanes
+// 0..31 of its second holding the other half's values; permlane16_swap does
+// the same for the odd / even 16-lane rows of each half.
+__device__ inline float lane_xor32(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  return __uint_as_float((threadIdx.x & 32) ? r[0] : r[1]);
+}
+__device__ inline float lane_xor16(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  return __uint_as_float((threadIdx.x & 16) ? r[0] : r[1]);
+}
+
 // ------------------------------------------------------- global -> LDS DMA
 // One 16-byte global -> LDS copy per lane (global_load_lds_dwordx4): lane l's
 // bytes land at lds + 16 l.  Inline asm, so the compiler neither waits on it

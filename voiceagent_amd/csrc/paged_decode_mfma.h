@@ -352,8 +352,8 @@ __global__ __launch_bounds__(MfmaDecodeShape<D>::W * 64, 1) void paged_decode_mf
 #pragma unroll
     for (int i = 0; i < 4; ++i) sv[i] = i < rel ? sacc[i] : -INFINITY;
     float mx = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
-    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    mx = fmaxf(mx, lane_xor16(mx));
+    mx = fmaxf(mx, lane_xor32(mx));
     const float mxs = mx * p.scale_log2;
     if (__builtin_amdgcn_ballot_w64(mxs > m + kDecLazy) != 0) {
       const float mnew = fmaxf(m, mxs);
@@ -386,8 +386,8 @@ __global__ __launch_bounds__(MfmaDecodeShape<D>::W * 64, 1) void paged_decode_mf
   }
 
   // ---- merge the waves through LDS ----
-  l += __shfl_xor(l, 16, 64);
-  l += __shfl_xor(l, 32, 64);
+  l += lane_xor16(l);
+  l += lane_xor32(l);
   __syncthreads();  // every wave is done with its stages
   float* s_o = reinterpret_cast<float*>(s_buf);              // [W][G][D]
   float* s_m = s_o + W * G * D;                               // [W][G]

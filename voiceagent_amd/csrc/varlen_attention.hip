@@ -438,8 +438,8 @@ __global__ __launch_bounds__(kVarlenThreads, 2) void varlen_attention_kernel(Var
       for (int kt = 0; kt < KT; ++kt)
 #pragma unroll
         for (int i = 0; i < 4; ++i) mx = fmaxf(mx, sv[kt][i]);
-      mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      mx = fmaxf(mx, lane_xor16(mx));
+      mx = fmaxf(mx, lane_xor32(mx));
       const float mxs = mx * p.scale_log2;
       if (__builtin_amdgcn_ballot_w64(mxs > m[tt] + kLazy) != 0) {
         const float mnew = fmaxf(m[tt], mxs);
@@ -489,8 +489,8 @@ __global__ __launch_bounds__(kVarlenThreads, 2) void varlen_attention_kernel(Var
 #pragma unroll
   for (int tt = 0; tt < 2; ++tt) {
     float lt = l[tt];
-    lt += __shfl_xor(lt, 16, 64);
-    lt += __shfl_xor(lt, 32, 64);
+    lt += lane_xor16(lt);
+    lt += lane_xor32(lt);
     if (qpos[tt] >= ql) continue;
     const float inv = lt > 0.f ? 1.f / lt : 0.f;
     char* dst = p.out + (int64_t)(q0 + qpos[tt]) * p.o_st + (int64_t)qhead[tt] * p.o_sh;
