@@ -1,0 +1,120 @@
+"""The matrix-core decode path (16-bit K/V, block size a multiple of 16, no key
+mask) against the CPU oracle: block sizes, tile edges, context partitions,
+zero-length rows, unmapped blocks, the TTS page layout with the fused current-row
+write, and contexts long enough to refill a wave's block-id prefetch.
+
+Tolerance: max-abs 2e-2 for bf16/fp16 against the oracle in fp32; pools written
+by the fused store are compared bit for bit.
+"""
+
+import pytest
+import torch
+
+from oracle import attention as oracle
+from voiceagent_amd import ops
+from voiceagent_amd.agent import paged_attention_decode
+
+pytestmark = pytest.mark.gpu
+
+TOL = 2e-2
+EDGE_LENS = [1, 15, 16, 17, 31, 63, 64, 65, 130, 255, 256, 257, 700]
+
+
+def _err(out, ref):
+    return (out.float().cpu() - ref.float()).abs().max().item()
+
+
+def _nhd_case(lens, bs, dtype, hq=16, hkv=8, d=128, seed=0):
+    g = torch.Generator().manual_seed(seed)
+    need = [(n + bs - 1) // bs for n in lens]
+    nb = sum(need) + 4
+    perm = torch.randperm(nb, generator=g).tolist()
+    width = max(need)
+    rows, cur = [], 0
+    for m in need:
+        rows.append(perm[cur:cur + m] + [-1] * (width - m))
+        cur += m
+    table = torch.tensor(rows, dtype=torch.int32)
+    kp = (torch.randn(nb, bs, hkv, d, generator=g) * 0.5).to(dtype)
+    vp = (torch.randn(nb, bs, hkv, d, generator=g) * 0.5).to(dtype)
+    q = torch.randn(len(lens), hq, d, generator=g).to(dtype)
+    return q, kp, vp, table, torch.tensor(lens, dtype=torch.int32)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("bs", [16, 32, 48, 64])
+def test_block_sizes_and_tile_edges(dev, dtype, bs):
+    q, kp, vp, table, lt = _nhd_case(EDGE_LENS, bs, dtype, seed=bs)
+    out = ops.paged_decode(q.to(dev), kp.to(dev), vp.to(dev), table.to(dev), lt.to(dev),
+                           max_seq_len=max(EDGE_LENS), scale=128 ** -0.5)
+    ref = oracle.paged_decode(q, kp, vp, table, lt, 128 ** -0.5)
+    assert _err(out, ref) <= TOL
+
+
+@pytest.mark.parametrize("split", [64, 256, 512, 2048])
+def test_partitions_and_merge(dev, split):
+    lens = [1, 16, 300, 1500, 4000]
+    q, kp, vp, table, lt = _nhd_case(lens, 16, torch.bfloat16, seed=split)
+    out = ops.paged_decode(q.to(dev), kp.to(dev), vp.to(dev), table.to(dev), lt.to(dev),
+                           max_seq_len=max(lens), scale=128 ** -0.5, split_tokens=split)
+    ref = oracle.paged_decode(q, kp, vp, table, lt, 128 ** -0.5)
+    assert _err(out, ref) <= TOL
+
+
+def test_zero_length_rows_and_unmapped_blocks(dev):
+    q, kp, vp, table, _ = _nhd_case([40, 40, 40], 16, torch.bfloat16, seed=3)
+    table[1, 1] = 999999  # unmapped: its 16 tokens are masked, never read
+    table[2, 2] = -1
+    lt = torch.tensor([0, 40, 40], dtype=torch.int32)
+    out = ops.paged_decode(q.to(dev), kp.to(dev), vp.to(dev), table.to(dev), lt.to(dev),
+                           max_seq_len=40, scale=0.1).cpu()
+    assert torch.count_nonzero(out[0]) == 0
+    keep = torch.ones(3, 40, dtype=torch.bool)
+    keep[1, 16:32] = False
+    keep[2, 32:40] = False
+    safe = table.clone()
+    safe[1, 1] = 0
+    safe[2, 2] = 0
+    ref = oracle.paged_decode(q, kp, vp, safe, lt, 0.1, valid_mask=keep)
+    assert _err(out[1:], ref[1:]) <= TOL
+
+
+def test_prefetch_refill_past_64_tiles_per_wave(dev):
+    # One partition of 20000 tokens: each of the 8 waves owns ~156 tiles, so the
+    # block-id prefetch (64 tiles per refill) is refilled twice.
+    lens = [20000, 37]
+    q, kp, vp, table, lt = _nhd_case(lens, 16, torch.bfloat16, seed=21)
+    out = ops.paged_decode(q.to(dev), kp.to(dev), vp.to(dev), table.to(dev), lt.to(dev),
+                           max_seq_len=20000, scale=128 ** -0.5, split_tokens=20480)
+    ref = oracle.paged_decode(q, kp, vp, table, lt, 128 ** -0.5)
+    assert _err(out, ref) <= TOL
+
+
+@pytest.mark.parametrize("page", [16, 32])
+def test_tts_page_layout_with_fused_write(dev, page):
+    # TTS pool [pages, Hkv, page_size, D], int64 tables, no key mask: the
+    # current row is written at seq_len - 1 and attended in the same launch.
+    g = torch.Generator().manual_seed(page)
+    lens = torch.tensor([1, page, page + 1, 3 * page - 2], dtype=torch.long)
+    pages_needed = [(int(n) + page - 1) // page for n in lens]
+    P = sum(pages_needed) + 3
+    perm = torch.randperm(P, generator=g).tolist()
+    width = max(pages_needed)
+    rows, cur = [], 0
+    for m in pages_needed:
+        rows.append(perm[cur:cur + m] + [-1] * (width - m))
+        cur += m
+    table = torch.tensor(rows, dtype=torch.long)
+    kp = torch.randn(P, 8, page, 128, generator=g).to(torch.bfloat16)
+    vp = torch.randn(P, 8, page, 128, generator=g).to(torch.bfloat16)
+    q = torch.randn(4, 16, 1, 128, generator=g).to(torch.bfloat16)
+    nk = torch.randn(4, 8, 1, 128, generator=g).to(torch.bfloat16)
+    nv = torch.randn(4, 8, 1, 128, generator=g).to(torch.bfloat16)
+    ek, ev = oracle.write_current_kv(kp, vp, table, lens, nk[:, :, 0], nv[:, :, 0])
+    kd, vd = kp.to(dev), vp.to(dev)
+    out = paged_attention_decode(q.to(dev), kd, vd, table.to(dev), lens.to(dev),
+                                 new_key=nk.to(dev), new_value=nv.to(dev))
+    torch.cuda.synchronize()
+    assert torch.equal(kd.cpu(), ek) and torch.equal(vd.cpu(), ev)
+    ref = oracle.paged_decode(q[:, :, 0], ek, ev, table, lens, 128 ** -0.5, layout=oracle.HND)
+    assert _err(out[:, :, 0], ref) <= TOL
