@@ -497,25 +497,25 @@ __global__ __launch_bounds__((DecodeShape<ET, D, G>::NW * 64),
 // beyond this), which bounds the merge kernel's LDS.
 constexpr int kMaxParts = 256;
 
-// Merge of the partitions of one (sequence, kv head) pair: out = sum_q
-// 2^(m_q - M) o_q / sum_q 2^(m_q - M) l_q with M = max_q m_q.  Pairs that
-// fit one partition were written by the first kernel and are skipped.
-// Phase 1: wave w reduces (m, l) of every partition for query heads
-// g = w, w + 4, ... (lanes over partitions) into LDS weights 2^(m_q - M) and
-// 1 / sum.  Phase 2: each thread sums o_q[d] for its (g, d) in batches of
-// 32 partitions whose loads are all in flight together.  Loads use clamped
+// Merge of the partitions of one (sequence, kv head) pair: for each query head
+//   out = sum_q 2^(m_q - M) o_q / sum_q 2^(m_q - M) l_q,  M = max_q m_q.
+// Pairs that fit one partition were written by the attention kernel and are
+// skipped.  Every wave serves one query head g over 64 of its D outputs
+// (idx = (g, d) in 64-wide slices).  Lane q of the wave holds (m, l) of
+// partitions q, q + 64, ..., and the o values of the first kBatch
+// partitions are loaded by every lane for its d in the same breath, so the
+// merge costs one round trip after the length.  The weights 2^(m_q - M) reach
+// the o sums through readlane (q is wave-uniform).  Loads use clamped
 // indices and are masked afterwards, so no load sits behind a branch.
 template <typename ET, int D, int G>
 __global__ __launch_bounds__(256) void paged_decode_merge_kernel(DecodeParams p) {
   constexpr int E = ET::kPerVec;
   constexpr int kPerLane = kMaxParts / 64;
   constexpr int kBatch = 32;
-  __shared__ float s_w[kMaxParts][G];
-  __shared__ float s_inv[G];
+  static_assert(D % 64 == 0, "a wave covers 64 outputs of one query head");
   const int h = blockIdx.x;
   const int b = blockIdx.y;
   const int tid = threadIdx.x;
-  const int wave = tid >> 6;
   const int lane = tid & 63;
   int L;
   if (p.lens_cum)
@@ -527,11 +527,14 @@ __global__ __launch_bounds__(256) void paged_decode_merge_kernel(DecodeParams p)
   int nparts = (L + p.split_tokens - 1) / p.split_tokens;
   if (nparts > p.max_parts) nparts = p.max_parts;
   if (nparts <= 1) return;
-  const int64_t base = (int64_t)b * p.num_kv_heads + h;  // pair index
-  const int64_t pair_slot0 = base * p.max_parts;
+  const int64_t pair_slot0 = ((int64_t)b * p.num_kv_heads + h) * p.max_parts;
 
-  for (int g = wave; g < G; g += 4) {
-    float mq[kPerLane], lq[kPerLane];
+  for (int idx0 = tid & ~63; idx0 < G * D; idx0 += 256) {
+    const int g = idx0 / D;                // uniform per wave
+    const int d = idx0 % D + lane;
+    // (m, l) of this lane's partitions and o of the first batch, all issued
+    // before any is used.
+    float mq[kPerLane], lq[kPerLane], oq[kBatch];
 #pragma unroll
     for (int i = 0; i < kPerLane; ++i) {
       const int q = lane + 64 * i;
@@ -539,41 +542,47 @@ __global__ __launch_bounds__(256) void paged_decode_merge_kernel(DecodeParams p)
       mq[i] = p.part_ml[slot * 2];
       lq[i] = p.part_ml[slot * 2 + 1];
     }
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j) {
+      const int q = j < nparts ? j : nparts - 1;
+      oq[j] = p.part_o[((pair_slot0 + q) * G + g) * D + d];
+    }
     float M = kNegBig;
 #pragma unroll
     for (int i = 0; i < kPerLane; ++i)
       if (lane + 64 * i < nparts) M = fmaxf(M, mq[i]);
     M = group_max<64>(M);
-    float Lt = 0.f;
+    float w[kPerLane], Lt = 0.f;
 #pragma unroll
     for (int i = 0; i < kPerLane; ++i) {
-      const int q = lane + 64 * i;
-      if (q < nparts) {
-        const float w = fast_exp2(mq[i] - M);
-        s_w[q][g] = w;
-        Lt += w * lq[i];
-      }
+      w[i] = lane + 64 * i < nparts ? fast_exp2(mq[i] - M) : 0.f;
+      Lt = fmaf(w[i], lq[i], Lt);
     }
     Lt = group_sum<64>(Lt);
-    if (lane == 0) s_inv[g] = Lt > 0.f ? 1.f / Lt : 0.f;
-  }
-  __syncthreads();
-
-  for (int idx = tid; idx < G * D; idx += 256) {
-    const int g = idx / D, d = idx % D;
     float acc = 0.f;
-    for (int q0 = 0; q0 < nparts; q0 += kBatch) {
-      float oq[kBatch];
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j)
+      if (j < nparts)
+        acc = fmaf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(w[0]), j)), oq[j], acc);
+    for (int q0 = kBatch; q0 < nparts; q0 += kBatch) {
 #pragma unroll
       for (int j = 0; j < kBatch; ++j) {
         const int q = q0 + j < nparts ? q0 + j : nparts - 1;
         oq[j] = p.part_o[((pair_slot0 + q) * G + g) * D + d];
       }
 #pragma unroll
-      for (int j = 0; j < kBatch; ++j)
-        if (q0 + j < nparts) acc = fmaf(s_w[q0 + j][g], oq[j], acc);
+      for (int j = 0; j < kBatch; ++j) {
+        const int q = q0 + j;
+        if (q < nparts) {
+          float wq = 0.f;
+#pragma unroll
+          for (int i = 0; i < kPerLane; ++i)
+            if ((q >> 6) == i) wq = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w[i]), q & 63));
+          acc = fmaf(wq, oq[j], acc);
+        }
+      }
     }
-    const float val = acc * s_inv[g];
+    const float val = Lt > 0.f ? acc / Lt : 0.f;
     char* dst = p.out + b * p.o_sb + (int64_t)(h * G + g) * p.o_sh + d * ET::kBytes;
     if constexpr (ET::kBytes == 4) {
       *reinterpret_cast<float*>(dst) = val;
