@@ -183,10 +183,15 @@ def bench_prologue(args, dev, stream, dec):
                       "applied to the raw projections"}
 
 
+MAX_MODEL_LEN = 65536  # max_position_embeddings of the decoder (qwen_asr_vllm/config.py:71)
+
+
 def bench_longform(args, dev, stream):
     """Config 5: long-form decode, (i) one 16384-token context, (ii) 8 contexts
     U[4096, 16384]; 28 layers with their own pools, fused store, contexts split
-    into partitions and merged (the split the library picks by default)."""
+    into partitions and merged (the split the library picks by default).
+    Each variant also runs with max_seq_len = max_model_len, as the engine's
+    decode graph passes it (qwen_asr_vllm/engine/graph_runner.py:85-93)."""
     res = {}
     layers = workloads.LAYERS
     for variant in ("single", "batch8"):
@@ -205,24 +210,31 @@ def bench_longform(args, dev, stream):
                            device=dev) * 0.5).to(torch.bfloat16)
         outs = torch.empty_like(qs)
 
-        def step():
-            for i in range(layers):
-                ops.paged_decode(qs[i], batch.k_pools[i], batch.v_pools[i], batch.block_tables,
-                                 batch.cu_seqlens_k, lens_cumulative=True,
-                                 max_seq_len=batch.max_seq_len, scale=batch.scale,
-                                 new_k=nks[i], new_v=nvs[i], new_slots=batch.slot_mapping,
-                                 out=outs[i], split_tokens=args.split)
+        def make_step(max_seq_len):
+            def step():
+                for i in range(layers):
+                    ops.paged_decode(qs[i], batch.k_pools[i], batch.v_pools[i],
+                                     batch.block_tables, batch.cu_seqlens_k,
+                                     lens_cumulative=True, max_seq_len=max_seq_len,
+                                     scale=batch.scale, new_k=nks[i], new_v=nvs[i],
+                                     new_slots=batch.slot_mapping, out=outs[i],
+                                     split_tokens=args.split)
+            return step
 
-        ms, _ = timed_graph(step, args.steps, args.warmup, stream)
         nbytes = workloads.decode_bytes(lens) + 2 * B * workloads.HKV * workloads.HEAD_DIM * 2 \
             + 4 * B
+        ms, _ = timed_graph(make_step(batch.max_seq_len), args.steps, args.warmup, stream)
         us = ms * 1000.0 / layers
         gbs = nbytes / (us * 1e-6) / 1e9
+        ms_g, _ = timed_graph(make_step(MAX_MODEL_LEN), args.steps, args.warmup, stream)
+        us_g = ms_g * 1000.0 / layers
         log(f"[longform {variant}] B={B} ctx sum {sum(lens)}: {us:.2f} us/layer, {gbs:.0f} GB/s "
-            f"({nbytes / 1e6:.1f} MB/layer, {gbs / HBM_PEAK_GBS:.3f} of HBM peak)")
+            f"({nbytes / 1e6:.1f} MB/layer, {gbs / HBM_PEAK_GBS:.3f} of HBM peak); "
+            f"max_seq_len={MAX_MODEL_LEN}: {us_g:.2f} us/layer")
         res[variant] = {"us_per_layer": round(us, 2), "gbs": round(gbs, 1),
                         "frac": round(gbs / HBM_PEAK_GBS, 4), "bytes_per_layer": nbytes,
-                        "batch": B, "context_tokens": sum(lens)}
+                        "batch": B, "context_tokens": sum(lens),
+                        "us_per_layer_max_model_len": round(us_g, 2)}
         del batch, qs, nks, nvs, outs
         torch.cuda.empty_cache()
     return res

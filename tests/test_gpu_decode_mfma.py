@@ -118,3 +118,18 @@ def test_tts_page_layout_with_fused_write(dev, page):
     assert torch.equal(kd.cpu(), ek) and torch.equal(vd.cpu(), ev)
     ref = oracle.paged_decode(q[:, :, 0], ek, ev, table, lens, 128 ** -0.5, layout=oracle.HND)
     assert _err(out[:, :, 0], ref) <= TOL
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("max_seq_len", [4000, 65536, 100])
+def test_max_seq_len_as_upper_bound(dev, dtype, max_seq_len):
+    # A decode graph is captured with max_seqlen_k = max_model_len
+    # (qwen_asr_vllm/engine/graph_runner.py:85-93): the automatic split sizes
+    # each context's partitions from its own length, so an upper bound (or an
+    # underestimate) gives the same result as the exact maximum.
+    lens = [7, 300, 1500, 4000]
+    q, kp, vp, table, lt = _nhd_case(lens, 16, dtype, seed=max_seq_len % 97)
+    out = ops.paged_decode(q.to(dev), kp.to(dev), vp.to(dev), table.to(dev), lt.to(dev),
+                           max_seq_len=max_seq_len, scale=128 ** -0.5)
+    ref = oracle.paged_decode(q, kp, vp, table, lt, 128 ** -0.5)
+    assert _err(out, ref) <= (TOL if dtype != torch.float32 else 1e-5)

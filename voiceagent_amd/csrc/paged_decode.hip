@@ -16,6 +16,7 @@ namespace va {
 struct DecodePlan {
   int split_tokens;
   int max_parts;
+  int dyn_split;
   size_t ml_bytes, o_bytes, total_bytes;
 };
 
@@ -99,11 +100,26 @@ static DecodePlan plan_decode(const va_decode_args* a) {
   if (P <= 0) {
     // Split contexts only as far as needed to give every CU one workgroup:
     // with at least as many (sequence, kv head) pairs as CUs, one partition
-    // per pair.  Partitions are at least one round of in-flight chunks.
+    // per pair.  Otherwise every context gets up to `want` partitions whose
+    // size each workgroup derives from its own context length
+    // (partition_tokens), so a max_seq_len that is only an upper bound (a
+    // decode graph captured at max_model_len) still spreads short contexts.
     const int64_t cus = current_device_cus();
     const int64_t want = pairs >= cus ? 1 : cus / (pairs > 0 ? pairs : 1);
-    P = (int)((max_len + want - 1) / want);
-    if (P < unit) P = unit;
+    int64_t parts = want;
+    const int64_t by_len = (max_len + kDynGrain - 1) / kDynGrain;
+    if (parts > by_len) parts = by_len;
+    if (parts > kMaxParts) parts = kMaxParts;
+    if (parts > 1) {
+      pl.dyn_split = 1;
+      pl.split_tokens = kDynGrain;
+      pl.max_parts = (int)parts;
+      pl.ml_bytes = ((size_t)pairs * pl.max_parts * G * 2 * 4 + 255) / 256 * 256;
+      pl.o_bytes = (size_t)pairs * pl.max_parts * G * a->head_dim * 4;
+      pl.total_bytes = pl.ml_bytes + pl.o_bytes;
+      return pl;
+    }
+    P = max_len;
   }
   // Any split (automatic or requested) keeps at most kMaxParts partitions.
   const int cap = (max_len + kMaxParts - 1) / kMaxParts;
@@ -259,6 +275,7 @@ extern "C" int va_paged_decode(const va_decode_args* a, void* stream) {
   p.num_kv_heads = a->num_kv_heads;
   p.split_tokens = pl.split_tokens;
   p.max_parts = pl.max_parts;
+  p.dyn_split = pl.dyn_split;
   p.scale_log2 = a->scale * 1.4426950408889634f;
   p.has_pro = a->prologue != nullptr;
   p.pro = PrologueParams{};

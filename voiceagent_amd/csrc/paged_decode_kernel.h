@@ -67,6 +67,7 @@ struct DecodeParams {
   int32_t num_kv_heads;
   int32_t split_tokens;
   int32_t max_parts;
+  int32_t dyn_split;  // partition size from each context's length (see partition_tokens)
   float scale_log2;
   float* part_ml;
   float* part_o;
@@ -82,6 +83,19 @@ __device__ inline int64_t table_entry(const DecodeParams& p, int64_t row, int id
   return idx < p.table_width ? load_index(p.table, row + idx, p.table_i64) : 0;
 }
 constexpr float kNegBig = -1.0e30f;
+
+// Tokens per context partition.  Fixed (split_tokens), or with dyn_split
+// derived on the device from the context length L, so that the max_parts
+// partitions of a pair share its context evenly in multiples of kDynGrain
+// tokens.  The dynamic form serves launches whose max_seq_len is only an
+// upper bound, such as a decode graph captured at max_model_len.
+constexpr int kDynGrain = 64;
+__device__ inline int partition_tokens(const DecodeParams& p, int L) {
+  if (!p.dyn_split) return p.split_tokens;
+  int P = (L + p.max_parts - 1) / p.max_parts;
+  P = (P + kDynGrain - 1) / kDynGrain * kDynGrain;
+  return P > kDynGrain ? P : kDynGrain;
+}
 
 __device__ inline float uniform(float x) {
   return __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(x)));
@@ -131,8 +145,8 @@ __global__ __launch_bounds__((DecodeShape<ET, D, G>::NW * 64),
   const int lane = tid & 63;
   const int rg = lane / LPR;
   const int col = lane % LPR;
-  const int P = p.split_tokens;
-  const int start = part * P;
+  int P = p.split_tokens;  // placeholder in dyn_split mode, fixed below from L
+  int start = part * P;
   const int64_t table_row = (int64_t)b * p.t_sb;
 
   // Independent loads first, none depending on another: the context length,
@@ -182,6 +196,16 @@ __global__ __launch_bounds__((DecodeShape<ET, D, G>::NW * 64),
       }
     }
     return;
+  }
+  if (p.dyn_split) {
+    // The partition follows from L: re-read this wave's block ids for it.
+    P = partition_tokens(p, L);
+    start = part * P;
+    if (kAligned && start < L) {
+      const int c = wave + NW * lane;
+      tab = c * kChunk < P ? (int)table_entry(p, table_row, (start + c * kChunk) / p.block_size)
+                           : 0;
+    }
   }
   if (start >= L) return;
   int nparts = (L + P - 1) / P;
@@ -524,7 +548,8 @@ __global__ __launch_bounds__(256) void paged_decode_merge_kernel(DecodeParams p)
     L = (int)load_index(p.lens, b, p.lens_i64);
   L = __builtin_amdgcn_readfirstlane(L);
   if (L <= 0) return;
-  int nparts = (L + p.split_tokens - 1) / p.split_tokens;
+  const int P = partition_tokens(p, L);
+  int nparts = (L + P - 1) / P;
   if (nparts > p.max_parts) nparts = p.max_parts;
   if (nparts <= 1) return;
   const int64_t pair_slot0 = ((int64_t)b * p.num_kv_heads + h) * p.max_parts;

@@ -147,8 +147,8 @@ __global__ __launch_bounds__(MfmaDecodeShape<D>::W * 64, 1) void paged_decode_mf
   const int c4 = lane >> 4;    // MFMA k-group of this lane
   const int rg = lane / LPR;   // row-layout row of this lane
   const int col = lane % LPR;  // row-layout 16-byte column of this lane
-  const int P = p.split_tokens;
-  const int start = part * P;
+  int P = p.split_tokens;  // placeholder in dyn_split mode, fixed below from L
+  int start = part * P;
   const int64_t table_row = (int64_t)b * p.t_sb;
 
   // ---- independent loads: length, this wave's block ids, the query rows,
@@ -203,6 +203,16 @@ __global__ __launch_bounds__(MfmaDecodeShape<D>::W * 64, 1) void paged_decode_mf
       }
     }
     return;
+  }
+  if (p.dyn_split) {
+    // The partition follows from L: re-read this wave's block ids for it.
+    P = partition_tokens(p, L);
+    start = part * P;
+    if (start < L) {
+      const int c = wave + W * lane;
+      tab = c * kChunk < P ? (int)table_entry(p, table_row, (start + c * kChunk) / p.block_size)
+                           : 0;
+    }
   }
   if (start >= L) return;
   int nparts = (L + P - 1) / P;
