@@ -1,5 +1,6 @@
 // Error channel and version query of the C ABI.
 #include <stdarg.h>
+#include <atomic>
 #include <stdio.h>
 
 #include "common.h"
@@ -22,6 +23,30 @@ int check_launch(const char* what) {
     return VA_ERR_LAUNCH;
   }
   return VA_OK;
+}
+
+// Compute units of the current device (cached per device; 256, the MI355X
+// count, when no device is visible, e.g. when only the workspace size is
+// queried on a host without a GPU).
+int current_device_cus() {
+  static std::atomic<int> cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0) {
+    (void)hipGetLastError();
+    return 256;
+  }
+  if (dev < 64) {
+    const int v = cache[dev].load(std::memory_order_relaxed);
+    if (v > 0) return v;
+  }
+  int n = 0;
+  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      n <= 0) {
+    (void)hipGetLastError();
+    n = 256;
+  }
+  if (dev < 64) cache[dev].store(n, std::memory_order_relaxed);
+  return n;
 }
 
 }  // namespace va

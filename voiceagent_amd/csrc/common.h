@@ -23,6 +23,10 @@ void set_error(const char* fmt, ...);
 
 int check_launch(const char* what);
 
+// Compute units of the current device (cached per device; 256, the MI355X
+// count, when no device is visible).
+int current_device_cus();
+
 // ------------------------------------------------------------ element types
 // Each type describes how 16 bytes (one dwordx4 lane load) unpack to floats
 // and how floats pack back.  bf16 -> f32 is exact (bit shift); f32 -> bf16

@@ -1,7 +1,6 @@
 // Host side of the paged decode: argument checks, the context split and
 // launch dispatch (kernels in paged_decode_kernel.h and paged_decode_mfma.h,
 // instantiated per element type in paged_decode_{bf16,f16,f32}.hip).
-#include <atomic>
 #include <cstdlib>
 #include <cstring>
 
@@ -62,30 +61,6 @@ static int mfma_unit_for(int D) {
     case 256: return mfma_decode_unit<256>();
     default: return 0;
   }
-}
-
-// Compute units of the current device (cached per device; 256, the MI355X
-// count, when no device is visible, e.g. when only the workspace size is
-// queried on a host without a GPU).
-static int current_device_cus() {
-  static std::atomic<int> cache[64];
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0) {
-    (void)hipGetLastError();
-    return 256;
-  }
-  if (dev < 64) {
-    const int v = cache[dev].load(std::memory_order_relaxed);
-    if (v > 0) return v;
-  }
-  int n = 0;
-  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-      n <= 0) {
-    (void)hipGetLastError();
-    n = 256;
-  }
-  if (dev < 64) cache[dev].store(n, std::memory_order_relaxed);
-  return n;
 }
 
 static DecodePlan plan_decode(const va_decode_args* a) {

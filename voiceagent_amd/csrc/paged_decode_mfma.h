@@ -6,9 +6,10 @@
 // the grid is (sequence, kv head, partition); a workgroup owns P consecutive
 // tokens of one (sequence, kv head) pair and all G query heads of its group.
 //
-// Work decomposition.  A workgroup is W = 4 wave64s (one per SIMD).  The
-// partition's 16-token tiles go round robin to the waves (tile c to wave
-// c % W), and each wave runs its own pipeline with no workgroup barrier:
+// Work decomposition.  A workgroup is W wave64s (8, two per SIMD, for head
+// dims up to 128; 4 for 256).  The partition's 16-token tiles go round robin
+// to the waves (tile c to wave c % W), and each wave runs its own pipeline
+// with no workgroup barrier:
 //   * the K and V rows of a tile (16 rows of one block) are copied from HBM
 //     straight into the wave's LDS ring of S stages with
 //     global_load_lds_dwordx4 (1 KiB per instruction, 16-byte chunks stored
@@ -23,9 +24,11 @@
 //   * O^T += V^T P^T with v_mfma_f32_16x16x16: P^T is the S^T accumulator
 //     packed to 16 bits in place (its layout is already the B operand's),
 //     V^T comes from the row-major V tile through ds_read_b64_tr_b16.
-// Nearly all arithmetic runs on the matrix cores, so one wave per SIMD keeps
+// Nearly all arithmetic runs on the matrix cores, so two waves per SIMD keep
 // HBM busy and a workgroup can pull several times its fair share of
-// bandwidth once shorter contexts have finished.  The waves merge through
+// bandwidth once shorter contexts have finished.  With one partition per
+// pair the first tiles are requested before the context length has
+// arrived (see `early` below).  The waves merge through
 // LDS at the end; partitioned contexts write (m, l, o) partials that
 // paged_decode_merge_kernel combines.
 #pragma once
@@ -151,36 +154,59 @@ __global__ __launch_bounds__(MfmaDecodeShape<D>::W * 64, 1) void paged_decode_mf
   int start = part * P;
   const int64_t table_row = (int64_t)b * p.t_sb;
 
-  // ---- independent loads: length, this wave's block ids, the query rows,
-  // the current K/V row and its slot, the prologue inputs ----
-  int L;
-  if (p.lens_cum)
-    L = (int)(load_index(p.lens, b + 1, p.lens_i64) - load_index(p.lens, b, p.lens_i64));
-  else
-    L = (int)load_index(p.lens, b, p.lens_i64);
+  // ---- independent loads, all issued before the first wait: this wave's
+  // block ids, the query, the current K/V row, the length and the slot.
+  // Index arrays are read as raw 32-bit words (the low word of an int64
+  // entry) and combined only after the last load is issued, so that no load
+  // waits behind another one's arithmetic. ----
   // Block of the wave's tile `lane` (tile 64 i + lane after refills): `tab`
   // serves the DMA issue, which runs S tiles ahead; `tab_proc` is the copy
   // the tile being reduced reads (refreshed when it reaches the refill).
+  const uint32_t* const tabw = reinterpret_cast<const uint32_t*>(p.table);
+  auto block_of = [&](int tok) -> int {  // table entry of token tok's block, 0 past the width
+    const int idx = tok / p.block_size;
+    return idx < p.table_width ? (int)tabw[(table_row + idx) << p.table_i64] : 0;
+  };
   int tab = 0;
   {
     const int c = wave + W * lane;
-    if (c * kChunk < P || part == p.max_parts - 1)
-      tab = (int)table_entry(p, table_row, (start + c * kChunk) / p.block_size);
+    if (c * kChunk < P || part == p.max_parts - 1) tab = block_of(start + c * kChunk);
   }
+  // The query: in the B-operand layout of S^T = K Q^T (lane holds
+  // q[head r16][32 j + 8 c4, +8)), or, for the prologue, as rows in the row
+  // layout, which go through LDS into the B layout after normalisation.
+  uint4 qb[DS];
   uint4 qrow[QROWS];
+  if constexpr (!kProlog) {
 #pragma unroll
-  for (int k = 0; k < QROWS; ++k) {
-    const int g = rg + RPL * k;
-    qrow[k] = g < G ? ld16(p.q + b * p.q_sb + (int64_t)(h * G + g) * p.q_sh + col * 16)
-                    : make_uint4(0, 0, 0, 0);
+    for (int j = 0; j < DS; ++j)
+      qb[j] = r16 < G ? ld16(p.q + b * p.q_sb + (int64_t)(h * G + r16) * p.q_sh +
+                             (32 * j + 8 * c4) * 2)
+                      : make_uint4(0, 0, 0, 0);
+  } else {
+#pragma unroll
+    for (int k = 0; k < QROWS; ++k) {
+      const int g = rg + RPL * k;
+      qrow[k] = g < G ? ld16(p.q + b * p.q_sb + (int64_t)(h * G + g) * p.q_sh + col * 16)
+                      : make_uint4(0, 0, 0, 0);
+    }
   }
   uint4 kcur = make_uint4(0, 0, 0, 0), vcur = make_uint4(0, 0, 0, 0);
   if (p.new_k != nullptr) {
     kcur = ld16(p.new_k + b * p.nk_sb + h * p.nk_sh + col * 16);
     vcur = ld16(p.new_v + b * p.nv_sb + h * p.nv_sh + col * 16);
   }
-  int64_t new_slot = -1;
-  if (p.new_slots != nullptr) new_slot = load_index(p.new_slots, b, p.new_slots_i64);
+  // Length: lens[b] or cu[b + 1] - cu[b]; only the low words matter for a
+  // 32-bit length.
+  const uint32_t* const lensw = reinterpret_cast<const uint32_t*>(p.lens);
+  const uint32_t len_hi = lensw[(int64_t)(b + p.lens_cum) << p.lens_i64];
+  const uint32_t len_lo = lensw[(int64_t)b << p.lens_i64];
+  uint32_t slot_lo = ~0u, slot_hi = ~0u;  // new_slots[b] (-1 without one)
+  if (p.new_slots != nullptr) {
+    const uint32_t* const sw = reinterpret_cast<const uint32_t*>(p.new_slots);
+    slot_lo = sw[(int64_t)b << p.new_slots_i64];
+    slot_hi = sw[((int64_t)b << p.new_slots_i64) + p.new_slots_i64];
+  }
   float pro_c[E], pro_s[E];
   WeightRaw<E> pro_wq{}, pro_wk{};
   int64_t pos = 0;
@@ -192,9 +218,73 @@ __global__ __launch_bounds__(MfmaDecodeShape<D>::W * 64, 1) void paged_decode_mf
                                  col * E);
     load_rotary<E, LPR>(p.pro, pos, col, D, pro_c, pro_s);
   }
+
+  char* const s_wave = s_buf + wave * Sh::WAVE_B;
+  const uint32_t lds_wave = __builtin_amdgcn_readfirstlane(
+      (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)s_wave);
+
+  // ---- tile DMA: instruction i of a tile moves rows RPI i .. RPI i + RPI - 1;
+  // lane l writes row RPI i + l / CPR at chunk position l % CPR, i.e. reads
+  // logical chunk (l % CPR) ^ swz(row) of that row ----
+  uint32_t loff[NI];
+#pragma unroll
+  for (int i = 0; i < NI; ++i) {
+    const int row = RPI * i + lane / CPR;
+    loff[i] = (uint32_t)(row * p.s_slot) + (uint32_t)(((lane % CPR) ^ dec_swz<D>(row)) << 4);
+  }
+  const char* zero_row = reinterpret_cast<const char*>(&kDecZeroRow);
+  const int64_t head_off = (int64_t)h * p.s_head;
+  int span = 0;  // tokens of this partition (set once the length is known)
+  // Issue tile k of this wave into stage k % S.  Tiles whose block id is
+  // outside [0, num_blocks) read zeros (their scores are masked).
+  auto issue = [&](int k) {
+    if (k > 0 && (k & 63) == 0) {
+      // Next 64 tiles of this wave: refill the block-id prefetch.
+      const int c = wave + W * (k + lane);
+      tab = c * kChunk < span ? block_of(start + c * kChunk) : 0;
+    }
+    const int tb = start + (wave + W * k) * kChunk;
+    const int32_t blk = __builtin_amdgcn_readlane(tab, k & 63);
+    const uint32_t dst = lds_wave + (uint32_t)((k % S) * 2 * TILE_B);
+    if (blk >= 0 && blk < p.num_blocks) {
+      const int64_t off = (int64_t)blk * p.s_blk + (int64_t)(tb % p.block_size) * p.s_slot +
+                          head_off;
+      const char* kb = uniform_ptr(p.kp + off);
+      const char* vb = uniform_ptr(p.vp + off);
+#pragma unroll
+      for (int i = 0; i < NI; ++i) dma16_nt(loff[i], kb, dst + i * 1024);
+#pragma unroll
+      for (int i = 0; i < NI; ++i) dma16_nt(loff[i], vb, dst + TILE_B + i * 1024);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 2 * NI; ++i) dma16(zero_row, dst + i * 1024);
+    }
+  };
+
+  // With one partition per pair (start 0, the common decode batch) the first
+  // S tiles are issued now, before the length is known: a block id outside
+  // [0, num_blocks) reads zeros and tokens past the context are masked, so the
+  // early tiles are safe to fetch, and the length's round trip leaves the
+  // critical path.  The vector loads above are waited for first, so the
+  // compiler's own waits for them do not fall after the DMA (where they
+  // would also wait for it).
+  const bool early = !kProlog && p.max_parts == 1;
+  if (early) {
+#pragma unroll
+    for (int j = 0; j < DS; ++j)
+      asm volatile("" ::"v"(qb[j].x), "v"(qb[j].y), "v"(qb[j].z), "v"(qb[j].w));
+    asm volatile("" ::"v"(kcur.x), "v"(kcur.y), "v"(kcur.z), "v"(kcur.w), "v"(vcur.x),
+                 "v"(vcur.y), "v"(vcur.z), "v"(vcur.w), "v"(tab));
+    for (int k = 0; k < S; ++k) issue(k);
+  }
+
+  int L = (int)(p.lens_cum ? len_hi - len_lo : len_lo);
   L = __builtin_amdgcn_readfirstlane(L);
+  const int64_t new_slot = p.new_slots_i64 ? (int64_t)(((uint64_t)slot_hi << 32) | slot_lo)
+                                           : (int64_t)(int32_t)slot_lo;
 
   if (L <= 0) {
+    wait_vmcnt<0>();  // early tiles land before the workgroup's LDS is released
     // Nothing to attend: the output is defined as 0.
     if (part == 0) {
       for (int idx = tid; idx < G * D / E; idx += NT) {
@@ -210,15 +300,18 @@ __global__ __launch_bounds__(MfmaDecodeShape<D>::W * 64, 1) void paged_decode_mf
     start = part * P;
     if (start < L) {
       const int c = wave + W * lane;
-      tab = c * kChunk < P ? (int)table_entry(p, table_row, (start + c * kChunk) / p.block_size)
-                           : 0;
+      tab = c * kChunk < P ? block_of(start + c * kChunk) : 0;
     }
   }
-  if (start >= L) return;
+  if (start >= L) {
+    wait_vmcnt<0>();
+    return;
+  }
   int nparts = (L + P - 1) / P;
   const bool last_grid_part = part == p.max_parts - 1;
   if (nparts > p.max_parts) nparts = p.max_parts;  // the last partition absorbs the rest
   const int end = last_grid_part ? L : min(start + P, L);
+  span = end - start;
   const int nch = (end - start + kChunk - 1) / kChunk;
   const int ntw = nch > wave ? (nch - wave + W - 1) / W : 0;  // tiles of this wave
 
@@ -227,10 +320,6 @@ __global__ __launch_bounds__(MfmaDecodeShape<D>::W * 64, 1) void paged_decode_mf
   const int new_tok = (p.new_k != nullptr && L - 1 >= start && L - 1 < end) ? L - 1 : -1;
   const int new_tile = new_tok >= 0 ? (new_tok - start) / kChunk : -1;  // partition chunk
   const int64_t cap = (int64_t)p.num_blocks * p.block_size;
-
-  char* const s_wave = s_buf + wave * Sh::WAVE_B;
-  const uint32_t lds_wave = __builtin_amdgcn_readfirstlane(
-      (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)s_wave);
 
   // ---- prologue (Qwen3 q/k RMSNorm + RoPE) in the row layout, then the
   // query rows go through LDS into the B-operand layout ----
@@ -252,61 +341,22 @@ __global__ __launch_bounds__(MfmaDecodeShape<D>::W * 64, 1) void paged_decode_mf
       qk_prologue<ET, LPR, E>(x, w, p.pro.eps, D, pro_c, pro_s, first_half);
       kcur = ET::pack(x);
     }
-  }
 #pragma unroll
-  for (int k = 0; k < QROWS; ++k) {
-    const int g = rg + RPL * k;
-    if (g < G) st16(s_wave + g * ROWB + col * 16, qrow[k]);
-  }
-  uint4 qb[DS];  // Q^T: lane holds q[head r16][32 j + 8 c4, +8)
-#pragma unroll
-  for (int j = 0; j < DS; ++j)
-    qb[j] = r16 < G ? *reinterpret_cast<const uint4*>(s_wave + r16 * ROWB + (4 * j + c4) * 16)
-                    : make_uint4(0, 0, 0, 0);
-  // Every wave has its q before any DMA may overwrite the scratch rows.
-  wait_lgkmcnt0();
-
-  // ---- tile DMA: instruction i of a tile moves rows RPI i .. RPI i + RPI - 1;
-  // lane l writes row RPI i + l / CPR at chunk position l % CPR, i.e. reads
-  // logical chunk (l % CPR) ^ swz(row) of that row ----
-  uint32_t loff[NI];
-#pragma unroll
-  for (int i = 0; i < NI; ++i) {
-    const int row = RPI * i + lane / CPR;
-    loff[i] = (uint32_t)(row * p.s_slot) + (uint32_t)(((lane % CPR) ^ dec_swz<D>(row)) << 4);
-  }
-  const char* zero_row = reinterpret_cast<const char*>(&kDecZeroRow);
-  const int64_t head_off = (int64_t)h * p.s_head;
-  // Issue tile k of this wave into stage k % S.  Tiles whose block id is
-  // outside [0, num_blocks) read zeros (their scores are masked).
-  auto issue = [&](int k) {
-    if (k > 0 && (k & 63) == 0) {
-      // Next 64 tiles of this wave: refill the block-id prefetch.
-      const int c = wave + W * (k + lane);
-      tab = c * kChunk < end - start
-                ? (int)table_entry(p, table_row, (start + c * kChunk) / p.block_size)
-                : 0;
+    for (int k = 0; k < QROWS; ++k) {
+      const int g = rg + RPL * k;
+      if (g < G) st16(s_wave + g * ROWB + col * 16, qrow[k]);
     }
-    const int tb = start + (wave + W * k) * kChunk;
-    const int32_t blk = __builtin_amdgcn_readlane(tab, k & 63);
-    const uint32_t dst = lds_wave + (uint32_t)((k % S) * 2 * TILE_B);
-    if (blk >= 0 && blk < p.num_blocks) {
-      const int64_t off = (int64_t)blk * p.s_blk + (int64_t)(tb % p.block_size) * p.s_slot +
-                          head_off;
-      const char* kb = uniform_ptr(p.kp + off);
-      const char* vb = uniform_ptr(p.vp + off);
 #pragma unroll
-      for (int i = 0; i < NI; ++i) dma16_nt(loff[i], kb, dst + i * 1024);
-#pragma unroll
-      for (int i = 0; i < NI; ++i) dma16_nt(loff[i], vb, dst + TILE_B + i * 1024);
-    } else {
-#pragma unroll
-      for (int i = 0; i < 2 * NI; ++i) dma16(zero_row, dst + i * 1024);
-    }
-  };
+    for (int j = 0; j < DS; ++j)
+      qb[j] = r16 < G ? *reinterpret_cast<const uint4*>(s_wave + r16 * ROWB + (4 * j + c4) * 16)
+                      : make_uint4(0, 0, 0, 0);
+    // Every wave has its q before any DMA may overwrite the scratch rows.
+    wait_lgkmcnt0();
+  }
 
-  for (int k = 0; k < S; ++k)
-    if (k < ntw) issue(k);
+  if (!early)
+    for (int k = 0; k < S; ++k)
+      if (k < ntw) issue(k);
   int tab_proc = tab;
 
   float m = kNegBig, l = 0.f;  // running max (scaled, log2) and sum of this lane's column
@@ -396,6 +446,9 @@ __global__ __launch_bounds__(MfmaDecodeShape<D>::W * 64, 1) void paged_decode_mf
   }
 
   // ---- merge the waves through LDS ----
+  // A wave with fewer tiles than the early issue fetched still has them in
+  // flight: they land before the merge reuses the LDS.
+  wait_vmcnt<0>();
   l += lane_xor16(l);
   l += lane_xor32(l);
   __syncthreads();  // every wave is done with its stages

@@ -10,13 +10,15 @@
 // (0 when none is visible).  The non-causal case with cu_q = cu_k is the
 // block-diagonal mask of reference/modeling_qwen3_asr.py:649-667.
 //
-// Tiling (one workgroup = 4 wave64 = 256 lanes): a workgroup owns one
-// (sequence, kv head, query block) and serves all G query heads of the kv
-// group, so its 128 MFMA rows are BQ = 128 / G query positions x G heads.
-// Each wave owns two 16-row tiles.  Keys stream through LDS in 64-key tiles
-// (K and V row-major, 16-byte chunks XOR-swizzled by row against bank
-// conflicts) over a ring of kStages stages filled by global_load_lds DMA, so
-// kStages - 1 tiles are in flight while one is reduced.  Per tile:
+// Tiling (one workgroup = 4 wave64 = 256 lanes): an item is one
+// (sequence, kv head, query block) with all G query heads of the kv group,
+// so its 128 MFMA rows are BQ = 128 / G query positions x G heads.  Each wave
+// owns two 16-row tiles.  Workgroups are persistent: the grid fills the
+// GPU's workgroup slots once and each workgroup works through a list of
+// items.  Keys stream through LDS in 64-key tiles (K and V row-major,
+// 16-byte chunks XOR-swizzled by row against bank conflicts) over a ring of
+// two stages filled by global_load_lds DMA, so one tile is in flight while
+// one is reduced; the ring runs on from one item into the next.  Per tile:
 //   S^T = K Q^T  with v_mfma_f32_16x16x32 (A = K rows from LDS via
 //                ds_read_b128, B = Q^T held in registers for the whole loop);
 //   online softmax in the exp2 domain on the S^T accumulators: each lane
@@ -27,7 +29,7 @@
 //                and V^T comes from row-major V through ds_read_b64_tr_b16.
 // With a paged pool, keys j < k_len - q_len are gathered through the block
 // table while the tile is loaded; the new keys come from k/v.  The fused
-// store copies this workgroup's new K/V rows to slot_mapping before the loop.
+// store copies an item's new K/V rows from the staged tiles to slot_mapping.
 #include "common.h"
 
 namespace va {
@@ -91,7 +93,7 @@ struct Mma {
 constexpr int kVarlenThreads = 256;
 constexpr int kRowsPerWG = 128;
 constexpr int kKeyTile = 64;
-// Stages of the K/V ring: kStages - 1 tiles stream in while one is reduced.
+// Stages of the K/V ring: one tile streams in while one is reduced.
 constexpr int kStages = 2;
 // MI355X hands workgroup i of a launch to XCD i % 8; each XCD has its own L2.
 constexpr int kXcds = 8;
@@ -142,8 +144,9 @@ __global__ __launch_bounds__(kVarlenThreads, 2) void varlen_attention_kernel(Var
   static_assert(NI * 4 * 1024 == TILE_B, "tile DMA split");
   using M = Mma<kBF16>;
 
-  // kStages stages of (K tile, V tile): kStages - 1 tiles stream in while
-  // the current one is reduced.
+  // Two stages of (K tile, V tile): one streams in while the other is
+  // reduced.
+  static_assert(kStages == 2, "the tile loop alternates two stages");
   __shared__ __align__(1024) char s_kv[kStages * 2 * TILE_B];
 
   const int tid = threadIdx.x;
@@ -152,85 +155,130 @@ __global__ __launch_bounds__(kVarlenThreads, 2) void varlen_attention_kernel(Var
   const int r16 = lane & 15;
   const int g4 = lane >> 4;
 
-  // XCD-aware schedule: the query blocks of one (sequence, kv head) pair all
-  // go to one XCD, whose L2 then serves the K/V rows they share.  XCD x owns
-  // pairs x, x + 8, ... and works through a list of their live query blocks
-  // (blocks past a sequence's end are left out, so no slot is spent on
-  // them); workgroup 8 i + x takes item i of that list, and items past its
-  // end exit.  With at most 64 pairs per XCD, lane k of every wave reads
-  // pair k's lengths and the list is formed with wave ballots; otherwise
-  // the list holds every (pair, block) and dead blocks exit on arrival.
+  // ---- persistent schedule ----
+  // Workgroup 8 j + x runs on XCD x (MI355X hands workgroup i of a launch to
+  // XCD i % 8, and each XCD has its own L2) and takes items from XCD x's
+  // list: the query blocks of pairs x, x + 8, ... (pair = sequence *
+  // num_kv_heads + kv head), so the blocks that share a pair's K/V rows
+  // share one L2.  The list is level-major: every pair's last block, then
+  // every pair's second to last, ... (late blocks are the heavy ones under
+  // causal masking).  It is dealt to the XCD's nslots workgroups in snake
+  // order: in round r workgroup j takes item r nslots + j when r is even and
+  // r nslots + nslots - 1 - j when r is odd, which evens out the sums of a
+  // list sorted heavy first.  A workgroup keeps its K/V ring running from
+  // one item into the next: the next item's first tile, query rows and store
+  // slots are loading while the current item's last tile is reduced.
   const int nqb = p.num_qblocks;
   const int npairs = p.num_seqs * p.num_kv_heads;
   const int xcd = (int)blockIdx.x % kXcds;
-  const int local = (int)blockIdx.x / kXcds;
+  const int wslot = (int)blockIdx.x / kXcds;
+  const int nslots = (int)gridDim.x / kXcds;
   const int ppx = (npairs - xcd + kXcds - 1) / kXcds;  // pairs on this XCD
-  int s, h, qb, q0, ql, k0, kl;
-  if (ppx <= 64) {
-    int nq = 0, lq0 = 0, lql = 0, lk0 = 0, lkl = 0;
+  // With at most 64 pairs per XCD (lane_pairs), lane k holds pair k's
+  // query and key ranges and the list is walked with wave ballots, no memory
+  // access per item.  Otherwise the list holds every (pair, block), blocks
+  // past a sequence's end are skipped, and lane k holds the ranges of this
+  // workgroup's item 64 i + k (refilled every 64 items).
+  const bool lane_pairs = ppx <= 64;
+  int lq0 = 0, lql = 0, lk0 = 0, lkl = 0, lnq = 0, lpair = 0;
+  auto load_ranges = [&](int pair) {
+    const int ls = pair / p.num_kv_heads;
+    lq0 = p.cu_q[ls];
+    lql = p.cu_q[ls + 1] - lq0;
+    lk0 = p.cu_k[ls];
+    lkl = p.cu_k[ls + 1] - lk0;
+  };
+  const int64_t total = (int64_t)ppx * nqb;  // list length without lane_pairs
+  auto item_index = [&](int r) -> int64_t {  // list index of this workgroup's round r
+    return (int64_t)r * nslots + ((r & 1) ? nslots - 1 - wslot : wslot);
+  };
+  auto refill = [&](int r0) {
+    const int64_t li = item_index(r0 + lane);
+    lnq = -1;
+    if (li < total) {
+      lpair = xcd + kXcds * (int)(li % ppx);
+      lnq = nqb - 1 - (int)(li / ppx);  // the item's query block
+      load_ranges(lpair);
+    }
+  };
+  if (lane_pairs) {
     if (lane < ppx) {
-      const int ls = (xcd + kXcds * lane) / p.num_kv_heads;
-      lq0 = p.cu_q[ls];
-      lql = p.cu_q[ls + 1] - lq0;
-      lk0 = p.cu_k[ls];
-      lkl = p.cu_k[ls + 1] - lk0;
-      nq = (lql + BQ - 1) / BQ;
+      load_ranges(xcd + kXcds * lane);
+      lnq = (lql + BQ - 1) / BQ;
     }
-    int ksel;
-    // Level-major: every pair's last block, then every pair's second to
-    // last, ... (late blocks are the heavy ones under causal masking).
-    int rem = local;
-    ksel = -1;
-    qb = -1;
-    for (int lev = nqb - 1; lev >= 0; --lev) {
-      const uint64_t live = __builtin_amdgcn_ballot_w64(nq > lev);
-      const int cnt = __popcll(live);
-      if (rem < cnt) {
-        const int below = __builtin_amdgcn_mbcnt_hi((uint32_t)(live >> 32),
-                                                     __builtin_amdgcn_mbcnt_lo((uint32_t)live, 0));
-        ksel = __builtin_ctzll(__builtin_amdgcn_ballot_w64(nq > lev && below == rem));
-        qb = lev;
-        break;
-      }
-      rem -= cnt;
-    }
-    if (qb < 0) return;
-    const int pair = xcd + kXcds * ksel;
-    s = pair / p.num_kv_heads;
-    h = pair % p.num_kv_heads;
-    q0 = __shfl(lq0, ksel, 64);
-    ql = __shfl(lql, ksel, 64);
-    k0 = __shfl(lk0, ksel, 64);
-    kl = __shfl(lkl, ksel, 64);
   } else {
-    if (local >= ppx * nqb) return;
-    qb = nqb - 1 - local / ppx;
-    const int pair = xcd + kXcds * (local % ppx);
-    s = pair / p.num_kv_heads;
-    h = pair % p.num_kv_heads;
-    q0 = p.cu_q[s];
-    ql = p.cu_q[s + 1] - q0;
-    k0 = p.cu_k[s];
-    kl = p.cu_k[s + 1] - k0;
+    refill(0);
   }
-  const int pos0 = qb * BQ;
-  if (pos0 >= ql) return;
-  const int pos_end = min(ql, pos0 + BQ);
-  const int diag = kl - ql;  // bottom-right alignment offset
-  const int pool_prefix = kPaged ? (p.k != nullptr ? kl - ql : kl) : 0;
-  const int kend = kCausal ? max(0, min(kl, diag + pos_end)) : kl;
-  const int ntiles = (kend + kKeyTile - 1) / kKeyTile;
-  const int64_t table_row = (int64_t)s * p.t_sb;
+
+  struct Item {
+    int h, qb, q0, ql, k0, kl;
+    int pos0, pos_end, diag, pool_prefix, kend, ntiles;
+    int64_t new_base, table_row;
+  };
+  int round = 0;                         // this workgroup's next round
+  int lev = nqb - 1, cum = 0;            // lane_pairs walk: level and items above it
+  auto next_item = [&](Item& it) -> bool {
+    int ksel, qb;
+    if (lane_pairs) {
+      const int64_t li = item_index(round);
+      // Levels are walked downwards once over the workgroup's life: the
+      // list indices of its rounds increase.
+      int cnt = 0;
+      while (lev >= 0) {
+        cnt = __popcll(__builtin_amdgcn_ballot_w64(lnq > lev));
+        if (li < cum + cnt) break;
+        cum += cnt;
+        --lev;
+      }
+      if (lev < 0) return false;
+      ++round;
+      const int rem = (int)(li - cum);
+      const uint64_t live = __builtin_amdgcn_ballot_w64(lnq > lev);
+      const int below = __builtin_amdgcn_mbcnt_hi((uint32_t)(live >> 32),
+                                                   __builtin_amdgcn_mbcnt_lo((uint32_t)live, 0));
+      ksel = __builtin_ctzll(__builtin_amdgcn_ballot_w64(lnq > lev && below == rem));
+      qb = lev;
+      const int pair = xcd + kXcds * ksel;
+      it.h = pair % p.num_kv_heads;
+    } else {
+      for (;;) {
+        if (item_index(round) >= total) return false;
+        if (round > 0 && (round & 63) == 0) refill(round);
+        ksel = round & 63;
+        ++round;
+        qb = __builtin_amdgcn_readlane(lnq, ksel);
+        if (qb * BQ < __builtin_amdgcn_readlane(lql, ksel)) break;  // else past the end
+      }
+      it.h = __builtin_amdgcn_readlane(lpair, ksel) % p.num_kv_heads;
+    }
+    const int pair = lane_pairs ? xcd + kXcds * ksel : __builtin_amdgcn_readlane(lpair, ksel);
+    const int s = pair / p.num_kv_heads;
+    it.qb = qb;
+    it.q0 = __builtin_amdgcn_readlane(lq0, ksel);
+    it.ql = __builtin_amdgcn_readlane(lql, ksel);
+    it.k0 = __builtin_amdgcn_readlane(lk0, ksel);
+    it.kl = __builtin_amdgcn_readlane(lkl, ksel);
+    it.pos0 = qb * BQ;
+    it.pos_end = min(it.ql, it.pos0 + BQ);
+    it.diag = it.kl - it.ql;  // bottom-right alignment offset
+    it.pool_prefix = kPaged ? (p.k != nullptr ? it.kl - it.ql : it.kl) : 0;
+    it.kend = kCausal ? max(0, min(it.kl, it.diag + it.pos_end)) : it.kl;
+    it.ntiles = (it.kend + kKeyTile - 1) / kKeyTile;
+    // Keys from k/v: key j is row new_base + j of k and v.
+    it.new_base = kPaged ? (int64_t)it.q0 - it.pool_prefix : (int64_t)it.k0;
+    it.table_row = (int64_t)s * p.t_sb;
+    return true;
+  };
+
   const uint32_t lds_base = __builtin_amdgcn_readfirstlane(
       (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)s_kv);
 
   // ---- DMA of key tile [kb, kb + 64) into stage st ----
+  // (h, pool_prefix, kend, new_base, table_row) are the item's; all uniform.
   // Wave w fills 1 KiB blocks w NI .. w NI + NI - 1 of the K and V tiles;
   // lane l of a block writes row RPI * block + l / CPR, chunk position l % CPR,
   // so it reads logical chunk (l % CPR) ^ swz(row) of that key.  Every lane
   // issues exactly 2 NI DMAs per tile.
-  // Keys from k/v: key j is row new_base + j of k and v.
-  const int64_t new_base = kPaged ? (int64_t)q0 - pool_prefix : (int64_t)k0;
   uint32_t koff[NI], voff[NI];  // per-lane byte offsets inside a tile of k/v rows
 #pragma unroll
   for (int i = 0; i < NI; ++i) {
@@ -240,7 +288,8 @@ __global__ __launch_bounds__(kVarlenThreads, 2) void varlen_attention_kernel(Var
     voff[i] = (uint32_t)(row * p.v_st + chunk * 16);
   }
   const char* zero_row = reinterpret_cast<const char*>(&kZeroRow);
-  auto issue_tile = [&](int kb, int st) {
+  auto issue_tile = [&](int h, int pool_prefix, int kend, int64_t new_base, int64_t table_row,
+                        int kb, int st) {
     const uint32_t dst0 = lds_base + (uint32_t)(st * 2 * TILE_B + wave * NI * 1024);
     if (kb >= pool_prefix && kb + kKeyTile <= kend) {
       // Whole tile from k/v: uniform bases, constant lane offsets.
@@ -254,292 +303,388 @@ __global__ __launch_bounds__(kVarlenThreads, 2) void varlen_attention_kernel(Var
       return;
     }
     // Tile with pool keys or past kend: per-lane addresses; rows past kend
-    // or with an unmapped block read kZeroRow.
-    int64_t bid[NI];
+    // or with an unmapped block read kZeroRow.  The lane's first row is
+    // made opaque so that the per-lane address arithmetic stays here
+    // instead of being hoisted out of the tile loop into live registers.
+    // Block ids are loaded as raw words and widened after the last load, and
+    // every address is formed before the first DMA: a register still
+    // awaiting its load when a DMA has been issued would make the compiler's
+    // wait for it also wait for that DMA.
+    int row0 = wave * NI * RPI + lane / CPR;
+    asm volatile("" : "+v"(row0));
+    uint2 braw[NI];
+#pragma unroll
+    for (int i = 0; i < NI; ++i) braw[i] = make_uint2(0u, 0u);
     if (kPaged && kb < pool_prefix) {
-      // Read all block ids first, so the loads share one wait.
+      int64_t e[NI];
+      bool ok[NI];
 #pragma unroll
       for (int i = 0; i < NI; ++i) {
-        const int j = kb + (wave * NI + i) * RPI + lane / CPR;
+        const int j = kb + row0 + i * RPI;
         const int col = j / p.block_size;
-        bid[i] = (j < pool_prefix && j < kend && col < p.table_width)
-                     ? load_index(p.table, table_row + col, p.table_i64)
-                     : 0;
+        ok[i] = j < pool_prefix && j < kend && col < p.table_width;
+        e[i] = table_row + col;
+      }
+      if (p.table_i64) {
+#pragma unroll
+        for (int i = 0; i < NI; ++i)
+          if (ok[i]) braw[i] = reinterpret_cast<const uint2*>(p.table)[e[i]];
+      } else {
+#pragma unroll
+        for (int i = 0; i < NI; ++i)
+          if (ok[i]) braw[i].x = reinterpret_cast<const uint32_t*>(p.table)[e[i]];
+      }
+    }
+    const char* ka[NI];
+    const char* va_[NI];
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      const int row = row0 + i * RPI;
+      const int chunk = (lane % CPR) ^ swz<D>(row);
+      const int j = kb + row;
+      ka[i] = zero_row;
+      va_[i] = zero_row;
+      if (j < kend) {
+        if (kPaged && j < pool_prefix) {
+          const int64_t bid = p.table_i64 ? (int64_t)(((uint64_t)braw[i].y << 32) | braw[i].x)
+                                          : (int64_t)(int32_t)braw[i].x;
+          if (bid >= 0 && bid < p.num_blocks) {
+            const int64_t off = bid * p.s_blk + (int64_t)(j % p.block_size) * p.s_slot +
+                                h * p.s_head + chunk * 16;
+            ka[i] = p.kp + off;
+            va_[i] = p.vp + off;
+          }
+        } else {
+          ka[i] = p.k + (new_base + j) * p.k_st + h * p.k_sh + chunk * 16;
+          va_[i] = p.v + (new_base + j) * p.v_st + h * p.v_sh + chunk * 16;
+        }
       }
     }
 #pragma unroll
     for (int i = 0; i < NI; ++i) {
-      const int row = (wave * NI + i) * RPI + lane / CPR;
-      const int chunk = (lane % CPR) ^ swz<D>(row);
-      const int j = kb + row;
-      const char* ka = zero_row;
-      const char* va_ = zero_row;
-      if (j < kend) {
-        if (kPaged && j < pool_prefix) {
-          if (bid[i] >= 0 && bid[i] < p.num_blocks) {
-            const int64_t off = bid[i] * p.s_blk + (int64_t)(j % p.block_size) * p.s_slot +
-                                h * p.s_head + chunk * 16;
-            ka = p.kp + off;
-            va_ = p.vp + off;
-          }
-        } else {
-          ka = p.k + (new_base + j) * p.k_st + h * p.k_sh + chunk * 16;
-          va_ = p.v + (new_base + j) * p.v_st + h * p.v_sh + chunk * 16;
-        }
-      }
-      dma16(ka, dst0 + i * 1024);
-      dma16(va_, dst0 + TILE_B + i * 1024);
+      dma16(ka[i], dst0 + i * 1024);
+      dma16(va_[i], dst0 + TILE_B + i * 1024);
     }
   };
 
+  // ---- query rows and store slots of an item ----
+  // Two 16-row tiles per wave: row 16 (2 wave + tt) + r16 of the block is
+  // query position pos0 + row % BQ of head h G + row / BQ.
+  uint4 qreg[2][DS];
+  auto load_q = [&](const Item& it) {
 #pragma unroll
-  for (int st = 0; st < kStages - 1; ++st)
-    if (st < ntiles) issue_tile(st * kKeyTile, st);
-
-  // ---- fused store of this block's new K/V rows (kv head h) ----
-  // The new rows are keys [pool_prefix + pos0, pool_prefix + pos_end), which
-  // the tile loop stages in LDS anyway: each is copied from there to its
-  // slot, so k/v are read once.  TPR threads share a row; thread `sub` of a
-  // row moves items sub, sub + TPR, ... of its 2 CPR chunks (K then V).
+    for (int tt = 0; tt < 2; ++tt) {
+      const int row = 16 * (2 * wave + tt) + r16;
+      const int qpos = it.pos0 + row % BQ;
+      const int qhead = it.h * G + row / BQ;
+#pragma unroll
+      for (int ds = 0; ds < DS; ++ds) {
+        if (qpos < it.ql)
+          qreg[tt][ds] = ld16(p.q + (int64_t)(it.q0 + qpos) * p.q_st +
+                              (int64_t)qhead * p.q_sh + (32 * ds + 8 * g4) * 2);
+        else
+          qreg[tt][ds] = make_uint4(0, 0, 0, 0);
+      }
+    }
+  };
+  // Fused store: the item's new rows are keys [pool_prefix + pos0,
+  // pool_prefix + pos_end), which the tile loop stages in LDS anyway: each is
+  // copied from there to its slot, so k/v are read once.  TPR threads share
+  // a row; thread `sub` of a row moves items sub, sub + TPR, ... of its
+  // 2 CPR chunks (K then V).  The slot index is loaded with the item's query
+  // rows, as the raw 32-bit word(s) of the mapping (all ones for no row), and
+  // widened only where it is used, once the tile holding the row has landed:
+  // widening at the load would wait for it there, behind the tile DMA just
+  // issued.
   constexpr int TPR = kVarlenThreads / BQ;
   constexpr int IPT = 2 * CPR / TPR;
   static_assert(TPR * BQ == kVarlenThreads && IPT * TPR == 2 * CPR, "store split");
   const bool fused_store = kPaged && p.slots != nullptr;
   const int st_row = tid / TPR, st_sub = tid % TPR;
-  const int st_key = pool_prefix + pos0 + st_row;  // key index of this thread's row
-  int64_t st_dst = -1;                             // pool byte offset of the row's slot
-  if (fused_store && pos0 + st_row < pos_end) {
-    const int64_t slot = load_index(p.slots, q0 + pos0 + st_row, p.slot_i64);
-    if (slot >= 0 && slot < (int64_t)p.num_blocks * p.block_size) {
-      const int64_t blk = slot / p.block_size;
-      st_dst = blk * p.s_blk + (slot - blk * p.block_size) * p.s_slot + h * p.s_head;
-    }
-  }
-
-  // ---- per-lane row bookkeeping: two 16-row tiles per wave ----
-  int qpos[2], qhead[2];
-#pragma unroll
-  for (int tt = 0; tt < 2; ++tt) {
-    const int row = 16 * (2 * wave + tt) + r16;
-    qhead[tt] = h * G + row / BQ;
-    qpos[tt] = pos0 + row % BQ;
-  }
-
-  uint4 qreg[2][DS];
-#pragma unroll
-  for (int tt = 0; tt < 2; ++tt)
-#pragma unroll
-    for (int ds = 0; ds < DS; ++ds) {
-      if (qpos[tt] < ql)
-        qreg[tt][ds] = ld16(p.q + (int64_t)(q0 + qpos[tt]) * p.q_st +
-                            (int64_t)qhead[tt] * p.q_sh + (32 * ds + 8 * g4) * 2);
+  auto load_slot = [&](const Item& it) -> uint2 {
+    uint2 raw = make_uint2(~0u, ~0u);
+    if (fused_store && it.pos0 + st_row < it.pos_end) {
+      const int64_t i = (int64_t)it.q0 + it.pos0 + st_row;
+      if (p.slot_i64)
+        raw = reinterpret_cast<const uint2*>(p.slots)[i];
       else
-        qreg[tt][ds] = make_uint4(0, 0, 0, 0);
+        raw.x = reinterpret_cast<const uint32_t*>(p.slots)[i];
     }
-
-  // Wait for the query (and, in order, everything issued before it) here, so
-  // the compiler has no load of its own pending inside the tile loop, where
-  // its wait would also stall on the next tile's DMA.
-#pragma unroll
-  for (int tt = 0; tt < 2; ++tt)
-#pragma unroll
-    for (int ds = 0; ds < DS; ++ds)
-      asm volatile("" ::"v"(qreg[tt][ds].x), "v"(qreg[tt][ds].y), "v"(qreg[tt][ds].z),
-                   "v"(qreg[tt][ds].w));
-  asm volatile("" ::"v"((uint32_t)st_dst), "v"((uint32_t)(st_dst >> 32)));
-
-  float m[2] = {-1.0e30f, -1.0e30f};
-  float l[2] = {0.f, 0.f};
-  f32x4_t o[2][DT];
-#pragma unroll
-  for (int tt = 0; tt < 2; ++tt)
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt) o[tt][dt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-
-  // Visible keys per row: j < lim[tt]; tiles ending at or below lim_lo (the
-  // smallest limit in the workgroup) need no mask.  Rows past the end of the
-  // sequence have zero queries; their outputs are never written.
-  int lim[2];
-#pragma unroll
-  for (int tt = 0; tt < 2; ++tt) lim[tt] = kCausal ? min(kend, diag + qpos[tt] + 1) : kend;
-  const int lim_lo = kCausal ? min(kend, diag + pos0 + 1) : kend;
+    return raw;
+  };
 
   // Swizzled chunk positions of this lane's reads (row % 16 is fixed per lane).
   const int kswz = swz<D>(r16);
   const int vswz = swz<D>(4 * g4 + (r16 >> 2));
 
-  for (int t = 0; t < ntiles; ++t) {
-    const int kb = t * kKeyTile;
-    // Tile t has landed once at most the 2 NI DMAs of each of tiles
-    // t + 1 .. t + kStages - 2 are pending; the barrier makes every wave's part
-    // of it visible and tells that every wave is done with tile t - 1, whose
-    // stage then takes tile t + kStages - 1.
-    if (t + kStages - 2 < ntiles)
-      wait_vmcnt<2 * NI * (kStages - 2)>();
-    else
-      wait_vmcnt<0>();
-    __syncthreads();
-    if (t + kStages - 1 < ntiles)
-      issue_tile(kb + (kStages - 1) * kKeyTile, (t + kStages - 1) % kStages);
-    const char* s_k = s_kv + (t % kStages) * 2 * TILE_B;
-    const char* s_v = s_k + TILE_B;
+  Item cur, nxt;
+  if (!next_item(cur)) return;
+  if (cur.ntiles > 0)
+    issue_tile(cur.h, cur.pool_prefix, cur.kend, cur.new_base, cur.table_row, 0, 0);
+  load_q(cur);
+  uint2 st_slot = load_slot(cur), nxt_slot = make_uint2(~0u, ~0u);
+  int stage = 0;  // stage holding the current item's next tile to reduce
 
-    if (fused_store && st_dst >= 0 && st_key >= kb && st_key < kb + kKeyTile) {
-      const int r = st_key - kb;
-#pragma unroll
-      for (int k = 0; k < IPT; ++k) {
-        const int e = st_sub + TPR * k;
-        const int c = e % CPR;
-        const uint4 w = lds_read16(e < CPR ? s_k : s_v, r * ROWB + ((c ^ swz<D>(r)) << 4));
-        st16((e < CPR ? p.kp : p.vp) + st_dst + c * 16, w);
-      }
-    }
+  for (;;) {
+    const bool has_next = next_item(nxt);
 
-    // ---- S^T = K Q^T for both row tiles ----
-    f32x4_t sacc[2][KT];
-#pragma unroll
-    for (int kt = 0; kt < KT; ++kt) {
-      sacc[0][kt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-      sacc[1][kt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int ds = 0; ds < DS; ++ds) {
-        const uint4 a = lds_read16(s_k, (16 * kt + r16) * ROWB + (((4 * ds + g4) ^ kswz) << 4));
-        sacc[0][kt] = M::mfma(a, qreg[0][ds], sacc[0][kt]);
-        sacc[1][kt] = M::mfma(a, qreg[1][ds], sacc[1][kt]);
-      }
-    }
-
-    // ---- online softmax (exp2 domain) and P^T packing ----
-    // Scores stay unscaled until the exponent: p = 2^(s c - m) with
-    // c = scale log2 e > 0 and m the row's running max of s c.  The max used
-    // as reference is raised only when a row's new max exceeds it by more
-    // than kLazy (or on the first scores); in between, p <= 2^kLazy, which
-    // the fp32 sums and 16-bit P hold exactly as well.  Key masking is
-    // applied only on tiles that cross a row's limit.
-    const bool need_mask = kb + kKeyTile > lim_lo;
-    uint4 pb[2][KS];
+    int qpos[2], qhead[2], lim[2];
 #pragma unroll
     for (int tt = 0; tt < 2; ++tt) {
-      float sv[KT][4];
-      if (need_mask) {
-        const int rel = lim[tt] - kb - 4 * g4;  // key 16 kt + i of this lane is visible iff < rel
+      const int row = 16 * (2 * wave + tt) + r16;
+      qhead[tt] = cur.h * G + row / BQ;
+      qpos[tt] = cur.pos0 + row % BQ;
+      // Visible keys per row: j < lim[tt].  Rows past the end of the
+      // sequence have zero queries; their outputs are never written.
+      lim[tt] = kCausal ? min(cur.kend, cur.diag + qpos[tt] + 1) : cur.kend;
+    }
+    // Tiles ending at or below lim_lo (the smallest limit in the block) need
+    // no mask.
+    const int lim_lo = kCausal ? min(cur.kend, cur.diag + cur.pos0 + 1) : cur.kend;
+    const int st_key = cur.pool_prefix + cur.pos0 + st_row;  // key of this thread's row
+
+    float m[2] = {-1.0e30f, -1.0e30f};
+    float l[2] = {0.f, 0.f};
+    f32x4_t o[2][DT];
 #pragma unroll
-        for (int kt = 0; kt < KT; ++kt)
+    for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
-          for (int i = 0; i < 4; ++i) sv[kt][i] = 16 * kt + i < rel ? sacc[tt][kt][i] : -INFINITY;
-      } else {
+      for (int dt = 0; dt < DT; ++dt) o[tt][dt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+    for (int t = 0; t < cur.ntiles; ++t) {
+      const int kb = t * kKeyTile;
+      // Tile t (and, in order, everything issued before it) has landed once
+      // nothing is pending; the barrier makes every wave's part of it
+      // visible and tells that every wave is done with the other stage,
+      // which then takes the next tile: this item's tile t + 1, or the next
+      // item's first tile.
+      wait_vmcnt<0>();
+      __syncthreads();
+      // The query rows and slot were loaded before the wait: make the
+      // compiler's own wait for them fall here, before the next DMA, where
+      // it is free (a later wait would also stall on that DMA).
 #pragma unroll
-        for (int kt = 0; kt < KT; ++kt)
+      for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
-          for (int i = 0; i < 4; ++i) sv[kt][i] = sacc[tt][kt][i];
+        for (int ds = 0; ds < DS; ++ds)
+          asm volatile("" ::"v"(qreg[tt][ds].x), "v"(qreg[tt][ds].y), "v"(qreg[tt][ds].z),
+                       "v"(qreg[tt][ds].w));
+      asm volatile("" ::"v"(st_slot.x), "v"(st_slot.y));
+      {
+        // One call site, fields picked one by one (uniform selects).
+        const bool same = t + 1 < cur.ntiles;
+        if (same || (has_next && nxt.ntiles > 0))
+          issue_tile(same ? cur.h : nxt.h, same ? cur.pool_prefix : nxt.pool_prefix,
+                     same ? cur.kend : nxt.kend, same ? cur.new_base : nxt.new_base,
+                     same ? cur.table_row : nxt.table_row, same ? kb + kKeyTile : 0, stage ^ 1);
       }
-      float mx = -INFINITY;
+      const char* s_k = s_kv + stage * 2 * TILE_B;
+      const char* s_v = s_k + TILE_B;
+
+      const int64_t slot = p.slot_i64 ? (int64_t)(((uint64_t)st_slot.y << 32) | st_slot.x)
+                                      : (int64_t)(int32_t)st_slot.x;
+      if (fused_store && slot >= 0 && slot < (int64_t)p.num_blocks * p.block_size &&
+          st_key >= kb && st_key < kb + kKeyTile) {
+        const int64_t blk = slot / p.block_size;
+        const int64_t st_dst =
+            blk * p.s_blk + (slot - blk * p.block_size) * p.s_slot + cur.h * p.s_head;
+        const int r = st_key - kb;
 #pragma unroll
-      for (int kt = 0; kt < KT; ++kt)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) mx = fmaxf(mx, sv[kt][i]);
-      mx = fmaxf(mx, lane_xor16(mx));
-      mx = fmaxf(mx, lane_xor32(mx));
-      const float mxs = mx * p.scale_log2;
-      if (__builtin_amdgcn_ballot_w64(mxs > m[tt] + kLazy) != 0) {
-        const float mnew = fmaxf(m[tt], mxs);
-        const float alpha = fast_exp2(m[tt] - mnew);
-        m[tt] = mnew;
-        l[tt] *= alpha;
-#pragma unroll
-        for (int dt = 0; dt < DT; ++dt) o[tt][dt] *= alpha;
-      }
-      float pr[KT][4];
-#pragma unroll
-      for (int kt = 0; kt < KT; ++kt)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          pr[kt][i] = fast_exp2(fmaf(sv[kt][i], p.scale_log2, -m[tt]));
-          l[tt] += pr[kt][i];
+        for (int k = 0; k < IPT; ++k) {
+          const int e = st_sub + TPR * k;
+          const int c = e % CPR;
+          const uint4 w = lds_read16(e < CPR ? s_k : s_v, r * ROWB + ((c ^ swz<D>(r)) << 4));
+          st16((e < CPR ? p.kp : p.vp) + st_dst + c * 16, w);
         }
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks) {
-        pb[tt][ks].x = M::pack2(pr[2 * ks][0], pr[2 * ks][1]);
-        pb[tt][ks].y = M::pack2(pr[2 * ks][2], pr[2 * ks][3]);
-        pb[tt][ks].z = M::pack2(pr[2 * ks + 1][0], pr[2 * ks + 1][1]);
-        pb[tt][ks].w = M::pack2(pr[2 * ks + 1][2], pr[2 * ks + 1][3]);
       }
+
+      // ---- S^T = K Q^T for both row tiles ----
+      f32x4_t sacc[2][KT];
+#pragma unroll
+      for (int kt = 0; kt < KT; ++kt) {
+        sacc[0][kt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        sacc[1][kt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ds = 0; ds < DS; ++ds) {
+          const uint4 a = lds_read16(s_k, (16 * kt + r16) * ROWB + (((4 * ds + g4) ^ kswz) << 4));
+          sacc[0][kt] = M::mfma(a, qreg[0][ds], sacc[0][kt]);
+          sacc[1][kt] = M::mfma(a, qreg[1][ds], sacc[1][kt]);
+        }
+      }
+      // The query rows are dead now: on the item's last tile, start the next
+      // item's loads.
+      if (t + 1 == cur.ntiles && has_next) {
+        load_q(nxt);
+        nxt_slot = load_slot(nxt);
+      }
+
+      // ---- online softmax (exp2 domain) and P^T packing ----
+      // Scores stay unscaled until the exponent: p = 2^(s c - m) with
+      // c = scale log2 e > 0 and m the row's running max of s c.  The max used
+      // as reference is raised only when a row's new max exceeds it by more
+      // than kLazy (or on the first scores); in between, p <= 2^kLazy, which
+      // the fp32 sums and 16-bit P hold exactly as well.  Key masking is
+      // applied only on tiles that cross a row's limit.
+      const bool need_mask = kb + kKeyTile > lim_lo;
+      uint4 pb[2][KS];
+#pragma unroll
+      for (int tt = 0; tt < 2; ++tt) {
+        float sv[KT][4];
+        if (need_mask) {
+          const int rel = lim[tt] - kb - 4 * g4;  // key 16 kt + i of this lane is visible iff < rel
+#pragma unroll
+          for (int kt = 0; kt < KT; ++kt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) sv[kt][i] = 16 * kt + i < rel ? sacc[tt][kt][i] : -INFINITY;
+        } else {
+#pragma unroll
+          for (int kt = 0; kt < KT; ++kt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) sv[kt][i] = sacc[tt][kt][i];
+        }
+        float mx = -INFINITY;
+#pragma unroll
+        for (int kt = 0; kt < KT; ++kt)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) mx = fmaxf(mx, sv[kt][i]);
+        mx = fmaxf(mx, lane_xor16(mx));
+        mx = fmaxf(mx, lane_xor32(mx));
+        const float mxs = mx * p.scale_log2;
+        if (__builtin_amdgcn_ballot_w64(mxs > m[tt] + kLazy) != 0) {
+          const float mnew = fmaxf(m[tt], mxs);
+          const float alpha = fast_exp2(m[tt] - mnew);
+          m[tt] = mnew;
+          l[tt] *= alpha;
+#pragma unroll
+          for (int dt = 0; dt < DT; ++dt) o[tt][dt] *= alpha;
+        }
+        float pr[KT][4];
+#pragma unroll
+        for (int kt = 0; kt < KT; ++kt)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            pr[kt][i] = fast_exp2(fmaf(sv[kt][i], p.scale_log2, -m[tt]));
+            l[tt] += pr[kt][i];
+          }
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+          pb[tt][ks].x = M::pack2(pr[2 * ks][0], pr[2 * ks][1]);
+          pb[tt][ks].y = M::pack2(pr[2 * ks][2], pr[2 * ks][3]);
+          pb[tt][ks].z = M::pack2(pr[2 * ks + 1][0], pr[2 * ks + 1][1]);
+          pb[tt][ks].w = M::pack2(pr[2 * ks + 1][2], pr[2 * ks + 1][3]);
+        }
+      }
+
+      // ---- O^T += V^T P^T ----
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) {
+          const int off = (32 * ks + 4 * g4 + (r16 >> 2)) * ROWB +
+                          (((2 * dt + ((r16 >> 1) & 1)) ^ vswz) << 4) + ((r16 & 1) << 3);
+          const s16x4_t lo = lds_read_tr(s_v, off);
+          const s16x4_t hi = lds_read_tr(s_v, off + 16 * ROWB);
+          uint4 a;
+          a.x = (uint32_t)(uint16_t)lo[0] | ((uint32_t)(uint16_t)lo[1] << 16);
+          a.y = (uint32_t)(uint16_t)lo[2] | ((uint32_t)(uint16_t)lo[3] << 16);
+          a.z = (uint32_t)(uint16_t)hi[0] | ((uint32_t)(uint16_t)hi[1] << 16);
+          a.w = (uint32_t)(uint16_t)hi[2] | ((uint32_t)(uint16_t)hi[3] << 16);
+          o[0][dt] = M::mfma(a, pb[0][ks], o[0][dt]);
+          o[1][dt] = M::mfma(a, pb[1][ks], o[1][dt]);
+        }
+      stage ^= 1;
+    }
+    if (cur.ntiles == 0 && has_next) {
+      // No visible keys in this item: its output is 0 and the next item's
+      // loads start here.  `stage` is free: no wave has read it since the
+      // last barrier.
+      if (nxt.ntiles > 0)
+        issue_tile(nxt.h, nxt.pool_prefix, nxt.kend, nxt.new_base, nxt.table_row, 0, stage);
+      load_q(nxt);
+      nxt_slot = load_slot(nxt);
     }
 
-    // ---- O^T += V^T P^T ----
+    // ---- normalise and write: lane holds O[row r16][16 dt + 4 g4 + i] ----
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks)
+    for (int tt = 0; tt < 2; ++tt) {
+      float lt = l[tt];
+      lt += lane_xor16(lt);
+      lt += lane_xor32(lt);
+      if (qpos[tt] >= cur.ql) continue;
+      const float inv = lt > 0.f ? 1.f / lt : 0.f;
+      char* dst = p.out + (int64_t)(cur.q0 + qpos[tt]) * p.o_st + (int64_t)qhead[tt] * p.o_sh;
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt) {
-        const int off = (32 * ks + 4 * g4 + (r16 >> 2)) * ROWB +
-                        (((2 * dt + ((r16 >> 1) & 1)) ^ vswz) << 4) + ((r16 & 1) << 3);
-        const s16x4_t lo = lds_read_tr(s_v, off);
-        const s16x4_t hi = lds_read_tr(s_v, off + 16 * ROWB);
-        uint4 a;
-        a.x = (uint32_t)(uint16_t)lo[0] | ((uint32_t)(uint16_t)lo[1] << 16);
-        a.y = (uint32_t)(uint16_t)lo[2] | ((uint32_t)(uint16_t)lo[3] << 16);
-        a.z = (uint32_t)(uint16_t)hi[0] | ((uint32_t)(uint16_t)hi[1] << 16);
-        a.w = (uint32_t)(uint16_t)hi[2] | ((uint32_t)(uint16_t)hi[3] << 16);
-        o[0][dt] = M::mfma(a, pb[0][ks], o[0][dt]);
-        o[1][dt] = M::mfma(a, pb[1][ks], o[1][dt]);
+        uint2 w;
+        w.x = M::pack2(o[tt][dt][0] * inv, o[tt][dt][1] * inv);
+        w.y = M::pack2(o[tt][dt][2] * inv, o[tt][dt][3] * inv);
+        *reinterpret_cast<uint2*>(dst + (16 * dt + 4 * g4) * 2) = w;
       }
-  }
-
-  // ---- normalise and write: lane holds O[row r16][16 dt + 4 g4 + i] ----
-#pragma unroll
-  for (int tt = 0; tt < 2; ++tt) {
-    float lt = l[tt];
-    lt += lane_xor16(lt);
-    lt += lane_xor32(lt);
-    if (qpos[tt] >= ql) continue;
-    const float inv = lt > 0.f ? 1.f / lt : 0.f;
-    char* dst = p.out + (int64_t)(q0 + qpos[tt]) * p.o_st + (int64_t)qhead[tt] * p.o_sh;
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt) {
-      uint2 w;
-      w.x = M::pack2(o[tt][dt][0] * inv, o[tt][dt][1] * inv);
-      w.y = M::pack2(o[tt][dt][2] * inv, o[tt][dt][3] * inv);
-      *reinterpret_cast<uint2*>(dst + (16 * dt + 4 * g4) * 2) = w;
     }
+    if (!has_next) break;
+    cur = nxt;
+    st_slot = nxt_slot;
   }
+}
+
+// Launch the persistent grid: per XCD, as many workgroups as the kernel
+// keeps resident on one XCD's CUs, or fewer when the XCD's item list (at
+// most items_per_xcd long) is shorter.
+template <bool kBF16, int D, int G, bool kCausal, bool kPaged>
+static void launch_persistent(const VarlenParams& p, int64_t items_per_xcd, hipStream_t st) {
+  const auto kern = varlen_attention_kernel<kBF16, D, G, kCausal, kPaged>;
+  static const int per_cu = [kern] {
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kern, kVarlenThreads, 0) != hipSuccess ||
+        n <= 0) {
+      (void)hipGetLastError();
+      n = 1;
+    }
+    return n;
+  }();
+  int64_t cus_per_xcd = current_device_cus() / kXcds;
+  if (cus_per_xcd < 1) cus_per_xcd = 1;
+  int64_t per_xcd = (int64_t)per_cu * cus_per_xcd;
+  if (per_xcd > items_per_xcd) per_xcd = items_per_xcd;
+  if (per_xcd < 1) per_xcd = 1;
+  hipLaunchKernelGGL(kern, dim3((unsigned)(per_xcd * kXcds)), dim3(kVarlenThreads), 0, st, p);
 }
 
 template <bool kBF16, int D, int G, bool kCausal>
-static void launch_varlen_c(const VarlenParams& p, dim3 grid, hipStream_t st) {
+static void launch_varlen_c(const VarlenParams& p, int64_t items_per_xcd, hipStream_t st) {
   if (p.has_pool)
-    hipLaunchKernelGGL((varlen_attention_kernel<kBF16, D, G, kCausal, true>), grid,
-                       dim3(kVarlenThreads), 0, st, p);
+    launch_persistent<kBF16, D, G, kCausal, true>(p, items_per_xcd, st);
   else
-    hipLaunchKernelGGL((varlen_attention_kernel<kBF16, D, G, kCausal, false>), grid,
-                       dim3(kVarlenThreads), 0, st, p);
+    launch_persistent<kBF16, D, G, kCausal, false>(p, items_per_xcd, st);
 }
 
 template <bool kBF16, int D, int G>
-static void launch_varlen(const VarlenParams& p, bool causal, dim3 grid, hipStream_t st) {
+static void launch_varlen(const VarlenParams& p, bool causal, int64_t items_per_xcd,
+                          hipStream_t st) {
   if (causal)
-    launch_varlen_c<kBF16, D, G, true>(p, grid, st);
+    launch_varlen_c<kBF16, D, G, true>(p, items_per_xcd, st);
   else
-    launch_varlen_c<kBF16, D, G, false>(p, grid, st);
+    launch_varlen_c<kBF16, D, G, false>(p, items_per_xcd, st);
 }
 
 template <bool kBF16, int D>
-static bool dispatch_varlen_g(int G, const VarlenParams& p, bool causal, dim3 grid,
+static bool dispatch_varlen_g(int G, const VarlenParams& p, bool causal, int64_t items_per_xcd,
                               hipStream_t st) {
   switch (G) {
-    case 1: launch_varlen<kBF16, D, 1>(p, causal, grid, st); return true;
-    case 2: launch_varlen<kBF16, D, 2>(p, causal, grid, st); return true;
-    case 4: launch_varlen<kBF16, D, 4>(p, causal, grid, st); return true;
-    case 8: launch_varlen<kBF16, D, 8>(p, causal, grid, st); return true;
+    case 1: launch_varlen<kBF16, D, 1>(p, causal, items_per_xcd, st); return true;
+    case 2: launch_varlen<kBF16, D, 2>(p, causal, items_per_xcd, st); return true;
+    case 4: launch_varlen<kBF16, D, 4>(p, causal, items_per_xcd, st); return true;
+    case 8: launch_varlen<kBF16, D, 8>(p, causal, items_per_xcd, st); return true;
     default: return false;
   }
 }
 
 template <bool kBF16>
-static bool dispatch_varlen(int D, int G, const VarlenParams& p, bool causal, dim3 grid,
-                            hipStream_t st) {
+static bool dispatch_varlen(int D, int G, const VarlenParams& p, bool causal,
+                            int64_t items_per_xcd, hipStream_t st) {
   switch (D) {
-    case 64: return dispatch_varlen_g<kBF16, 64>(G, p, causal, grid, st);
-    case 128: return dispatch_varlen_g<kBF16, 128>(G, p, causal, grid, st);
+    case 64: return dispatch_varlen_g<kBF16, 64>(G, p, causal, items_per_xcd, st);
+    case 128: return dispatch_varlen_g<kBF16, 128>(G, p, causal, items_per_xcd, st);
     default: return false;
   }
 }
@@ -644,15 +789,16 @@ extern "C" int va_varlen_attention(const va_varlen_args* a, void* stream) {
   p.num_seqs = a->num_seqs;
   p.num_kv_heads = a->num_kv_heads;
 
-  // 1-D grid: kXcds interleaved lists of (pair, query block); see the kernel.
+  // Persistent 1-D grid over kXcds interleaved item lists; see the kernel.
   const int64_t npairs = (int64_t)a->num_seqs * a->num_kv_heads;
-  const int64_t nwg = (npairs + kXcds - 1) / kXcds * kXcds * nqb;
-  VA_CHECK_ARG(npairs <= INT32_MAX / 2 && nwg <= INT32_MAX, "va_varlen_attention: grid too large");
-  const dim3 grid((unsigned)nwg);
+  const int64_t items_per_xcd = (npairs + kXcds - 1) / kXcds * nqb;
+  VA_CHECK_ARG(npairs <= INT32_MAX / 2 && items_per_xcd * kXcds <= INT32_MAX,
+               "va_varlen_attention: too many (sequence, kv head, query block) items");
   const hipStream_t st = (hipStream_t)stream;
-  const bool ok = a->dtype == VA_BF16
-                      ? dispatch_varlen<true>(a->head_dim, G, p, a->causal != 0, grid, st)
-                      : dispatch_varlen<false>(a->head_dim, G, p, a->causal != 0, grid, st);
+  const bool ok =
+      a->dtype == VA_BF16
+          ? dispatch_varlen<true>(a->head_dim, G, p, a->causal != 0, items_per_xcd, st)
+          : dispatch_varlen<false>(a->head_dim, G, p, a->causal != 0, items_per_xcd, st);
   if (!ok) {
     set_error("va_varlen_attention: unsupported configuration");
     return VA_ERR_UNSUPPORTED;
