@@ -219,6 +219,8 @@ extern "C" int va_paged_decode(const va_decode_args* a, void* stream) {
   p.block_size = a->pool.block_size;
   p.num_blocks = a->pool.num_blocks;
   p.block_is_chunk_aligned = a->pool.block_size % kChunk == 0;
+  p.bs_div = make_fastdiv((uint32_t)a->pool.block_size);
+  p.slot_small = (int64_t)a->pool.num_blocks * a->pool.block_size <= ((int64_t)1 << 31);
   {
     // Largest byte offset inside one pool: the last slot of the last head of
     // the last block, plus a row.

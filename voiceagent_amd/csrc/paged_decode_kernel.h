@@ -35,6 +35,7 @@
 // than the imbalance between long and short contexts.
 #pragma once
 
+#include "fastdiv.h"
 #include "prologue.h"
 
 namespace va {
@@ -49,6 +50,8 @@ struct DecodeParams {
   int64_t s_blk, s_slot, s_head;  // bytes
   int32_t block_size, num_blocks;
   int32_t block_is_chunk_aligned;  // block_size % 16 == 0
+  FastDiv bs_div;                  // block_size
+  int32_t slot_small;              // num_blocks * block_size <= 2^31
   int32_t pool_off32;              // every pool byte offset fits 32 bits
   const void* table;
   int64_t t_sb;  // elements

@@ -164,7 +164,7 @@ __global__ __launch_bounds__(MfmaDecodeShape<D>::W * 64, 1) void paged_decode_mf
   // the tile being reduced reads (refreshed when it reaches the refill).
   const uint32_t* const tabw = reinterpret_cast<const uint32_t*>(p.table);
   auto block_of = [&](int tok) -> int {  // table entry of token tok's block, 0 past the width
-    const int idx = tok / p.block_size;
+    const int idx = (int)fast_div((uint32_t)tok, p.bs_div);
     return idx < p.table_width ? (int)tabw[(table_row + idx) << p.table_i64] : 0;
   };
   int tab = 0;
@@ -247,7 +247,7 @@ __global__ __launch_bounds__(MfmaDecodeShape<D>::W * 64, 1) void paged_decode_mf
     const int32_t blk = __builtin_amdgcn_readlane(tab, k & 63);
     const uint32_t dst = lds_wave + (uint32_t)((k % S) * 2 * TILE_B);
     if (blk >= 0 && blk < p.num_blocks) {
-      const int64_t off = (int64_t)blk * p.s_blk + (int64_t)(tb % p.block_size) * p.s_slot +
+      const int64_t off = (int64_t)blk * p.s_blk + (int64_t)fast_mod((uint32_t)tb, p.bs_div) * p.s_slot +
                           head_off;
       const char* kb = uniform_ptr(p.kp + off);
       const char* vb = uniform_ptr(p.vp + off);
@@ -385,13 +385,14 @@ __global__ __launch_bounds__(MfmaDecodeShape<D>::W * 64, 1) void paged_decode_mf
       // slot of L - 1) and put it in place of the staged pool row.
       int64_t slot = new_slot;
       if (p.new_slots == nullptr)
-        slot = blk_ok ? (int64_t)blk * p.block_size + new_tok % p.block_size : -1;
+        slot = blk_ok ? (int64_t)blk * p.block_size + fast_mod((uint32_t)new_tok, p.bs_div) : -1;
       if (slot >= 0 && slot < cap && rg == 0) {
         const int r = new_tok - tb;
         const int pos16 = (col ^ dec_swz<D>(r)) << 4;
         *reinterpret_cast<uint4*>(sK + r * ROWB + pos16) = kcur;
         *reinterpret_cast<uint4*>(sV + r * ROWB + pos16) = vcur;
-        const int64_t sb = slot / p.block_size;
+        const int64_t sb = p.slot_small ? (int64_t)fast_div((uint32_t)slot, p.bs_div)
+                                        : slot / p.block_size;
         const int64_t dst = sb * p.s_blk + (slot - sb * p.block_size) * p.s_slot + head_off +
                             col * 16;
         st16(p.kp + dst, kcur);

@@ -31,6 +31,7 @@
 // table while the tile is loaded; the new keys come from k/v.  The fused
 // store copies an item's new K/V rows from the staged tiles to slot_mapping.
 #include "common.h"
+#include "fastdiv.h"
 
 namespace va {
 
@@ -64,6 +65,8 @@ struct VarlenParams {
   int32_t slot_i64;
   int32_t num_qblocks;
   int32_t num_seqs, num_kv_heads;
+  FastDiv bs_div, hkv_div;  // block_size, num_kv_heads
+  int32_t slot_small;       // num_blocks * block_size <= 2^31: slots divide in 32 bits
 };
 
 template <bool kBF16>
@@ -182,7 +185,7 @@ __global__ __launch_bounds__(kVarlenThreads, 2) void varlen_attention_kernel(Var
   const bool lane_pairs = ppx <= 64;
   int lq0 = 0, lql = 0, lk0 = 0, lkl = 0, lnq = 0, lpair = 0;
   auto load_ranges = [&](int pair) {
-    const int ls = pair / p.num_kv_heads;
+    const int ls = (int)fast_div((uint32_t)pair, p.hkv_div);
     lq0 = p.cu_q[ls];
     lql = p.cu_q[ls + 1] - lq0;
     lk0 = p.cu_k[ls];
@@ -196,8 +199,9 @@ __global__ __launch_bounds__(kVarlenThreads, 2) void varlen_attention_kernel(Var
     const int64_t li = item_index(r0 + lane);
     lnq = -1;
     if (li < total) {
-      lpair = xcd + kXcds * (int)(li % ppx);
-      lnq = nqb - 1 - (int)(li / ppx);  // the item's query block
+      const int li32 = (int)li;  // list indices stay below 2^31 (host check)
+      lpair = xcd + kXcds * (li32 % ppx);
+      lnq = nqb - 1 - li32 / ppx;  // the item's query block
       load_ranges(lpair);
     }
   };
@@ -239,7 +243,7 @@ __global__ __launch_bounds__(kVarlenThreads, 2) void varlen_attention_kernel(Var
       ksel = __builtin_ctzll(__builtin_amdgcn_ballot_w64(lnq > lev && below == rem));
       qb = lev;
       const int pair = xcd + kXcds * ksel;
-      it.h = pair % p.num_kv_heads;
+      it.h = (int)fast_mod((uint32_t)pair, p.hkv_div);
     } else {
       for (;;) {
         if (item_index(round) >= total) return false;
@@ -249,10 +253,10 @@ __global__ __launch_bounds__(kVarlenThreads, 2) void varlen_attention_kernel(Var
         qb = __builtin_amdgcn_readlane(lnq, ksel);
         if (qb * BQ < __builtin_amdgcn_readlane(lql, ksel)) break;  // else past the end
       }
-      it.h = __builtin_amdgcn_readlane(lpair, ksel) % p.num_kv_heads;
+      it.h = (int)fast_mod((uint32_t)__builtin_amdgcn_readlane(lpair, ksel), p.hkv_div);
     }
     const int pair = lane_pairs ? xcd + kXcds * ksel : __builtin_amdgcn_readlane(lpair, ksel);
-    const int s = pair / p.num_kv_heads;
+    const int s = (int)fast_div((uint32_t)pair, p.hkv_div);
     it.qb = qb;
     it.q0 = __builtin_amdgcn_readlane(lq0, ksel);
     it.ql = __builtin_amdgcn_readlane(lql, ksel);
@@ -321,7 +325,7 @@ __global__ __launch_bounds__(kVarlenThreads, 2) void varlen_attention_kernel(Var
 #pragma unroll
       for (int i = 0; i < NI; ++i) {
         const int j = kb + row0 + i * RPI;
-        const int col = j / p.block_size;
+        const int col = (int)fast_div((uint32_t)j, p.bs_div);
         ok[i] = j < pool_prefix && j < kend && col < p.table_width;
         e[i] = table_row + col;
       }
@@ -349,7 +353,7 @@ __global__ __launch_bounds__(kVarlenThreads, 2) void varlen_attention_kernel(Var
           const int64_t bid = p.table_i64 ? (int64_t)(((uint64_t)braw[i].y << 32) | braw[i].x)
                                           : (int64_t)(int32_t)braw[i].x;
           if (bid >= 0 && bid < p.num_blocks) {
-            const int64_t off = bid * p.s_blk + (int64_t)(j % p.block_size) * p.s_slot +
+            const int64_t off = bid * p.s_blk + (int64_t)fast_mod((uint32_t)j, p.bs_div) * p.s_slot +
                                 h * p.s_head + chunk * 16;
             ka[i] = p.kp + off;
             va_[i] = p.vp + off;
@@ -485,7 +489,8 @@ __global__ __launch_bounds__(kVarlenThreads, 2) void varlen_attention_kernel(Var
                                       : (int64_t)(int32_t)st_slot.x;
       if (fused_store && slot >= 0 && slot < (int64_t)p.num_blocks * p.block_size &&
           st_key >= kb && st_key < kb + kKeyTile) {
-        const int64_t blk = slot / p.block_size;
+        const int64_t blk = p.slot_small ? (int64_t)fast_div((uint32_t)slot, p.bs_div)
+                                         : slot / p.block_size;
         const int64_t st_dst =
             blk * p.s_blk + (slot - blk * p.block_size) * p.s_slot + cur.h * p.s_head;
         const int r = st_key - kb;
@@ -788,6 +793,9 @@ extern "C" int va_varlen_attention(const va_varlen_args* a, void* stream) {
   p.num_qblocks = nqb;
   p.num_seqs = a->num_seqs;
   p.num_kv_heads = a->num_kv_heads;
+  p.bs_div = make_fastdiv((uint32_t)p.block_size);
+  p.hkv_div = make_fastdiv((uint32_t)a->num_kv_heads);
+  p.slot_small = (int64_t)p.num_blocks * p.block_size <= ((int64_t)1 << 31);
 
   // Persistent 1-D grid over kXcds interleaved item lists; see the kernel.
   const int64_t npairs = (int64_t)a->num_seqs * a->num_kv_heads;
