@@ -60,14 +60,14 @@ def test_ragged_lengths_and_geometries(dev, dtype, causal, hq, hkv, d):
     assert _err(out, ref) <= TOL
 
 
-def _paged_prefill_case(seed=3, bs=16, nb=512):
+def _paged_prefill_case(seed=3, bs=16, nb=512, hq=16, hkv=8, d=128, slot_dtype=torch.int32,
+                        spec=((0, 70), (32, 50), (160, 1), (48, 200), (0, 1), (17, 64))):
     g = torch.Generator().manual_seed(seed)
     # (cached prefix, new tokens) per sequence: prefix-cache hits and plain prompts
-    spec = [(0, 70), (32, 50), (160, 1), (48, 200), (0, 1), (17, 64)]
     q_lens = [n for _, n in spec]
     k_lens = [p + n for p, n in spec]
-    kp = (torch.randn(nb, bs, 8, 128, generator=g)).to(torch.bfloat16)
-    vp = (torch.randn(nb, bs, 8, 128, generator=g)).to(torch.bfloat16)
+    kp = (torch.randn(nb, bs, hkv, d, generator=g)).to(torch.bfloat16)
+    vp = (torch.randn(nb, bs, hkv, d, generator=g)).to(torch.bfloat16)
     width = max(math.ceil(k / bs) for k in k_lens)
     perm = torch.randperm(nb, generator=g).tolist()
     rows, cur = [], 0
@@ -77,15 +77,15 @@ def _paged_prefill_case(seed=3, bs=16, nb=512):
         cur += n
     table = torch.tensor(rows, dtype=torch.int32)
     total = sum(q_lens)
-    q = torch.randn(total, 16, 128, generator=g).to(torch.bfloat16)
-    k = torch.randn(total, 8, 128, generator=g).to(torch.bfloat16)
-    v = torch.randn(total, 8, 128, generator=g).to(torch.bfloat16)
+    q = torch.randn(total, hq, d, generator=g).to(torch.bfloat16)
+    k = torch.randn(total, hkv, d, generator=g).to(torch.bfloat16)
+    v = torch.randn(total, hkv, d, generator=g).to(torch.bfloat16)
     slots = []
     for s, (p, n) in enumerate(spec):
         for pos in range(p, p + n):
             slots.append(int(table[s, pos // bs]) * bs + pos % bs)
     return dict(kp=kp, vp=vp, table=table, q=q, k=k, v=v, cu_q=_cu(q_lens), cu_k=_cu(k_lens),
-                max_q=max(q_lens), max_k=max(k_lens), slots=torch.tensor(slots, dtype=torch.int32))
+                max_q=max(q_lens), max_k=max(k_lens), slots=torch.tensor(slots, dtype=slot_dtype))
 
 
 def test_paged_prefix_with_fused_store(dev):
@@ -106,6 +106,29 @@ def test_paged_prefix_with_fused_store(dev):
                                 c["max_q"], c["max_k"], scale=128 ** -0.5, causal=True,
                                 k_cache=kd, v_cache=vd, block_tables=c["table"].to(dev))
     assert _err(out2, ref) <= TOL
+
+
+@pytest.mark.parametrize("hq,hkv,d", [(16, 8, 128), (8, 8, 128), (32, 4, 128), (64, 8, 128),
+                                      (14, 14, 64), (16, 2, 64)])
+@pytest.mark.parametrize("slot_dtype", [torch.int32, torch.int64])
+def test_fused_store_geometries(dev, hq, hkv, d, slot_dtype):
+    # Every (group, head_dim) store split: rows of one block straddle key tiles
+    # (unaligned prefixes), blocks shorter than a store step, and -1 slots
+    # (padding rows) that must be skipped without touching the pool.
+    spec = ((0, 70), (32, 50), (160, 1), (48, 200), (5, 3), (17, 129), (100, 17))
+    c = _paged_prefill_case(seed=hq + d, hq=hq, hkv=hkv, d=d, slot_dtype=slot_dtype, spec=spec)
+    c["slots"][::7] = -1
+    kd, vd = c["kp"].to(dev), c["vp"].to(dev)
+    out = ops.varlen_attention(c["q"].to(dev), c["k"].to(dev), c["v"].to(dev), c["cu_q"].to(dev),
+                               c["cu_k"].to(dev), c["max_q"], c["max_k"], scale=d ** -0.5,
+                               causal=True, k_cache=kd, v_cache=vd, block_tables=c["table"].to(dev),
+                               slot_mapping=c["slots"].to(dev))
+    ek, ev = oracle.store_kvcache(c["k"], c["v"], c["kp"], c["vp"], c["slots"])
+    torch.cuda.synchronize()
+    assert torch.equal(kd.cpu(), ek) and torch.equal(vd.cpu(), ev)
+    ref = oracle.varlen_attention(c["q"], c["k"], c["v"], c["cu_q"], c["cu_k"], d ** -0.5, True,
+                                  k_cache=c["kp"], v_cache=c["vp"], block_tables=c["table"])
+    assert _err(out, ref) <= TOL
 
 
 def test_rows_without_visible_keys_are_zero(dev):

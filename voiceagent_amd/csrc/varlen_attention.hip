@@ -393,18 +393,25 @@ __global__ __launch_bounds__(kVarlenThreads, 2) void varlen_attention_kernel(Var
   };
   // Fused store: the item's new rows are keys [pool_prefix + pos0,
   // pool_prefix + pos_end), which the tile loop stages in LDS anyway: each is
-  // copied from there to its slot, so k/v are read once.  TPR threads share
-  // a row; thread `sub` of a row moves items sub, sub + TPR, ... of its
-  // 2 CPR chunks (K then V).  The slot index is loaded with the item's query
-  // rows, as the raw 32-bit word(s) of the mapping (all ones for no row), and
-  // widened only where it is used, once the tile holding the row has landed:
-  // widening at the load would wait for it there, behind the tile DMA just
-  // issued.
-  constexpr int TPR = kVarlenThreads / BQ;
-  constexpr int IPT = 2 * CPR / TPR;
-  static_assert(TPR * BQ == kVarlenThreads && IPT * TPR == 2 * CPR, "store split");
+  // copied from there to its slot, so k/v are read once.  The block's rows
+  // are BQ x CPR 16-byte chunks, e = row CPR + chunk; store step k of wave w
+  // takes e = 256 k + 64 w + lane, so each step writes RPS = 64 / CPR whole
+  // rows of K and the same rows of V.  Lane j < NSTEP RPS of a wave loads
+  // the slot of the wave's row j (step j / RPS, row j % RPS of the step), and
+  // a store step reads the slots it needs from those lanes.  The slot is
+  // loaded with the item's query rows, as the raw 32-bit word(s) of the
+  // mapping (all ones for no row), and widened only where it is used, once
+  // the tile holding the row has landed: widening at the load would wait for
+  // it there, behind the tile DMA just issued.
+  constexpr int RPS = 64 / CPR;  // rows per store step
+  constexpr int NSTEP = (BQ * CPR + kVarlenThreads - 1) / kVarlenThreads;
+  static_assert(NSTEP * RPS <= 64, "one slot lane per row");
   const bool fused_store = kPaged && p.slots != nullptr;
-  const int st_row = tid / TPR, st_sub = tid % TPR;
+  auto st_base = [&](int k) {  // first block row of store step k (BQ: none)
+    const int e0 = k * kVarlenThreads + 64 * wave;
+    return e0 < BQ * CPR ? e0 / CPR : BQ;
+  };
+  const int st_row = lane < NSTEP * RPS ? min(st_base(lane / RPS) + lane % RPS, BQ) : BQ;
   auto load_slot = [&](const Item& it) -> uint2 {
     uint2 raw = make_uint2(~0u, ~0u);
     if (fused_store && it.pos0 + st_row < it.pos_end) {
@@ -445,7 +452,7 @@ __global__ __launch_bounds__(kVarlenThreads, 2) void varlen_attention_kernel(Var
     // Tiles ending at or below lim_lo (the smallest limit in the block) need
     // no mask.
     const int lim_lo = kCausal ? min(cur.kend, cur.diag + cur.pos0 + 1) : cur.kend;
-    const int st_key = cur.pool_prefix + cur.pos0 + st_row;  // key of this thread's row
+    const int st_key0 = cur.pool_prefix + cur.pos0;  // key of the block's first row
 
     float m[2] = {-1.0e30f, -1.0e30f};
     float l[2] = {0.f, 0.f};
@@ -485,21 +492,30 @@ __global__ __launch_bounds__(kVarlenThreads, 2) void varlen_attention_kernel(Var
       const char* s_k = s_kv + stage * 2 * TILE_B;
       const char* s_v = s_k + TILE_B;
 
-      const int64_t slot = p.slot_i64 ? (int64_t)(((uint64_t)st_slot.y << 32) | st_slot.x)
-                                      : (int64_t)(int32_t)st_slot.x;
-      if (fused_store && slot >= 0 && slot < (int64_t)p.num_blocks * p.block_size &&
-          st_key >= kb && st_key < kb + kKeyTile) {
-        const int64_t blk = p.slot_small ? (int64_t)fast_div((uint32_t)slot, p.bs_div)
-                                         : slot / p.block_size;
-        const int64_t st_dst =
-            blk * p.s_blk + (slot - blk * p.block_size) * p.s_slot + cur.h * p.s_head;
-        const int r = st_key - kb;
-#pragma unroll
-        for (int k = 0; k < IPT; ++k) {
-          const int e = st_sub + TPR * k;
-          const int c = e % CPR;
-          const uint4 w = lds_read16(e < CPR ? s_k : s_v, r * ROWB + ((c ^ swz<D>(r)) << 4));
-          st16((e < CPR ? p.kp : p.vp) + st_dst + c * 16, w);
+      // Store steps run only on tiles that hold some of the block's new rows.
+      if (fused_store && st_key0 < kb + kKeyTile &&
+          st_key0 + (cur.pos_end - cur.pos0) > kb) {
+        const int64_t cap = (int64_t)p.num_blocks * p.block_size;
+        const int c = lane % CPR;
+#pragma unroll 4
+        for (int k = 0; k < NSTEP; ++k) {
+          const int holder = k * RPS + lane / CPR;
+          const uint32_t sx = (uint32_t)__shfl((int)st_slot.x, holder, 64);
+          const uint32_t sy = (uint32_t)__shfl((int)st_slot.y, holder, 64);
+          const int64_t slot = p.slot_i64 ? (int64_t)(((uint64_t)sy << 32) | sx)
+                                          : (int64_t)(int32_t)sx;
+          const int row = st_base(k) + lane / CPR;
+          const int key = st_key0 + row;
+          if (row < BQ && slot >= 0 && slot < cap && key >= kb && key < kb + kKeyTile) {
+            const int64_t blk = p.slot_small ? (int64_t)fast_div((uint32_t)slot, p.bs_div)
+                                             : slot / p.block_size;
+            const int64_t dst = blk * p.s_blk + (slot - blk * p.block_size) * p.s_slot +
+                                cur.h * p.s_head + c * 16;
+            const int r = key - kb;
+            const int off = r * ROWB + ((c ^ swz<D>(r)) << 4);
+            st16(p.kp + dst, lds_read16(s_k, off));
+            st16(p.vp + dst, lds_read16(s_v, off));
+          }
         }
       }
 
@@ -610,20 +626,58 @@ __global__ __launch_bounds__(kVarlenThreads, 2) void varlen_attention_kernel(Var
     }
 
     // ---- normalise and write: lane holds O[row r16][16 dt + 4 g4 + i] ----
+    // The rows go out through LDS so that each store instruction writes whole
+    // rows (16 bytes per lane, CPR lanes per row) instead of 8-byte pieces of
+    // 16 rows: the narrow pattern cost more per byte.  The staging area is
+    // the stage of the item's last tile (the next item's first tile is
+    // landing in the other one); wave w uses its own 32 rows of it, so the
+    // only barrier needed is the one that tells every wave is done reading
+    // that stage's K and V.  Chunks are XOR-swizzled by row against bank
+    // conflicts.
+    if (cur.ntiles > 0) {
+      __syncthreads();
+      char* s_o = s_kv + (stage ^ 1) * 2 * TILE_B + wave * 32 * ROWB;
 #pragma unroll
-    for (int tt = 0; tt < 2; ++tt) {
-      float lt = l[tt];
-      lt += lane_xor16(lt);
-      lt += lane_xor32(lt);
-      if (qpos[tt] >= cur.ql) continue;
-      const float inv = lt > 0.f ? 1.f / lt : 0.f;
-      char* dst = p.out + (int64_t)(cur.q0 + qpos[tt]) * p.o_st + (int64_t)qhead[tt] * p.o_sh;
+      for (int tt = 0; tt < 2; ++tt) {
+        float lt = l[tt];
+        lt += lane_xor16(lt);
+        lt += lane_xor32(lt);
+        const float inv = lt > 0.f ? 1.f / lt : 0.f;
 #pragma unroll
-      for (int dt = 0; dt < DT; ++dt) {
-        uint2 w;
-        w.x = M::pack2(o[tt][dt][0] * inv, o[tt][dt][1] * inv);
-        w.y = M::pack2(o[tt][dt][2] * inv, o[tt][dt][3] * inv);
-        *reinterpret_cast<uint2*>(dst + (16 * dt + 4 * g4) * 2) = w;
+        for (int dt = 0; dt < DT; ++dt) {
+          uint2 w;
+          w.x = M::pack2(o[tt][dt][0] * inv, o[tt][dt][1] * inv);
+          w.y = M::pack2(o[tt][dt][2] * inv, o[tt][dt][3] * inv);
+          const int chunk = (2 * dt + (g4 >> 1)) ^ (r16 % CPR);
+          *reinterpret_cast<uint2*>(s_o + (16 * tt + r16) * ROWB + chunk * 16 + (g4 & 1) * 8) = w;
+        }
+      }
+      __builtin_amdgcn_wave_barrier();
+      constexpr int RPS = 64 / CPR;  // rows per store instruction
+#pragma unroll 2
+      for (int j = 0; j < 32 / RPS; ++j) {
+        const int rw = RPS * j + lane / CPR;  // row within the wave's 32
+        const int c = lane % CPR;
+        const uint4 v = lds_read16(s_o, rw * ROWB + ((c ^ ((rw % 16) % CPR)) << 4));
+        const int row = 32 * wave + rw;  // MFMA row of the block
+        const int qp = cur.pos0 + row % BQ;
+        if (qp < cur.ql)
+          st16(p.out + (int64_t)(cur.q0 + qp) * p.o_st + (int64_t)(cur.h * G + row / BQ) * p.o_sh +
+                   c * 16,
+               v);
+      }
+    } else {
+      // No visible keys: the rows are 0 (the other stage may be receiving the
+      // next item's first tile, so nothing is staged).
+#pragma unroll
+      for (int tt = 0; tt < 2; ++tt) {
+        const int row = 16 * (2 * wave + tt) + r16;
+        const int qp = cur.pos0 + row % BQ;
+        if (qp >= cur.ql) continue;
+        char* dst = p.out + (int64_t)(cur.q0 + qp) * p.o_st + (int64_t)(cur.h * G + row / BQ) * p.o_sh;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt)
+          *reinterpret_cast<uint2*>(dst + (16 * dt + 4 * g4) * 2) = make_uint2(0u, 0u);
       }
     }
     if (!has_next) break;
