@@ -60,6 +60,35 @@ def test_ragged_lengths_and_geometries(dev, dtype, causal, hq, hkv, d):
     assert _err(out, ref) <= TOL
 
 
+def test_persistent_rounds_long_prompts(dev):
+    # 8 prompts of ~2000 tokens, 8 kv heads: each XCD lists 8 pairs x 32 blocks,
+    # so every workgroup takes several items in snake order and the level walk
+    # crosses 32 levels.
+    lens = [2000, 1999, 1500, 2048, 1, 700, 1937, 64]
+    b = workloads.make_varlen_batch(lens, 16, 8, 128, causal=True, seed=5)
+    out = ops.varlen_attention(b.q.to(dev), b.k.to(dev), b.v.to(dev), b.cu_seqlens.to(dev),
+                               b.cu_seqlens.to(dev), b.max_seqlen, b.max_seqlen, scale=b.scale,
+                               causal=True)
+    ref = oracle.varlen_attention(b.q, b.k, b.v, b.cu_seqlens, b.cu_seqlens, b.scale, True)
+    assert _err(out, ref) <= TOL
+
+
+def test_persistent_many_pairs_item_refill(dev):
+    # 400 sequences x 2 kv heads (group 8, 16-position blocks) = 800 pairs, 100
+    # per XCD: the list holds every (pair, block), most blocks past their
+    # sequence's end, and one 660-token sequence makes it 42 levels deep, so
+    # a workgroup walks more than 64 rounds and refills its item ranges.
+    g = torch.Generator().manual_seed(9)
+    lens = torch.randint(1, 21, (400,), generator=g).tolist()
+    lens[137] = 660
+    b = workloads.make_varlen_batch(lens, 16, 2, 128, causal=True, seed=6)
+    out = ops.varlen_attention(b.q.to(dev), b.k.to(dev), b.v.to(dev), b.cu_seqlens.to(dev),
+                               b.cu_seqlens.to(dev), b.max_seqlen, b.max_seqlen, scale=b.scale,
+                               causal=True)
+    ref = oracle.varlen_attention(b.q, b.k, b.v, b.cu_seqlens, b.cu_seqlens, b.scale, True)
+    assert _err(out, ref) <= TOL
+
+
 def _paged_prefill_case(seed=3, bs=16, nb=512, hq=16, hkv=8, d=128, slot_dtype=torch.int32,
                         spec=((0, 70), (32, 50), (160, 1), (48, 200), (0, 1), (17, 64))):
     g = torch.Generator().manual_seed(seed)
