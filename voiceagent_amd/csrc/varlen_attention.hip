@@ -30,6 +30,8 @@
 // With a paged pool, keys j < k_len - q_len are gathered through the block
 // table while the tile is loaded; the new keys come from k/v.  The fused
 // store copies an item's new K/V rows from the staged tiles to slot_mapping.
+#include <atomic>
+
 #include "common.h"
 #include "fastdiv.h"
 
@@ -692,15 +694,20 @@ __global__ __launch_bounds__(kVarlenThreads, 2) void varlen_attention_kernel(Var
 template <bool kBF16, int D, int G, bool kCausal, bool kPaged>
 static void launch_persistent(const VarlenParams& p, int64_t items_per_xcd, hipStream_t st) {
   const auto kern = varlen_attention_kernel<kBF16, D, G, kCausal, kPaged>;
-  static const int per_cu = [kern] {
-    int n = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kern, kVarlenThreads, 0) != hipSuccess ||
-        n <= 0) {
+  // Resident workgroups per CU, queried once (a failed query is not cached:
+  // the launch then assumes 1, which is correct but leaves slots idle).
+  static std::atomic<int> cached{0};
+  int per_cu = cached.load(std::memory_order_relaxed);
+  if (per_cu <= 0) {
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, kVarlenThreads, 0) ==
+            hipSuccess &&
+        per_cu > 0) {
+      cached.store(per_cu, std::memory_order_relaxed);
+    } else {
       (void)hipGetLastError();
-      n = 1;
+      per_cu = 1;
     }
-    return n;
-  }();
+  }
   int64_t cus_per_xcd = current_device_cus() / kXcds;
   if (cus_per_xcd < 1) cus_per_xcd = 1;
   int64_t per_xcd = (int64_t)per_cu * cus_per_xcd;
