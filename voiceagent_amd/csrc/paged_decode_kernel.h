@@ -530,10 +530,11 @@ constexpr int kMaxParts = 256;
 // skipped.  Every wave serves one query head g over 64 of its D outputs
 // (idx = (g, d) in 64-wide slices).  Lane q of the wave holds (m, l) of
 // partitions q, q + 64, ..., and the o values of the first kBatch
-// partitions are loaded by every lane for its d in the same breath, so the
-// merge costs one round trip after the length.  The weights 2^(m_q - M) reach
-// the o sums through readlane (q is wave-uniform).  Loads use clamped
-// indices and are masked afterwards, so no load sits behind a branch.
+// partitions are loaded by every lane for its d in the same breath, together
+// with the length, so the merge costs one round trip.  The weights
+// 2^(m_q - M) reach the o sums through readlane (q is wave-uniform).  Loads
+// use clamped indices and are masked afterwards, so no load sits behind a
+// branch.
 template <typename ET, int D, int G>
 __global__ __launch_bounds__(256) void paged_decode_merge_kernel(DecodeParams p) {
   constexpr int E = ET::kPerVec;
@@ -544,37 +545,39 @@ __global__ __launch_bounds__(256) void paged_decode_merge_kernel(DecodeParams p)
   const int b = blockIdx.y;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  int L;
-  if (p.lens_cum)
-    L = (int)(load_index(p.lens, b + 1, p.lens_i64) - load_index(p.lens, b, p.lens_i64));
-  else
-    L = (int)load_index(p.lens, b, p.lens_i64);
-  L = __builtin_amdgcn_readfirstlane(L);
-  if (L <= 0) return;
-  const int P = partition_tokens(p, L);
-  int nparts = (L + P - 1) / P;
-  if (nparts > p.max_parts) nparts = p.max_parts;
-  if (nparts <= 1) return;
+  // Every load is issued before the first wait: the length (raw low words,
+  // as in the attention kernels) and the partials of all max_parts slots of
+  // the pair, whether or not this context filled them.  Slots past the
+  // context's partition count hold stale data; they are read (the workspace
+  // has them) but never enter the arithmetic.
+  const uint32_t* const lensw = reinterpret_cast<const uint32_t*>(p.lens);
+  const uint32_t len_hi = lensw[(int64_t)(b + p.lens_cum) << p.lens_i64];
+  const uint32_t len_lo = lensw[(int64_t)b << p.lens_i64];
   const int64_t pair_slot0 = ((int64_t)b * p.num_kv_heads + h) * p.max_parts;
 
   for (int idx0 = tid & ~63; idx0 < G * D; idx0 += 256) {
     const int g = idx0 / D;                // uniform per wave
     const int d = idx0 % D + lane;
-    // (m, l) of this lane's partitions and o of the first batch, all issued
-    // before any is used.
     float mq[kPerLane], lq[kPerLane], oq[kBatch];
 #pragma unroll
     for (int i = 0; i < kPerLane; ++i) {
       const int q = lane + 64 * i;
-      const int64_t slot = (pair_slot0 + (q < nparts ? q : nparts - 1)) * G + g;
+      const int64_t slot = (pair_slot0 + (q < p.max_parts ? q : p.max_parts - 1)) * G + g;
       mq[i] = p.part_ml[slot * 2];
       lq[i] = p.part_ml[slot * 2 + 1];
     }
 #pragma unroll
     for (int j = 0; j < kBatch; ++j) {
-      const int q = j < nparts ? j : nparts - 1;
+      const int q = j < p.max_parts ? j : p.max_parts - 1;
       oq[j] = p.part_o[((pair_slot0 + q) * G + g) * D + d];
     }
+    int L = (int)(p.lens_cum ? len_hi - len_lo : len_lo);
+    L = __builtin_amdgcn_readfirstlane(L);
+    if (L <= 0) return;
+    const int P = partition_tokens(p, L);
+    int nparts = (L + P - 1) / P;
+    if (nparts > p.max_parts) nparts = p.max_parts;
+    if (nparts <= 1) return;  // the attention kernel wrote the output itself
     float M = kNegBig;
 #pragma unroll
     for (int i = 0; i < kPerLane; ++i)
@@ -583,8 +586,9 @@ __global__ __launch_bounds__(256) void paged_decode_merge_kernel(DecodeParams p)
     float w[kPerLane], Lt = 0.f;
 #pragma unroll
     for (int i = 0; i < kPerLane; ++i) {
-      w[i] = lane + 64 * i < nparts ? fast_exp2(mq[i] - M) : 0.f;
-      Lt = fmaf(w[i], lq[i], Lt);
+      const bool live = lane + 64 * i < nparts;
+      w[i] = live ? fast_exp2(mq[i] - M) : 0.f;
+      if (live) Lt = fmaf(w[i], lq[i], Lt);
     }
     Lt = group_sum<64>(Lt);
     float acc = 0.f;
