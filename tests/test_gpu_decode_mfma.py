@@ -133,3 +133,45 @@ def test_max_seq_len_as_upper_bound(dev, dtype, max_seq_len):
                            max_seq_len=max_seq_len, scale=128 ** -0.5)
     ref = oracle.paged_decode(q, kp, vp, table, lt, 128 ** -0.5)
     assert _err(out, ref) <= (TOL if dtype != torch.float32 else 1e-5)
+
+
+@pytest.mark.parametrize("idx_dtype", [torch.int32, torch.int64])
+@pytest.mark.parametrize("cumulative", [False, True])
+def test_early_issue_one_partition_per_pair(dev, idx_dtype, cumulative):
+    # 40 sequences x 8 kv heads = 320 pairs, more than the CUs: one partition per
+    # pair, so each wave requests its first tiles before the context length has
+    # arrived.  Zero-length contexts, contexts shorter than one tile, unmapped
+    # blocks (-1 and past num_blocks) inside the early tiles, the fused write of
+    # the current row, and int32/int64 tables, lengths and slots.
+    lens = [0, 1, 15, 16, 17, 33, 600, 0, 250, 129] * 4
+    bs = 16
+    q, kp, vp, table, _ = _nhd_case(lens, bs, torch.bfloat16, seed=77)
+    nb = kp.shape[0]
+    keep = torch.ones(len(lens), max(lens), dtype=torch.bool)
+    table[6, 1] = -1            # tokens 16..31 of a 600-token context
+    keep[6, 16:32] = False
+    table[8, 0] = nb + 5        # tokens 0..15 of a 250-token context
+    keep[8, 0:16] = False
+    g = torch.Generator().manual_seed(78)
+    nk = (torch.randn(len(lens), 8, 128, generator=g) * 0.5).to(torch.bfloat16)
+    nv = (torch.randn(len(lens), 8, 128, generator=g) * 0.5).to(torch.bfloat16)
+    slots = torch.tensor([int(table[b, (n - 1) // bs]) * bs + (n - 1) % bs if n > 0 else -1
+                          for b, n in enumerate(lens)], dtype=idx_dtype)
+    lt = torch.tensor(lens, dtype=idx_dtype)
+    if cumulative:
+        lt = torch.cat([torch.zeros(1, dtype=idx_dtype), torch.cumsum(lt, 0).to(idx_dtype)])
+    kd, vd = kp.to(dev), vp.to(dev)
+    out = ops.paged_decode(q.to(dev), kd, vd, table.to(idx_dtype).to(dev), lt.to(dev),
+                           lens_cumulative=cumulative, max_seq_len=max(lens),
+                           scale=128 ** -0.5, new_k=nk.to(dev), new_v=nv.to(dev),
+                           new_slots=slots.to(dev)).cpu()
+    ek, ev = oracle.store_kvcache(nk, nv, kp, vp, slots.long())
+    torch.cuda.synchronize()
+    assert torch.equal(kd.cpu(), ek) and torch.equal(vd.cpu(), ev)
+    assert torch.count_nonzero(out[[0, 7, 10, 17]]) == 0
+    safe = table.clone()
+    safe[6, 1] = 0
+    safe[8, 0] = 0
+    ref = oracle.paged_decode(q, ek, ev, safe, torch.tensor(lens), 128 ** -0.5, valid_mask=keep)
+    live = [b for b, n in enumerate(lens) if n > 0]
+    assert _err(out[live], ref[live]) <= TOL
