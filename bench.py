@@ -138,6 +138,35 @@ def bench_decode(args, dev, stream):
                 batch=batch, qs=qs, nks=nks, nvs=nvs)
 
 
+def bench_kv_format(args, dev, stream, dec):
+    """Config 2 decode with the pools in the head-major layout [num_blocks, Hkv,
+    block_size, D] (one (block, kv head) is a contiguous 4 KiB run) instead of
+    the engine's [num_blocks, block_size, Hkv, D]; same values, same step."""
+    batch, layers = dec["batch"], workloads.LAYERS
+    kps = [k.permute(0, 2, 1, 3).contiguous() for k in batch.k_pools]
+    vps = [v.permute(0, 2, 1, 3).contiguous() for v in batch.v_pools]
+    outs = torch.empty_like(dec["qs"])
+
+    def step():
+        for i in range(layers):
+            ops.paged_decode(dec["qs"][i], kps[i], vps[i], batch.block_tables,
+                             batch.cu_seqlens_k, lens_cumulative=True,
+                             max_seq_len=batch.max_seq_len, scale=batch.scale,
+                             layout=ops.LAYOUT_HND, new_k=dec["nks"][i], new_v=dec["nvs"][i],
+                             new_slots=batch.slot_mapping, out=outs[i], split_tokens=args.split)
+
+    ms, _ = timed_graph(step, args.steps, args.warmup, stream)
+    del kps, vps
+    us = ms * 1000.0 / layers
+    gbs = dec["bytes_layer"] / (us * 1e-6) / 1e9
+    log(f"[kv format] head-major pool: {us:.2f} us/layer, {gbs:.0f} GB/s "
+        f"(engine layout {dec['us_layer']:.2f} us/layer)")
+    return {"us_per_layer": round(us, 2), "gbs": round(gbs, 1),
+            "frac": round(gbs / HBM_PEAK_GBS, 4),
+            "layout": "[num_blocks, Hkv, block_size, D]",
+            "engine_layout_us_per_layer": round(dec["us_layer"], 2)}
+
+
 def bench_prologue(args, dev, stream, dec):
     """Config 2's decode step with Qwen3's q/k RMSNorm + RoPE in front
     (models/qwen3.py:44-49): fused into the decode launch vs the standalone
@@ -402,7 +431,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--split", type=int, default=0, help="decode split_tokens (0 = auto)")
     ap.add_argument("--only", choices=["decode", "prefill", "encoder", "store", "longform",
-                                       "prologue", "all"],
+                                       "prologue", "kvformat", "all"],
                     default="all")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
@@ -443,10 +472,14 @@ def main():
     if args.only == "prologue":
         print(json.dumps({"qwen3_prologue": bench_prologue(args, dev, stream, dec)}))
         return
+    if args.only == "kvformat":
+        print(json.dumps({"kv_format_hnd": bench_kv_format(args, dev, stream, dec)}))
+        return
     extra = {}
     if args.only == "all":
         extra["store"] = bench_store(args, dev, stream, dec)
         extra["qwen3_prologue"] = bench_prologue(args, dev, stream, dec)
+        extra["kv_format_hnd"] = bench_kv_format(args, dev, stream, dec)
         pre = bench_prefill(args, dev, stream)
         enc = bench_encoder(args, dev, stream)
         extra["prefill"] = {"us_per_layer": round(pre["us_layer"], 2),

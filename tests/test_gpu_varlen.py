@@ -229,6 +229,59 @@ def test_paged_attention_layer_prefill_then_decode(dev):
         assert torch.equal(kv[0].cpu(), kc) and torch.equal(kv[1].cpu(), vc), step
 
 
+@pytest.mark.parametrize("fuse", [True, False])
+def test_paged_attention_layer_hnd_pool_matches_nhd(dev, fuse):
+    """The same engine sequence (prefix-cached prefill, then decode steps) on an
+    NHD pool and on an HND pool [nb, Hkv, bs, D]: outputs are bit-identical and
+    the pools hold the same rows."""
+    g = torch.Generator().manual_seed(15)
+    bs, nb = 16, 256
+    lens = [37, 90, 5, 130]
+    width = 12
+    perm = torch.randperm(nb, generator=g).tolist()
+    tables = [perm[i * width:(i + 1) * width] for i in range(len(lens))]
+    table_t = torch.tensor(tables, dtype=torch.int32, device=dev)
+    total = sum(lens)
+    q = torch.randn(total, 16, 128, generator=g).to(torch.bfloat16).to(dev)
+    k = torch.randn(total, 8, 128, generator=g).to(torch.bfloat16).to(dev)
+    v = torch.randn(total, 8, 128, generator=g).to(torch.bfloat16).to(dev)
+    slots = [tables[s][p // bs] * bs + p % bs for s, n in enumerate(lens) for p in range(n)]
+    cu = _cu(lens).to(dev)
+    steps = [(torch.randn(len(lens), 16, 128, generator=g).to(torch.bfloat16).to(dev),
+              torch.randn(len(lens), 8, 128, generator=g).to(torch.bfloat16).to(dev),
+              torch.randn(len(lens), 8, 128, generator=g).to(torch.bfloat16).to(dev))
+             for _ in range(3)]
+    results = {}
+    for layout in (ops.LAYOUT_NHD, ops.LAYOUT_HND):
+        layer = PagedAttention(16, 128, 128 ** -0.5, 8)
+        layer.fuse_store = fuse
+        layer.kv_layout = layout
+        shape = (2, nb, bs, 8, 128) if layout == ops.LAYOUT_NHD else (2, nb, 8, bs, 128)
+        kv = torch.zeros(shape, dtype=torch.bfloat16, device=dev)
+        layer.k_cache, layer.v_cache = kv[0], kv[1]
+        outs = []
+        ctx = AttentionContext(cu, cu, max(lens), max(lens),
+                               torch.tensor(slots, dtype=torch.int32, device=dev), table_t)
+        with attention_context(ctx):
+            outs.append(layer(q, k, v).clone())
+        cur = list(lens)
+        for qd, kd, vd in steps:
+            cur = [n + 1 for n in cur]
+            dslots = [tables[s][(n - 1) // bs] * bs + (n - 1) % bs for s, n in enumerate(cur)]
+            ctx = AttentionContext(torch.arange(len(cur) + 1, dtype=torch.int32, device=dev),
+                                   _cu(cur).to(dev), 1, max(cur),
+                                   torch.tensor(dslots, dtype=torch.int32, device=dev), table_t)
+            with attention_context(ctx):
+                outs.append(layer(qd, kd, vd).clone())
+        torch.cuda.synchronize()
+        pool = kv.cpu() if layout == ops.LAYOUT_NHD else kv.cpu().permute(0, 1, 3, 2, 4)
+        results[layout] = (outs, pool)
+    (o_n, p_n), (o_h, p_h) = results[ops.LAYOUT_NHD], results[ops.LAYOUT_HND]
+    assert torch.equal(p_n, p_h)
+    for a, b in zip(o_n, o_h):
+        assert torch.equal(a, b)
+
+
 def test_paged_attention_layer_profiling_pass_without_cache(dev):
     g = torch.Generator().manual_seed(6)
     layer = PagedAttention(16, 128, 128 ** -0.5, 8)

@@ -20,6 +20,13 @@ Fusing the store relies on the engine's invariant that ``slot_mapping[i]``
 is the pool slot of query token i's position (model_runner.py:202-204,
 graph_runner.py:165-168); ``fuse_store = False`` restores the reference's
 store-then-attend order with two launches.
+
+``kv_layout`` names the pool layout: ``"nhd"`` ``[num_blocks, block_size,
+Hkv, D]`` as model_runner.py:116-131 allocates it (the default), or
+``"hnd"`` ``[num_blocks, Hkv, block_size, D]``, in which one (block, kv head)
+is a contiguous 4 KiB run; decode reads it ~9% faster.  Every reader and
+writer of the pool is a kernel of this package, so an engine may allocate
+either layout and set ``PagedAttention.kv_layout`` to match.
 """
 
 from __future__ import annotations
@@ -55,6 +62,7 @@ def store_kvcache(
 
 class PagedAttention(nn.Module):
     fuse_store = True
+    kv_layout = ops.LAYOUT_NHD
 
     def __init__(self, num_heads: int, head_dim: int, scale: float, num_kv_heads: int):
         super().__init__()
@@ -93,11 +101,12 @@ class PagedAttention(nn.Module):
                     lens_cumulative=True,
                     max_seq_len=context.max_seqlen_k,
                     scale=self.scale,
+                    layout=self.kv_layout,
                     new_k=k,
                     new_v=v,
                     new_slots=context.slot_mapping,
                 )
-            store_kvcache(k, v, self.k_cache, self.v_cache, context.slot_mapping)
+            self._store(k, v, context.slot_mapping)
             return ops.paged_decode(
                 q,
                 self.k_cache,
@@ -107,6 +116,7 @@ class PagedAttention(nn.Module):
                 lens_cumulative=True,
                 max_seq_len=context.max_seqlen_k,
                 scale=self.scale,
+                layout=self.kv_layout,
             )
         if self.fuse_store:
             return ops.varlen_attention(
@@ -123,8 +133,9 @@ class PagedAttention(nn.Module):
                 v_cache=self.v_cache,
                 block_tables=context.block_tables,
                 slot_mapping=context.slot_mapping,
+                layout=self.kv_layout,
             )
-        store_kvcache(k, v, self.k_cache, self.v_cache, context.slot_mapping)
+        self._store(k, v, context.slot_mapping)
         return ops.varlen_attention(
             q,
             None,
@@ -138,7 +149,17 @@ class PagedAttention(nn.Module):
             k_cache=self.k_cache,
             v_cache=self.v_cache,
             block_tables=context.block_tables,
+            layout=self.kv_layout,
         )
+
+    def _store(self, k: torch.Tensor, v: torch.Tensor, slot_mapping: torch.Tensor) -> None:
+        """Unfused store: the reference's store_kvcache (and its stride
+        contract) for an NHD pool, the same scatter by layout otherwise."""
+        if self.kv_layout == ops.LAYOUT_NHD:
+            store_kvcache(k, v, self.k_cache, self.v_cache, slot_mapping)
+        else:
+            ops.store_kvcache(k, v, self.k_cache, self.v_cache, slot_mapping,
+                              layout=self.kv_layout)
 
 
 class VarlenSelfAttention(nn.Module):
