@@ -105,9 +105,13 @@ def _decode_case(dtype, seed, B=8, nb=256):
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("engine_slots", [True, False])
-def test_fused_decode_prologue_matches_oracle(dev, dtype, engine_slots):
-    b, lens, q, nk, nv, wq, wk, cs, pos = _decode_case(dtype, seed=11)
-    print(f"fused decode prologue {dtype} engine_slots={engine_slots} lens={lens}", flush=True)
+@pytest.mark.parametrize("B", [8, 40])
+def test_fused_decode_prologue_matches_oracle(dev, dtype, engine_slots, B):
+    # B=8: 64 (sequence, kv head) pairs, split into partitions; B=40: 320 pairs,
+    # one partition each, so the first tiles are requested before the length
+    # and the position-dependent rotary rows arrive.
+    b, lens, q, nk, nv, wq, wk, cs, pos = _decode_case(dtype, seed=11, B=B, nb=1024)
+    print(f"fused decode prologue {dtype} engine_slots={engine_slots} B={B}", flush=True)
     kp, vp = b.k_pools[0].to(dev), b.v_pools[0].to(dev)
     pro = ops.QKPrologue(wq.to(dev), wk.to(dev), 1e-6, cs.to(dev), pos.to(dev))
     out = ops.paged_decode(q.to(dev), kp, vp, b.block_tables.to(dev), b.cu_seqlens_k.to(dev),
@@ -133,10 +137,11 @@ def test_fused_decode_prologue_matches_oracle(dev, dtype, engine_slots):
         assert _close_16bit(got_k, rk, dtype)[0] == 0
 
 
-def test_fused_prologue_equals_two_launch_path_bitwise(dev):
+@pytest.mark.parametrize("B", [16, 40])
+def test_fused_prologue_equals_two_launch_path_bitwise(dev, B):
     """The fused prologue runs the same per-row code as va_qk_norm_rope, so
     fused and two-launch decodes agree bit for bit (output and pool)."""
-    b, lens, q, nk, nv, wq, wk, cs, pos = _decode_case(torch.bfloat16, seed=21, B=16)
+    b, lens, q, nk, nv, wq, wk, cs, pos = _decode_case(torch.bfloat16, seed=21, B=B, nb=1024)
     pro = ops.QKPrologue(wq.to(dev), wk.to(dev), 1e-6, cs.to(dev), pos.to(dev))
     common = dict(lens_cumulative=True, max_seq_len=max(lens), scale=128 ** -0.5,
                   new_v=nv.to(dev), new_slots=b.slot_mapping.to(dev))

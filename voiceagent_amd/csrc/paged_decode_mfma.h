@@ -139,6 +139,9 @@ __global__ __launch_bounds__(MfmaDecodeShape<D>::W * 64, 1) void paged_decode_mf
   static_assert(W * G * D * 4 + 2 * W * G * 4 <= W * Sh::WAVE_B, "merge scratch");
 
   __shared__ __align__(1024) char s_buf[W * Sh::WAVE_B];
+  // Query rows of the prologue, per wave, apart from the tile ring so that
+  // early tile DMAs cannot land on them.
+  __shared__ __align__(16) char s_q[kProlog ? W * G * ROWB : 16];
 
   const int b = blockIdx.x;
   const int h = blockIdx.y;
@@ -216,7 +219,6 @@ __global__ __launch_bounds__(MfmaDecodeShape<D>::W * 64, 1) void paged_decode_mf
     pro_wq = load_weights_raw<E>(p.pro.q_w, p.pro.w_dtype, col * E);
     pro_wk = load_weights_raw<E>(p.pro.k_w != nullptr ? p.pro.k_w : p.pro.q_w, p.pro.w_dtype,
                                  col * E);
-    load_rotary<E, LPR>(p.pro, pos, col, D, pro_c, pro_s);
   }
 
   char* const s_wave = s_buf + wave * Sh::WAVE_B;
@@ -267,16 +269,23 @@ __global__ __launch_bounds__(MfmaDecodeShape<D>::W * 64, 1) void paged_decode_mf
   // early tiles are safe to fetch, and the length's round trip leaves the
   // critical path.  The vector loads above are waited for first, so the
   // compiler's own waits for them do not fall after the DMA (where they
-  // would also wait for it).
-  const bool early = !kProlog && p.max_parts == 1;
+  // would also wait for it).  With the prologue only the block ids are: its
+  // rotary rows depend on the position and are requested after the DMA, so
+  // the prologue arithmetic waits for the early tiles anyway, which it
+  // precedes only by a few hundred cycles.
+  const bool early = p.max_parts == 1;
   if (early) {
+    if constexpr (!kProlog) {
 #pragma unroll
-    for (int j = 0; j < DS; ++j)
-      asm volatile("" ::"v"(qb[j].x), "v"(qb[j].y), "v"(qb[j].z), "v"(qb[j].w));
-    asm volatile("" ::"v"(kcur.x), "v"(kcur.y), "v"(kcur.z), "v"(kcur.w), "v"(vcur.x),
-                 "v"(vcur.y), "v"(vcur.z), "v"(vcur.w), "v"(tab));
+      for (int j = 0; j < DS; ++j)
+        asm volatile("" ::"v"(qb[j].x), "v"(qb[j].y), "v"(qb[j].z), "v"(qb[j].w));
+      asm volatile("" ::"v"(kcur.x), "v"(kcur.y), "v"(kcur.z), "v"(kcur.w), "v"(vcur.x),
+                   "v"(vcur.y), "v"(vcur.z), "v"(vcur.w));
+    }
+    asm volatile("" ::"v"(tab));
     for (int k = 0; k < S; ++k) issue(k);
   }
+  if constexpr (kProlog) load_rotary<E, LPR>(p.pro, pos, col, D, pro_c, pro_s);
 
   int L = (int)(p.lens_cum ? len_hi - len_lo : len_lo);
   L = __builtin_amdgcn_readfirstlane(L);
@@ -344,14 +353,13 @@ __global__ __launch_bounds__(MfmaDecodeShape<D>::W * 64, 1) void paged_decode_mf
 #pragma unroll
     for (int k = 0; k < QROWS; ++k) {
       const int g = rg + RPL * k;
-      if (g < G) st16(s_wave + g * ROWB + col * 16, qrow[k]);
+      if (g < G) st16(s_q + (wave * G + g) * ROWB + col * 16, qrow[k]);
     }
 #pragma unroll
     for (int j = 0; j < DS; ++j)
-      qb[j] = r16 < G ? *reinterpret_cast<const uint4*>(s_wave + r16 * ROWB + (4 * j + c4) * 16)
+      qb[j] = r16 < G ? *reinterpret_cast<const uint4*>(s_q + (wave * G + r16) * ROWB +
+                                                         (4 * j + c4) * 16)
                       : make_uint4(0, 0, 0, 0);
-    // Every wave has its q before any DMA may overwrite the scratch rows.
-    wait_lgkmcnt0();
   }
 
   if (!early)
