@@ -327,3 +327,23 @@ def test_workspace_reuse_across_batch_sizes(dev):
         ops.paged_decode(b.q, b.k_pools[0], b.v_pools[0], b.block_tables, b.cu_seqlens_k,
                          lens_cumulative=True, max_seq_len=b.max_seq_len, scale=b.scale, out=out)
         assert _err(out, _oracle_for(b)) <= 2e-2, (it, B)
+
+
+def test_split_merge_with_many_pairs(dev):
+    # An explicit split over more than 65536 (sequence, kv head) pairs: the
+    # merge grid's second dimension runs to 1040 sequences.  The sequences
+    # share a small pool through their block tables.
+    B, hkv, d, bs, nb = 1040, 64, 64, 16, 64
+    g = torch.Generator().manual_seed(33)
+    lens = torch.randint(1, 300, (B,), generator=g)
+    lens[:4] = torch.tensor([1, 129, 256, 299])
+    width = 19
+    table = torch.randint(0, nb, (B, width), generator=g, dtype=torch.int32)
+    kp = (torch.randn(nb, bs, hkv, d, generator=g) * 0.5).to(torch.bfloat16)
+    vp = torch.randn(nb, bs, hkv, d, generator=g).to(torch.bfloat16)
+    q = torch.randn(B, hkv, d, generator=g).to(torch.bfloat16)
+    out = ops.paged_decode(q.to(dev), kp.to(dev), vp.to(dev), table.to(dev), lens.to(dev),
+                           max_seq_len=300, scale=d ** -0.5, split_tokens=128)
+    ref = oracle.paged_decode(q, kp, vp, table, lens, d ** -0.5)
+    assert B * hkv > 65536
+    assert _err(out, ref) <= 2e-2

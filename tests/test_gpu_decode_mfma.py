@@ -175,3 +175,49 @@ def test_early_issue_one_partition_per_pair(dev, idx_dtype, cumulative):
     ref = oracle.paged_decode(q, ek, ev, safe, torch.tensor(lens), 128 ** -0.5, valid_mask=keep)
     live = [b for b, n in enumerate(lens) if n > 0]
     assert _err(out[live], ref[live]) <= TOL
+
+
+@pytest.mark.parametrize("B", [3, 40])
+@pytest.mark.parametrize("width,shift", [(704, 0), (300, 0), (601, 0), (704, 3), (20001, 1)])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_key_valid_mask_on_matrix_cores(dev, B, width, shift, dtype):
+    # The TTS decode's key_valid_mask on the matrix-core kernel: B=3 splits
+    # contexts into partitions, B=40 runs one partition per pair with the early
+    # tile requests.  Widths: past every context (704), shorter than some
+    # contexts (300: later tokens count as valid), and odd (601: rows start
+    # at every byte offset within a 4-byte word), and wider than 16 KiB.
+    # shift places the whole mask at a storage offset of that many bytes.  One
+    # sequence has every token masked and must come out 0.
+    base = [1, 15, 16, 17, 130, 299, 300, 301, 600, 700]
+    lens = (base * ((B + len(base) - 1) // len(base)))[:B]
+    q, kp, vp, table, lt = _nhd_case(lens, 16, dtype, seed=B + width)
+    g = torch.Generator().manual_seed(width)
+    valid = torch.rand(B, width, generator=g) < 0.8
+    dead = 1 if B > 1 else 0
+    valid[dead] = False
+    flat = torch.zeros(shift + B * width, dtype=torch.bool, device=dev)
+    flat[shift:] = valid.flatten().to(dev)
+    vdev = flat[shift:].view(B, width)
+    out = ops.paged_decode(q.to(dev), kp.to(dev), vp.to(dev), table.to(dev), lt.to(dev),
+                           max_seq_len=max(lens), scale=128 ** -0.5, valid_mask=vdev).cpu()
+    ref = oracle.paged_decode(q, kp, vp, table, lt, 128 ** -0.5, valid_mask=valid)
+    if lens[dead] <= width:
+        assert torch.count_nonzero(out[dead]) == 0
+    assert _err(out, ref) <= TOL
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_key_valid_mask_past_64_tiles_per_wave(dev, dtype):
+    # One partition per pair (40 sequences) and a 9100-token context: its
+    # waves hold the block ids and mask bits of 64 tiles at a time and reload
+    # both for tiles 64 onwards.
+    lens = [9100] + [40 + 7 * i for i in range(39)]
+    q, kp, vp, table, lt = _nhd_case(lens, 16, dtype, seed=91)
+    g = torch.Generator().manual_seed(92)
+    valid = torch.rand(len(lens), 9105, generator=g) < 0.7
+    valid[0, 8192:8200] = False  # a run of masked tokens past the 64th tile of a wave
+    out = ops.paged_decode(q.to(dev), kp.to(dev), vp.to(dev), table.to(dev), lt.to(dev),
+                           max_seq_len=max(lens), scale=128 ** -0.5,
+                           valid_mask=valid.to(dev)).cpu()
+    ref = oracle.paged_decode(q, kp, vp, table, lt, 128 ** -0.5, valid_mask=valid)
+    assert _err(out, ref) <= TOL

@@ -137,6 +137,30 @@ def test_fused_decode_prologue_matches_oracle(dev, dtype, engine_slots, B):
         assert _close_16bit(got_k, rk, dtype)[0] == 0
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("B", [8, 40])
+def test_fused_decode_prologue_with_key_mask(dev, dtype, B):
+    # The prologue together with a key_valid_mask (bf16 takes the matrix-core
+    # kernel, fp32 the general one), split into partitions (B=8) or not (B=40).
+    b, lens, q, nk, nv, wq, wk, cs, pos = _decode_case(dtype, seed=31, B=B, nb=1024)
+    g = torch.Generator().manual_seed(32)
+    width = max(lens) - 17
+    valid = torch.rand(B, width, generator=g) < 0.75
+    kp, vp = b.k_pools[0].to(dev), b.v_pools[0].to(dev)
+    pro = ops.QKPrologue(wq.to(dev), wk.to(dev), 1e-6, cs.to(dev), pos.to(dev))
+    out = ops.paged_decode(q.to(dev), kp, vp, b.block_tables.to(dev), b.cu_seqlens_k.to(dev),
+                           lens_cumulative=True, max_seq_len=max(lens), scale=128 ** -0.5,
+                           new_k=nk.to(dev), new_v=nv.to(dev), new_slots=b.slot_mapping.to(dev),
+                           prologue=pro, valid_mask=valid.to(dev))
+    torch.cuda.synchronize()
+    rq, rk = oracle.qk_norm_rope(q, nk, pos, wq, wk, 1e-6, cs)
+    rkp, rvp = oracle.store_kvcache(rk, nv, b.k_pools[0], b.v_pools[0], b.slot_mapping)
+    ref = oracle.paged_decode(rq, rkp, rvp, b.block_tables, torch.tensor(lens), 128 ** -0.5,
+                              valid_mask=valid)
+    tol = 2e-2 if dtype == torch.bfloat16 else 1e-5
+    assert (out.float().cpu() - ref.float()).abs().max().item() <= tol
+
+
 @pytest.mark.parametrize("B", [16, 40])
 def test_fused_prologue_equals_two_launch_path_bitwise(dev, B):
     """The fused prologue runs the same per-row code as va_qk_norm_rope, so

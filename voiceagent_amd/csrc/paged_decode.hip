@@ -28,9 +28,9 @@ static int decode_unit() {
 static int decode_unit_for(int dtype, int D, int G);
 
 // The matrix-core kernel serves 16-bit K/V with block sizes that are
-// multiples of 16 and no key_valid_mask; every other call takes the general
-// kernel.  VA_DECODE_KERNEL=general in the environment forces the general
-// kernel (for comparisons).
+// multiples of 16 (with or without a key_valid_mask and the prologue); every
+// other call takes the general kernel.  VA_DECODE_KERNEL=general in the
+// environment forces the general kernel (for comparisons).
 static bool general_kernel_forced() {
   static const int forced = [] {
     const char* e = std::getenv("VA_DECODE_KERNEL");
@@ -42,7 +42,6 @@ static bool general_kernel_forced() {
 static bool use_mfma_decode(const va_decode_args* a) {
   if (a->dtype != VA_BF16 && a->dtype != VA_F16) return false;
   if (a->pool.block_size <= 0 || a->pool.block_size % kChunk != 0) return false;
-  if (a->valid_mask != nullptr && a->valid_len > 0) return false;
   if (a->head_dim != 64 && a->head_dim != 128 && a->head_dim != 256) return false;
   if (a->num_kv_heads <= 0 || a->num_heads % a->num_kv_heads != 0) return false;
   const int G = a->num_heads / a->num_kv_heads;

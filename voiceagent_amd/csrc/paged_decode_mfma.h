@@ -1,6 +1,7 @@
 // Paged-KV decode attention on CDNA4 matrix cores, for 16-bit K/V whose
-// block size is a multiple of 16 and without a key_valid_mask (the engine's
-// decode; the general kernel in paged_decode_kernel.h covers the rest).
+// block size is a multiple of 16: the engine's decode and the TTS decode
+// with its key_valid_mask.  The general kernel in paged_decode_kernel.h
+// covers the rest.
 //
 // Same semantics, grid and partial/merge protocol as paged_decode_kernel:
 // the grid is (sequence, kv head, partition); a workgroup owns P consecutive
@@ -125,7 +126,10 @@ __device__ __align__(16) const uint4 kDecZeroRow = {0u, 0u, 0u, 0u};
 // Lazy-rescale slack of the online softmax in log2 units (p <= 2^kDecLazy).
 constexpr float kDecLazy = 8.0f;
 
-template <typename ET, int D, int G, bool kProlog>
+
+// kMask: the launch has a key_valid_mask (a separate instantiation, so the
+// kernel without one carries none of its loads or branches).
+template <typename ET, int D, int G, bool kProlog, bool kMask>
 __global__ __launch_bounds__(MfmaDecodeShape<D>::W * 64, 1) void paged_decode_mfma_kernel(
     DecodeParams p) {
   using Sh = MfmaDecodeShape<D>;
@@ -139,8 +143,8 @@ __global__ __launch_bounds__(MfmaDecodeShape<D>::W * 64, 1) void paged_decode_mf
   static_assert(W * G * D * 4 + 2 * W * G * 4 <= W * Sh::WAVE_B, "merge scratch");
 
   __shared__ __align__(1024) char s_buf[W * Sh::WAVE_B];
-  // Query rows of the prologue, per wave, apart from the tile ring so that
-  // early tile DMAs cannot land on them.
+  // Apart from the tile ring, so that early tile DMAs cannot land on them:
+  // the query rows of the prologue (per wave).
   __shared__ __align__(16) char s_q[kProlog ? W * G * ROWB : 16];
 
   const int b = blockIdx.x;
@@ -194,6 +198,47 @@ __global__ __launch_bounds__(MfmaDecodeShape<D>::W * 64, 1) void paged_decode_mf
                       : make_uint4(0, 0, 0, 0);
     }
   }
+  // key_valid_mask: lane l holds the validity of the 16 tokens of this
+  // wave's tile l (of the current 64-tile group, like `tab`) as 16 bits,
+  // token i of the tile at bit i; tokens at or past the mask's width count
+  // as valid.  The tile's 16 bytes are read as the aligned 4-byte words that
+  // cover them (five when the row does not start on a word boundary); a
+  // word holding a byte of the row lies in the page holding that byte, so
+  // reading it whole stays within mapped memory.
+  constexpr bool has_mask = kMask;  // the host launches it only with a mask
+  const int mlen = has_mask ? p.valid_len : 0;
+  const uint8_t* const mrow = p.valid + (has_mask ? (int64_t)b * p.valid_sb : 0);
+  const int moff = (int)((uintptr_t)mrow & 3);
+  const uint32_t* const mwords = reinterpret_cast<const uint32_t*>(mrow - moff);
+  uint32_t mraw[5] = {~0u, ~0u, ~0u, ~0u, ~0u};
+  int mtb = 0;  // first token of the tile whose words mraw holds
+  auto mask_load = [&](int tb) {
+    mtb = tb;
+#pragma unroll
+    for (int j = 0; j < 5; ++j) {
+      const int rb = tb + 4 * j - moff;  // row byte at the word's start
+      mraw[j] = rb < mlen && (j < 4 || moff != 0) ? mwords[(tb >> 2) + j] : 0xffffffffu;
+    }
+  };
+  auto mask_bits = [&]() -> uint32_t {
+    uint32_t bits = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      uint32_t x = __builtin_amdgcn_alignbyte(mraw[j + 1], mraw[j], (uint32_t)moff);
+      x |= x >> 4;  // bit 0 of each byte becomes the OR of the byte's bits
+      x |= x >> 2;
+      x |= x >> 1;
+      x &= 0x01010101u;
+      bits |= ((x * 0x01020408u) >> 24) << (4 * j);  // byte i's bit to bit 24 + i
+    }
+    const int rem = mlen - mtb;  // tokens of the tile inside the mask's width
+    if (rem < 16) bits |= rem <= 0 ? 0xffffu : (0xffffu << rem) & 0xffffu;
+    return bits;
+  };
+  uint32_t mbits = 0xffffu;
+  // With one partition per pair the partition starts at token 0, so the
+  // words go out with the other start-up loads (see `early` below).
+  if (has_mask && p.max_parts == 1) mask_load((wave + W * lane) * kChunk);
   uint4 kcur = make_uint4(0, 0, 0, 0), vcur = make_uint4(0, 0, 0, 0);
   if (p.new_k != nullptr) {
     kcur = ld16(p.new_k + b * p.nk_sb + h * p.nk_sh + col * 16);
@@ -244,6 +289,10 @@ __global__ __launch_bounds__(MfmaDecodeShape<D>::W * 64, 1) void paged_decode_mf
       // Next 64 tiles of this wave: refill the block-id prefetch.
       const int c = wave + W * (k + lane);
       tab = c * kChunk < span ? block_of(start + c * kChunk) : 0;
+      if (has_mask) {
+        mask_load(start + c * kChunk);
+        mbits = mask_bits();
+      }
     }
     const int tb = start + (wave + W * k) * kChunk;
     const int32_t blk = __builtin_amdgcn_readlane(tab, k & 63);
@@ -283,6 +332,8 @@ __global__ __launch_bounds__(MfmaDecodeShape<D>::W * 64, 1) void paged_decode_mf
                    "v"(vcur.y), "v"(vcur.z), "v"(vcur.w));
     }
     asm volatile("" ::"v"(tab));
+    if constexpr (kMask)
+      asm volatile("" ::"v"(mraw[0]), "v"(mraw[1]), "v"(mraw[2]), "v"(mraw[3]), "v"(mraw[4]));
     for (int k = 0; k < S; ++k) issue(k);
   }
   if constexpr (kProlog) load_rotary<E, LPR>(p.pro, pos, col, D, pro_c, pro_s);
@@ -362,10 +413,16 @@ __global__ __launch_bounds__(MfmaDecodeShape<D>::W * 64, 1) void paged_decode_mf
                       : make_uint4(0, 0, 0, 0);
   }
 
-  if (!early)
+  if (!early) {
     for (int k = 0; k < S; ++k)
       if (k < ntw) issue(k);
+    // The partition's start follows from the length here, so the mask words
+    // are requested behind the first tiles.
+    if (has_mask) mask_load(start + (wave + W * lane) * kChunk);
+  }
+  if (has_mask) mbits = mask_bits();
   int tab_proc = tab;
+  uint32_t mbits_proc = mbits;
 
   float m = kNegBig, l = 0.f;  // running max (scaled, log2) and sum of this lane's column
   mf_f32x4 o[DT];
@@ -384,7 +441,10 @@ __global__ __launch_bounds__(MfmaDecodeShape<D>::W * 64, 1) void paged_decode_mf
     char* sV = sK + TILE_B;
     const int c = wave + W * k;  // partition chunk of this tile
     const int tb = start + c * kChunk;
-    if (k > 0 && (k & 63) == 0) tab_proc = tab;
+    if (k > 0 && (k & 63) == 0) {
+      tab_proc = tab;
+      mbits_proc = mbits;
+    }
     const int32_t blk = __builtin_amdgcn_readlane(tab_proc, k & 63);
     const bool blk_ok = blk >= 0 && blk < p.num_blocks;
 
@@ -418,8 +478,15 @@ __global__ __launch_bounds__(MfmaDecodeShape<D>::W * 64, 1) void paged_decode_mf
     }
     float sv[4];
     const int rel = blk_ok ? end - tb - 4 * c4 : 0;  // token 4 c4 + i is live iff i < rel
+    if (has_mask) {
+      // Validity bits of tokens 4 c4 .. 4 c4 + 3 of this tile.
+      const uint32_t mb = (uint32_t)__builtin_amdgcn_readlane((int)mbits_proc, k & 63) >> (4 * c4);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) sv[i] = i < rel ? sacc[i] : -INFINITY;
+      for (int i = 0; i < 4; ++i) sv[i] = i < rel && ((mb >> i) & 1u) ? sacc[i] : -INFINITY;
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) sv[i] = i < rel ? sacc[i] : -INFINITY;
+    }
     float mx = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
     mx = fmaxf(mx, lane_xor16(mx));
     mx = fmaxf(mx, lane_xor32(mx));
@@ -511,10 +578,16 @@ __global__ __launch_bounds__(MfmaDecodeShape<D>::W * 64, 1) void paged_decode_mf
 template <typename ET, int D, int G>
 static void launch_decode_mfma(const DecodeParams& p, dim3 grid, hipStream_t s) {
   constexpr int NT = MfmaDecodeShape<D>::W * 64;
-  if (p.has_pro)
-    hipLaunchKernelGGL((paged_decode_mfma_kernel<ET, D, G, true>), grid, dim3(NT), 0, s, p);
+  const bool mask = p.valid != nullptr && p.valid_len > 0;
+  if (p.has_pro && mask)
+    hipLaunchKernelGGL((paged_decode_mfma_kernel<ET, D, G, true, true>), grid, dim3(NT), 0, s, p);
+  else if (p.has_pro)
+    hipLaunchKernelGGL((paged_decode_mfma_kernel<ET, D, G, true, false>), grid, dim3(NT), 0, s, p);
+  else if (mask)
+    hipLaunchKernelGGL((paged_decode_mfma_kernel<ET, D, G, false, true>), grid, dim3(NT), 0, s, p);
   else
-    hipLaunchKernelGGL((paged_decode_mfma_kernel<ET, D, G, false>), grid, dim3(NT), 0, s, p);
+    hipLaunchKernelGGL((paged_decode_mfma_kernel<ET, D, G, false, false>), grid, dim3(NT), 0, s,
+                       p);
   if (p.max_parts > 1)
     hipLaunchKernelGGL((paged_decode_merge_kernel<ET, D, G>), dim3(grid.y, grid.x), dim3(256), 0,
                        s, p);
