@@ -59,7 +59,7 @@ def decode_kernel_name() -> str:
     VA_DECODE_KERNEL=general selects the general one."""
     if os.environ.get("VA_DECODE_KERNEL") == "general":
         return "paged_decode_kernel<BF16,128,2,aligned>"
-    return "paged_decode_mfma_kernel<BF16,128,2>"
+    return "paged_decode_mfma_kernel<BF16,128,2,false,false>"
 
 
 def timed_graph(fn, steps: int, warmup: int, stream: torch.cuda.Stream):
