@@ -249,6 +249,45 @@ def test_tts_fused_write_matches_reference_order(dev):
     assert _err(out[:, :, 0], ref) <= 2e-2
 
 
+@pytest.mark.parametrize("B", [6, 40])
+def test_tts_api_page16_mask_and_fused_write(dev, B):
+    # The TTS caller's shape of a tick (qwen_tts_outer_varlen.py:392-447): HND
+    # pool with 16-token pages, int64 page table padded with -1, a key mask
+    # padded with True up to kernel_seq_len, and the current rows written in
+    # the same launch.  16-token pages take the matrix-core kernel; B=6 splits
+    # contexts into partitions, B=40 runs one partition per (request, kv head).
+    g = torch.Generator().manual_seed(70 + B)
+    page, hq, hkv, d = 16, 16, 8, 128
+    lens = torch.randint(1, 520, (B,), generator=g)
+    need = [(int(n) + page - 1) // page for n in lens]
+    pages = sum(need) + 3
+    perm = torch.randperm(pages, generator=g).tolist()
+    width = max(need) + 2
+    table = torch.full((B, width), -1, dtype=torch.long)
+    cur = 0
+    for i, m in enumerate(need):
+        table[i, :m] = torch.tensor(perm[cur:cur + m])
+        cur += m
+    kp = (torch.randn(pages, hkv, page, d, generator=g) * 0.5).to(torch.bfloat16)
+    vp = torch.randn(pages, hkv, page, d, generator=g).to(torch.bfloat16)
+    q = torch.randn(B, hq, 1, d, generator=g).to(torch.bfloat16)
+    nk = torch.randn(B, hkv, 1, d, generator=g).to(torch.bfloat16)
+    nv = torch.randn(B, hkv, 1, d, generator=g).to(torch.bfloat16)
+    kernel_seq_len = 640
+    valid = torch.ones(B, kernel_seq_len, dtype=torch.bool)
+    valid[:, :520] = torch.rand(B, 520, generator=g) < 0.85
+    ek, ev = oracle.write_current_kv(kp, vp, table, lens, nk[:, :, 0], nv[:, :, 0])
+    kd, vd = kp.to(dev), vp.to(dev)
+    out = paged_attention_decode(q.to(dev), kd, vd, table.to(dev), lens.to(dev), valid.to(dev),
+                                 new_key=nk.to(dev), new_value=nv.to(dev), validate=False,
+                                 kernel_seq_len=kernel_seq_len, kernel_page_count=width + 4)
+    torch.cuda.synchronize()
+    assert torch.equal(kd.cpu(), ek) and torch.equal(vd.cpu(), ev)
+    ref = oracle.paged_decode(q[:, :, 0], ek, ev, table, lens, d ** -0.5, layout=oracle.HND,
+                              valid_mask=valid)
+    assert _err(out[:, :, 0], ref) <= 2e-2
+
+
 def test_tts_known_answer_integer_values(dev):
     # test_qwen_tts_outer_varlen_attention.py:54-66 at head_dim 64: constant K/V -> exact.
     kp = torch.zeros(8, 1, 2, 64)
