@@ -59,6 +59,10 @@ def test_decode_rejects_bad_geometry():
     assert lib.va_paged_decode(ctypes.byref(args), None) == -1
     assert "multiple" in N.last_error()
     args.num_heads = 8
+    args.valid_mask, args.valid_len, args.valid_stride_seq = 16, 64, -64
+    assert lib.va_paged_decode(ctypes.byref(args), None) == -1
+    assert "valid_stride_seq" in N.last_error()
+    args.valid_mask = None
     args.head_dim = 96  # unsupported head_dim reaches the dispatcher only after host checks
     args.q_stride_seq = 1  # not a 16-byte multiple
     assert lib.va_paged_decode(ctypes.byref(args), None) == -1

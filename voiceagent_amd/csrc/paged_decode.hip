@@ -181,6 +181,8 @@ extern "C" int va_paged_decode(const va_decode_args* a, void* stream) {
                "va_paged_decode: new_slots_dtype");
   VA_CHECK_ARG(a->max_seq_len >= 0, "va_paged_decode: max_seq_len < 0");
   VA_CHECK_ARG(a->table_width >= 0, "va_paged_decode: table_width < 0");
+  VA_CHECK_ARG(a->valid_mask == nullptr || (a->valid_len >= 0 && a->valid_stride_seq >= 0),
+               "va_paged_decode: valid_len and valid_stride_seq must be non-negative");
   const int64_t strides[] = {a->q_stride_seq,        a->q_stride_head,        a->out_stride_seq,
                              a->out_stride_head,     a->pool.stride_block,    a->pool.stride_slot,
                              a->pool.stride_head,    a->new_k_stride_seq,     a->new_k_stride_head,
