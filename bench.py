@@ -128,14 +128,49 @@ def bench_decode(args, dev, stream):
                              split_tokens=args.split)
 
     ms, _ = timed_graph(step, args.steps, args.warmup, stream)
-    per_layer_bytes = workloads.decode_bytes(lens) + 2 * B * workloads.HKV * \
-        workloads.HEAD_DIM * 2 + 4 * B
+    per_layer_bytes = decode_launch_bytes(lens)
     us_layer = ms * 1000.0 / layers
     gbs = per_layer_bytes / (us_layer * 1e-6) / 1e9
     log(f"[decode] {ms:.3f} ms/step, {us_layer:.2f} us/layer, {gbs:.0f} GB/s "
         f"({per_layer_bytes / 1e6:.2f} MB/layer)")
     return dict(ms=ms, us_layer=us_layer, gbs=gbs, bytes_layer=per_layer_bytes, lens=lens,
                 batch=batch, qs=qs, nks=nks, nvs=nvs)
+
+
+def decode_launch_bytes(lens) -> int:
+    """Algorithmic bytes of one config-2 decode launch (attention + fused store)."""
+    B = len(lens)
+    return workloads.decode_bytes(lens) + 2 * B * workloads.HKV * workloads.HEAD_DIM * 2 + 4 * B
+
+
+def bench_floor(args, dev, stream):
+    """HBM read floor for config 2's launch size: a plain contiguous read of
+    the same number of bytes in one launch (va_hbm_read_probe), 28 launches
+    per graph replay on distinct 2 GiB-buffer windows (cold, past the 256 MB
+    MALL), at several grid sizes; the fastest grid is reported."""
+    nbytes = decode_launch_bytes(workloads.cfg2_lens(0)) // 16 * 16
+    layers = workloads.LAYERS
+    stride = (nbytes + 65535) // 65536 * 65536
+    buf = torch.ones(stride * layers, dtype=torch.uint8, device=dev)
+    sink = torch.zeros(4096, dtype=torch.int32, device=dev)
+    views = [buf[i * stride:i * stride + nbytes] for i in range(layers)]
+    per_grid = {}
+    for wgs in (256, 512, 1024, 2048):
+        def step(wgs=wgs):
+            for v in views:
+                ops.hbm_read_probe(v, wgs, sink)
+
+        ms, _ = timed_graph(step, args.steps, args.warmup, stream)
+        per_grid[wgs] = ms * 1000.0 / layers
+    wgs, us = min(per_grid.items(), key=lambda kv: kv[1])
+    gbs = nbytes / (us * 1e-6) / 1e9
+    log(f"[floor] plain read of {nbytes / 1e6:.2f} MB per launch: {us:.2f} us/launch, "
+        f"{gbs:.0f} GB/s ({wgs} workgroups; " +
+        ", ".join(f"{k}: {v:.2f}" for k, v in per_grid.items()) + ")")
+    return {"us_per_launch": round(us, 2), "gbs": round(gbs, 1), "bytes": nbytes,
+            "workgroups": wgs, "us_by_grid": {str(k): round(v, 2) for k, v in per_grid.items()},
+            "note": "va_hbm_read_probe: plain contiguous read of config 2's per-launch bytes, "
+                    "28 cold launches per graph replay"}
 
 
 def bench_kv_format(args, dev, stream, dec):
@@ -431,7 +466,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--split", type=int, default=0, help="decode split_tokens (0 = auto)")
     ap.add_argument("--only", choices=["decode", "prefill", "encoder", "store", "longform",
-                                       "prologue", "kvformat", "all"],
+                                       "prologue", "kvformat", "floor", "all"],
                     default="all")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
@@ -465,6 +500,9 @@ def main():
     if args.only == "longform":
         print(json.dumps({"longform": bench_longform(args, dev, stream)}))
         return
+    if args.only == "floor":
+        print(json.dumps({"hbm_read_floor": bench_floor(args, dev, stream)}))
+        return
     dec = bench_decode(args, dev, stream)
     if args.only == "store":
         print(json.dumps({"store": bench_store(args, dev, stream, dec)}))
@@ -480,6 +518,7 @@ def main():
         extra["store"] = bench_store(args, dev, stream, dec)
         extra["qwen3_prologue"] = bench_prologue(args, dev, stream, dec)
         extra["kv_format_hnd"] = bench_kv_format(args, dev, stream, dec)
+        extra["hbm_read_floor"] = bench_floor(args, dev, stream)
         pre = bench_prefill(args, dev, stream)
         enc = bench_encoder(args, dev, stream)
         extra["prefill"] = {"us_per_layer": round(pre["us_layer"], 2),

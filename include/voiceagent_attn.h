@@ -239,6 +239,15 @@ typedef struct va_varlen_args {
  * fused), or non-causal block-diagonal (audio encoder windows). */
 int va_varlen_attention(const va_varlen_args* args, void* stream);
 
+/* ---------------------------------------------------------- diagnostics */
+/* Plain streaming read of `bytes` contiguous bytes at `src` (16-byte aligned)
+ * in one launch of `workgroups` 512-lane workgroups, each reading one
+ * contiguous slice; `sink` needs `workgroups` 32-bit words and is, in
+ * practice, never written.  No counterpart in the reference: it measures the
+ * HBM read floor that the decode kernel's bandwidth is read against (bench.py
+ * --only floor). */
+int va_hbm_read_probe(const void* src, size_t bytes, int workgroups, void* sink, void* stream);
+
 /* ----------------------------------------------------------------- misc */
 const char* va_last_error(void);
 int va_abi_version(void);

@@ -189,6 +189,7 @@ SIGNATURES = {
     "va_paged_decode": (c_int32, [ctypes.POINTER(DecodeArgs), c_void_p]),
     "va_varlen_attention": (c_int32, [ctypes.POINTER(VarlenArgs), c_void_p]),
     "va_qk_norm_rope": (c_int32, [ctypes.POINTER(QkNormRopeArgs), c_void_p]),
+    "va_hbm_read_probe": (c_int32, [c_void_p, c_size_t, ctypes.c_int, c_void_p, c_void_p]),
     "va_last_error": (ctypes.c_char_p, []),
     "va_abi_version": (c_int32, []),
 }

@@ -451,3 +451,21 @@ def varlen_attention(
 
 def default_scale(head_dim: int) -> float:
     return 1.0 / math.sqrt(head_dim)
+
+
+# --------------------------------------------------------------- diagnostics
+def hbm_read_probe(buf: torch.Tensor, workgroups: int, sink: torch.Tensor) -> None:
+    """Plain streaming read of the contiguous GPU tensor `buf` in one launch of
+    `workgroups` workgroups (va_hbm_read_probe): the HBM read floor that the
+    decode kernel's bandwidth is read against.  `sink` is an int32 tensor of
+    at least `workgroups` elements; nothing is computed."""
+    device = _check_gpu(buf, sink)
+    _require(buf.is_contiguous(), "the probe reads a contiguous tensor")
+    nbytes = buf.numel() * buf.element_size()
+    _require(buf.data_ptr() % 16 == 0 and nbytes % 16 == 0,
+             "the probe reads 16-byte aligned whole 16-byte words")
+    _require(sink.dtype == torch.int32 and sink.numel() >= workgroups,
+             "sink must be int32 with one element per workgroup")
+    N.check("va_hbm_read_probe",
+            N.lib().va_hbm_read_probe(buf.data_ptr(), nbytes, int(workgroups), sink.data_ptr(),
+                                      N.current_stream(device)))
