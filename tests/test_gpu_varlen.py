@@ -282,6 +282,71 @@ def test_paged_attention_layer_hnd_pool_matches_nhd(dev, fuse):
         assert torch.equal(a, b)
 
 
+def test_paged_attention_layer_with_qwen3_prologue(dev):
+    """forward(q, k, v, prologue=...) takes the raw projections and applies
+    Qwen3's q/k RMSNorm + RoPE itself (qk_norm_rope before a prefill, inside
+    the launch for a decode step).  Outputs and pools equal, bit for bit, a
+    layer fed the normalised and rotated q and k, and match the oracle."""
+    g = torch.Generator().manual_seed(25)
+    bs, nb = 16, 256
+    lens = [37, 90, 5]
+    width = 12
+    perm = torch.randperm(nb, generator=g).tolist()
+    tables = [perm[i * width:(i + 1) * width] for i in range(len(lens))]
+    table_t = torch.tensor(tables, dtype=torch.int32, device=dev)
+    wq = (torch.rand(128, generator=g) + 0.5).to(torch.bfloat16)
+    wk = (torch.rand(128, generator=g) + 0.5).to(torch.bfloat16)
+    cs = oracle.rope_cache(128, 1024, 1_000_000.0)
+    layers, pools = [], []
+    for _ in range(2):
+        layer = PagedAttention(16, 128, 128 ** -0.5, 8)
+        kv = torch.zeros(2, nb, bs, 8, 128, dtype=torch.bfloat16, device=dev)
+        layer.k_cache, layer.v_cache = kv[0], kv[1]
+        layers.append(layer)
+        pools.append(kv)
+
+    def run(q, k, v, pos, ctx):
+        pro = ops.QKPrologue(wq.to(dev), wk.to(dev), 1e-6, cs.to(dev), pos.to(dev))
+        qn, kn = ops.qk_norm_rope(q.to(dev), k.to(dev), pro)
+        with attention_context(ctx):
+            fused = layers[0](q.to(dev), k.to(dev), v.to(dev), prologue=pro)
+            plain = layers[1](qn, kn, v.to(dev))
+        torch.cuda.synchronize()
+        assert torch.equal(fused, plain)
+        assert torch.equal(pools[0], pools[1])
+        return fused, oracle.qk_norm_rope(q, k, pos, wq, wk, 1e-6, cs)
+
+    total = sum(lens)
+    q = torch.randn(total, 16, 128, generator=g).to(torch.bfloat16)
+    k = torch.randn(total, 8, 128, generator=g).to(torch.bfloat16)
+    v = torch.randn(total, 8, 128, generator=g).to(torch.bfloat16)
+    pos = torch.cat([torch.arange(n) for n in lens])
+    slots = [tables[s][p // bs] * bs + p % bs for s, n in enumerate(lens) for p in range(n)]
+    cu = _cu(lens)
+    ctx = AttentionContext(cu.to(dev), cu.to(dev), max(lens), max(lens),
+                           torch.tensor(slots, dtype=torch.int32, device=dev), table_t)
+    out, (rq, rk) = run(q, k, v, pos, ctx)
+    assert _err(out, oracle.varlen_attention(rq, rk, v, cu, cu, 128 ** -0.5, True)) <= TOL
+    kc, vc = oracle.store_kvcache(rk, v, torch.zeros(nb, bs, 8, 128, dtype=torch.bfloat16),
+                                  torch.zeros(nb, bs, 8, 128, dtype=torch.bfloat16),
+                                  torch.tensor(slots))
+    for step in range(2):
+        lens = [n + 1 for n in lens]
+        qd = torch.randn(3, 16, 128, generator=g).to(torch.bfloat16)
+        kd = torch.randn(3, 8, 128, generator=g).to(torch.bfloat16)
+        vd = torch.randn(3, 8, 128, generator=g).to(torch.bfloat16)
+        dpos = torch.tensor(lens) - 1
+        dslots = [tables[s][(n - 1) // bs] * bs + (n - 1) % bs for s, n in enumerate(lens)]
+        ctx = AttentionContext(torch.arange(4, dtype=torch.int32, device=dev),
+                               _cu(lens).to(dev), 1, max(lens),
+                               torch.tensor(dslots, dtype=torch.int32, device=dev), table_t)
+        out, (rq, rk) = run(qd, kd, vd, dpos, ctx)
+        kc, vc = oracle.store_kvcache(rk, vd, kc, vc, torch.tensor(dslots))
+        ref = oracle.paged_decode(rq, kc, vc, torch.tensor(tables), torch.tensor(lens),
+                                  128 ** -0.5)
+        assert _err(out, ref) <= TOL, step
+
+
 def test_paged_attention_layer_profiling_pass_without_cache(dev):
     g = torch.Generator().manual_seed(6)
     layer = PagedAttention(16, 128, 128 ** -0.5, 8)

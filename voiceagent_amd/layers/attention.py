@@ -21,6 +21,15 @@ is the pool slot of query token i's position (model_runner.py:202-204,
 graph_runner.py:165-168); ``fuse_store = False`` restores the reference's
 store-then-attend order with two launches.
 
+``forward(q, k, v, prologue=...)`` also takes Qwen3's q/k prologue
+(:class:`voiceagent_amd.ops.QKPrologue`: the q_norm / k_norm weights and eps,
+the rotary cos/sin cache and the tokens' positions): q and k are then the
+raw projections, and the layer applies RMSNorm and RoPE to them as
+Qwen3Attention.forward does before calling attention (models/qwen3.py:42-48).
+A decode batch with the fused store applies it inside the decode launch; any
+other batch runs ``ops.qk_norm_rope`` first.  Qwen3Attention then passes the
+prologue instead of calling q_norm, k_norm and rotary_emb itself.
+
 ``kv_layout`` names the pool layout: ``"nhd"`` ``[num_blocks, block_size,
 Hkv, D]`` as model_runner.py:116-131 allocates it (the default), or
 ``"hnd"`` ``[num_blocks, Hkv, block_size, D]``, in which one (block, kv head)
@@ -74,8 +83,15 @@ class PagedAttention(nn.Module):
         self.k_cache = torch.tensor([])
         self.v_cache = torch.tensor([])
 
-    def forward(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> torch.Tensor:
+    def forward(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                prologue: ops.QKPrologue | None = None) -> torch.Tensor:
         context = get_attention_context()
+        num_seqs = context.cu_seqlens_k.numel() - 1
+        decode = context.max_seqlen_q == 1 and q.shape[0] == num_seqs
+        if prologue is not None:
+            if self.k_cache.numel() and decode and self.fuse_store:
+                return self._decode_fused(q, k, v, context, prologue)
+            q, k = ops.qk_norm_rope(q, k, prologue)
         if not self.k_cache.numel():
             # Memory-profiling pass before the cache exists: packed causal varlen.
             return ops.varlen_attention(
@@ -89,23 +105,9 @@ class PagedAttention(nn.Module):
                 scale=self.scale,
                 causal=True,
             )
-        num_seqs = context.cu_seqlens_k.numel() - 1
-        if context.max_seqlen_q == 1 and q.shape[0] == num_seqs:
+        if decode:
             if self.fuse_store:
-                return ops.paged_decode(
-                    q,
-                    self.k_cache,
-                    self.v_cache,
-                    context.block_tables,
-                    context.cu_seqlens_k,
-                    lens_cumulative=True,
-                    max_seq_len=context.max_seqlen_k,
-                    scale=self.scale,
-                    layout=self.kv_layout,
-                    new_k=k,
-                    new_v=v,
-                    new_slots=context.slot_mapping,
-                )
+                return self._decode_fused(q, k, v, context, None)
             self._store(k, v, context.slot_mapping)
             return ops.paged_decode(
                 q,
@@ -150,6 +152,24 @@ class PagedAttention(nn.Module):
             v_cache=self.v_cache,
             block_tables=context.block_tables,
             layout=self.kv_layout,
+        )
+
+    def _decode_fused(self, q, k, v, context, prologue: ops.QKPrologue | None) -> torch.Tensor:
+        """One launch: (prologue,) store of the new rows, paged decode."""
+        return ops.paged_decode(
+            q,
+            self.k_cache,
+            self.v_cache,
+            context.block_tables,
+            context.cu_seqlens_k,
+            lens_cumulative=True,
+            max_seq_len=context.max_seqlen_k,
+            scale=self.scale,
+            layout=self.kv_layout,
+            new_k=k,
+            new_v=v,
+            new_slots=context.slot_mapping,
+            prologue=prologue,
         )
 
     def _store(self, k: torch.Tensor, v: torch.Tensor, slot_mapping: torch.Tensor) -> None:
