@@ -173,6 +173,63 @@ def bench_floor(args, dev, stream):
                     "28 cold launches per graph replay"}
 
 
+TTS_SHAPES = ((1, 600), (4, 1500), (8, 300))
+
+
+def bench_tts(args, dev, stream):
+    """The TTS talker's decode through the drop-in paged_attention_decode
+    (qwen_tts_paged_attention.py:383-516 signature): HND pool with 16-token
+    pages, int64 page table and lengths, a key mask over kernel_seq_len tokens
+    (left padding: the first 5% of each row masked, then random holes) and the
+    current rows written in the same launch; 16 query / 8 kv heads, head_dim
+    128, 28 layers with their own pools per graph replay.  Each shape is timed
+    with the mask and without it."""
+    from voiceagent_amd.agent import paged_attention_decode
+
+    hq, hkv, d, page, layers = workloads.HQ, workloads.HKV, workloads.HEAD_DIM, 16, workloads.LAYERS
+    g = torch.Generator(device=dev).manual_seed(11)
+    res = {}
+    for B, L in TTS_SHAPES:
+        need = (L + page - 1) // page
+        pages = B * need + 8
+        perm = torch.randperm(pages, device=dev, generator=g)
+        table = perm[:B * need].view(B, need).to(torch.long)
+        lens = torch.full((B,), L, dtype=torch.long, device=dev)
+        kernel_seq_len = (L + 127) // 128 * 128
+        mask = torch.rand(B, kernel_seq_len, device=dev, generator=g) < 0.9
+        mask[:, :L // 20] = False
+        kps = [(torch.randn(pages, hkv, page, d, device=dev, generator=g) * 0.5).to(torch.bfloat16)
+               for _ in range(layers)]
+        vps = [(torch.randn(pages, hkv, page, d, device=dev, generator=g) * 0.5).to(torch.bfloat16)
+               for _ in range(layers)]
+        q = torch.randn(layers, B, hq, 1, d, device=dev, generator=g).to(torch.bfloat16)
+        nk = (torch.randn(layers, B, hkv, 1, d, device=dev, generator=g) * 0.5).to(torch.bfloat16)
+        nv = (torch.randn(layers, B, hkv, 1, d, device=dev, generator=g) * 0.5).to(torch.bfloat16)
+        # K/V rows read, q read, out written, tables and lengths, mask bytes up to
+        # each length, current rows read and written.
+        nbytes = (B * L * hkv * d * 2 * 2 + 2 * B * hq * d * 2 + B * need * 8 + B * 8 +
+                  B * L + 2 * 2 * B * hkv * d * 2)
+        row = {}
+        for use_mask in (True, False):
+            def step(use_mask=use_mask):
+                for i in range(layers):
+                    paged_attention_decode(q[i], kps[i], vps[i], table, lens,
+                                           mask if use_mask else None, new_key=nk[i],
+                                           new_value=nv[i], kernel_seq_len=kernel_seq_len,
+                                           kernel_page_count=need, validate=False)
+
+            ms, _ = timed_graph(step, args.steps, args.warmup, stream)
+            row["mask" if use_mask else "no_mask"] = ms * 1000.0 / layers
+        us = row["mask"]
+        gbs = nbytes / (us * 1e-6) / 1e9
+        log(f"[tts] B={B} L={L}: {us:.2f} us/layer with the key mask ({gbs:.0f} GB/s, "
+            f"{nbytes / 1e6:.2f} MB/layer), {row['no_mask']:.2f} without")
+        res[f"B{B}_L{L}"] = {"us_per_layer": round(us, 2), "gbs": round(gbs, 1),
+                             "frac": round(gbs / HBM_PEAK_GBS, 4), "bytes_per_layer": nbytes,
+                             "us_per_layer_no_mask": round(row["no_mask"], 2)}
+    return res
+
+
 def bench_kv_format(args, dev, stream, dec):
     """Config 2 decode with the pools in the head-major layout [num_blocks, Hkv,
     block_size, D] (one (block, kv head) is a contiguous 4 KiB run) instead of
@@ -466,7 +523,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--split", type=int, default=0, help="decode split_tokens (0 = auto)")
     ap.add_argument("--only", choices=["decode", "prefill", "encoder", "store", "longform",
-                                       "prologue", "kvformat", "floor", "all"],
+                                       "prologue", "kvformat", "floor", "tts", "all"],
                     default="all")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
@@ -503,6 +560,9 @@ def main():
     if args.only == "floor":
         print(json.dumps({"hbm_read_floor": bench_floor(args, dev, stream)}))
         return
+    if args.only == "tts":
+        print(json.dumps({"tts_decode": bench_tts(args, dev, stream)}))
+        return
     dec = bench_decode(args, dev, stream)
     if args.only == "store":
         print(json.dumps({"store": bench_store(args, dev, stream, dec)}))
@@ -519,6 +579,7 @@ def main():
         extra["qwen3_prologue"] = bench_prologue(args, dev, stream, dec)
         extra["kv_format_hnd"] = bench_kv_format(args, dev, stream, dec)
         extra["hbm_read_floor"] = bench_floor(args, dev, stream)
+        extra["tts_decode"] = bench_tts(args, dev, stream)
         pre = bench_prefill(args, dev, stream)
         enc = bench_encoder(args, dev, stream)
         extra["prefill"] = {"us_per_layer": round(pre["us_layer"], 2),
