@@ -82,6 +82,13 @@ def test_decode_workspace_sizing():
     args.num_seqs = 2
     n = lib.va_paged_decode_workspace_bytes(ctypes.byref(args))
     assert n > 0
+    # ...unless no context can hold more than 192 KiB of one kv head's K/V
+    # (384 tokens at head_dim 128 in bf16): those stream whole, unmerged.
+    args.max_seq_len = 384
+    assert lib.va_paged_decode_workspace_bytes(ctypes.byref(args)) == 0
+    args.max_seq_len = 385
+    assert lib.va_paged_decode_workspace_bytes(ctypes.byref(args)) > 0
+    args.max_seq_len = 600
     args.max_seq_len = 16384
     assert lib.va_paged_decode_workspace_bytes(ctypes.byref(args)) >= n
     args.split_tokens = 1  # an explicit split is honoured (rounded up to a workgroup round)

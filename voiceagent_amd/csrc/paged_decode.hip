@@ -62,6 +62,18 @@ static int mfma_unit_for(int D) {
   }
 }
 
+static int elem_bytes_of(int dtype);
+
+// Contexts up to this many bytes of one kv head's K and V rows stay whole
+// (see plan_decode).
+constexpr int64_t kNoSplitBytes = 192 * 1024;
+
+// Context length whose K and V rows of one kv head fill kNoSplitBytes.
+static int nosplit_tokens_for(const va_decode_args* a) {
+  const int64_t per_token = (int64_t)a->head_dim * elem_bytes_of(a->dtype) * 2;
+  return per_token > 0 ? (int)(kNoSplitBytes / per_token) : 0;
+}
+
 static DecodePlan plan_decode(const va_decode_args* a) {
   DecodePlan pl{};
   const int G = a->num_kv_heads > 0 ? a->num_heads / a->num_kv_heads : 1;
@@ -78,9 +90,17 @@ static DecodePlan plan_decode(const va_decode_args* a) {
     // size each workgroup derives from its own context length
     // (partition_tokens), so a max_seq_len that is only an upper bound (a
     // decode graph captured at max_model_len) still spreads short contexts.
+    // When no pair can hold more than kNoSplitBytes of K/V (max_seq_len
+    // tokens), nothing is split: one CU streams that much (~64 GB/s) in less
+    // time than a split, its merge launch and the lost early start-up cost.
+    // Measured at 16 query / 8 kv heads, head_dim 128: 300-token contexts
+    // run faster whole (B = 8: 6.8 against 8.7 us), 600-token contexts
+    // faster split (B = 1: 7.5 against 8.8 us).  A max_seq_len that is only
+    // an upper bound (max_model_len) keeps the split.
     const int64_t cus = current_device_cus();
     const int64_t want = pairs >= cus ? 1 : cus / (pairs > 0 ? pairs : 1);
     int64_t parts = want;
+    if ((int64_t)max_len <= nosplit_tokens_for(a)) parts = 1;
     const int64_t by_len = (max_len + kDynGrain - 1) / kDynGrain;
     if (parts > by_len) parts = by_len;
     if (parts > kMaxParts) parts = kMaxParts;
