@@ -386,3 +386,24 @@ def test_split_merge_with_many_pairs(dev):
     ref = oracle.paged_decode(q, kp, vp, table, lens, d ** -0.5)
     assert B * hkv > 65536
     assert _err(out, ref) <= 2e-2
+
+
+@pytest.mark.parametrize("max_seq_len", [40960, 65536])
+def test_longest_context_with_fused_store(dev, max_seq_len):
+    # Qwen3's longest position (max_position_embeddings 40960) in one sequence
+    # beside short ones, the current rows stored in the same launch; with the
+    # exact maximum and with the bound a decode graph captured at 65536 passes.
+    lens = [40960, 1, 17, 300]
+    nb = sum((n + 15) // 16 for n in lens) + 8
+    b = workloads.make_decode_batch(lens, num_blocks=nb, dtype=torch.bfloat16, kv_std=0.5,
+                                    device=dev, seed=40)
+    k0, v0 = b.k_pools[0].cpu(), b.v_pools[0].cpu()
+    out = ops.paged_decode(b.q, b.k_pools[0], b.v_pools[0], b.block_tables, b.context_lens,
+                           max_seq_len=max_seq_len, scale=b.scale, new_k=b.new_k,
+                           new_v=b.new_v, new_slots=b.slot_mapping)
+    ek, ev = oracle.store_kvcache(b.new_k.cpu(), b.new_v.cpu(), k0, v0, b.slot_mapping.cpu())
+    torch.cuda.synchronize()
+    assert torch.equal(b.k_pools[0].cpu(), ek) and torch.equal(b.v_pools[0].cpu(), ev)
+    ref = oracle.paged_decode(b.q.cpu(), ek, ev, b.block_tables.cpu(), b.context_lens.cpu(),
+                              b.scale)
+    assert _err(out, ref) <= 2e-2

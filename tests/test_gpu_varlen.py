@@ -373,3 +373,15 @@ def test_varlen_self_attention_layer(dev):
     layer = VarlenSelfAttention(14, 64, 64 ** -0.5)
     out = layer(q.to(dev), k.to(dev), v.to(dev), cu.to(dev), widest)
     assert _err(out, oracle.varlen_attention(q, k, v, cu, cu, 0.125, False)) <= TOL
+
+
+def test_causal_prompt_of_4096_tokens(dev):
+    # The reference's default max_model_len (config.py:138) as one causal
+    # prompt, packed with a short one and a single token: 64 query blocks.
+    lens = [4096, 333, 1]
+    b = workloads.make_varlen_batch(lens, 16, 8, 128, causal=True, seed=44)
+    out = ops.varlen_attention(b.q.to(dev), b.k.to(dev), b.v.to(dev), b.cu_seqlens.to(dev),
+                               b.cu_seqlens.to(dev), b.max_seqlen, b.max_seqlen, scale=b.scale,
+                               causal=True)
+    ref = oracle.varlen_attention(b.q, b.k, b.v, b.cu_seqlens, b.cu_seqlens, b.scale, True)
+    assert _err(out, ref) <= TOL
