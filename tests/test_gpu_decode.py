@@ -407,3 +407,25 @@ def test_longest_context_with_fused_store(dev, max_seq_len):
     ref = oracle.paged_decode(b.q.cpu(), ek, ev, b.block_tables.cpu(), b.context_lens.cpu(),
                               b.scale)
     assert _err(out, ref) <= 2e-2
+
+
+def test_concurrent_decodes_on_two_streams_keep_their_partials(dev):
+    # Two split-context decodes in flight at once on two streams (an ASR
+    # decode beside a TTS decode, say): each stream has its own partials
+    # workspace, so neither reads the other's.
+    streams = [torch.cuda.Stream(dev), torch.cuda.Stream(dev)]
+    batches = [workloads.make_decode_batch([900, 1200, 700], num_blocks=512, dtype=torch.bfloat16,
+                                           kv_std=0.5, device=dev, seed=60 + i) for i in range(2)]
+    refs = [_oracle_for(b) for b in batches]
+    outs = [torch.empty_like(b.q) for b in batches]
+    torch.cuda.synchronize()
+    for rep in range(20):
+        for s, b, o in zip(streams, batches, outs):
+            with torch.cuda.stream(s):
+                ops.paged_decode(b.q, b.k_pools[0], b.v_pools[0], b.block_tables,
+                                 b.context_lens, max_seq_len=b.max_seq_len, scale=b.scale, out=o)
+        torch.cuda.synchronize()
+        for o, r in zip(outs, refs):
+            assert _err(o, r) <= 2e-2, rep
+    ws = [ops._WORKSPACES[(dev.index or 0, s.cuda_stream)] for s in streams]
+    assert ws[0].data_ptr() != ws[1].data_ptr()

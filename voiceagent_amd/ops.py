@@ -217,7 +217,7 @@ def qk_norm_rope(
 
 
 # -------------------------------------------------------------------- decode
-_WORKSPACES: dict[int, torch.Tensor] = {}
+_WORKSPACES: dict[tuple[int, int], torch.Tensor] = {}
 
 
 def _device_index(device: torch.device) -> int:
@@ -225,12 +225,14 @@ def _device_index(device: torch.device) -> int:
 
 
 def decode_workspace(device: torch.device, nbytes: int) -> torch.Tensor | None:
-    """Partial-result workspace shared by decode launches on one device (no
-    initialisation needed; grows by doubling; launches sharing it are
-    ordered on one stream)."""
+    """Partial-result workspace of the decode launches on the current stream
+    of `device` (no initialisation needed; grows by doubling).  One per
+    stream: launches on one stream are ordered, while decodes on two streams
+    (an ASR engine and a TTS talker, say) may run at once and must not share
+    their partials."""
     if nbytes == 0:
         return None
-    key = _device_index(device)
+    key = (_device_index(device), torch.cuda.current_stream(device).cuda_stream)
     ws = _WORKSPACES.get(key)
     if ws is None or ws.numel() < nbytes:
         size = max(nbytes, 0 if ws is None else 2 * ws.numel())
@@ -240,7 +242,8 @@ def decode_workspace(device: torch.device, nbytes: int) -> torch.Tensor | None:
 
 
 def reserve_decode_workspace(device: torch.device, nbytes: int) -> None:
-    """Allocate the decode workspace up front (before HIP graph capture)."""
+    """Allocate the decode workspace of the current stream up front (before
+    HIP graph capture on that stream)."""
     decode_workspace(torch.device(device), nbytes)
 
 
