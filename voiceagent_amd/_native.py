@@ -247,5 +247,9 @@ def ptr(t: torch.Tensor | None) -> int | None:
 
 
 def call(name: str, args, device: torch.device) -> None:
+    """Launch `name` on the current stream of `device`, with `device` made the
+    current HIP device for the call (the library plans launches for, and
+    launches on, the current device)."""
     fn = getattr(lib(), name)
-    check(name, fn(ctypes.byref(args), current_stream(device)))
+    with torch.cuda.device(device):
+        check(name, fn(ctypes.byref(args), current_stream(device)))

@@ -345,7 +345,8 @@ def paged_decode(
     if prologue is not None:
         pro_struct = _prologue_struct(prologue, d, B)  # kept alive through the call
         args.prologue = ctypes.pointer(pro_struct)
-    nbytes = N.lib().va_paged_decode_workspace_bytes(ctypes.byref(args))
+    with torch.cuda.device(device):  # the split plan depends on the device's CU count
+        nbytes = N.lib().va_paged_decode_workspace_bytes(ctypes.byref(args))
     ws = decode_workspace(device, nbytes)
     if ws is not None:
         args.workspace = ws.data_ptr()
@@ -469,6 +470,7 @@ def hbm_read_probe(buf: torch.Tensor, workgroups: int, sink: torch.Tensor) -> No
              "the probe reads 16-byte aligned whole 16-byte words")
     _require(sink.dtype == torch.int32 and sink.numel() >= workgroups,
              "sink must be int32 with one element per workgroup")
-    N.check("va_hbm_read_probe",
-            N.lib().va_hbm_read_probe(buf.data_ptr(), nbytes, int(workgroups), sink.data_ptr(),
-                                      N.current_stream(device)))
+    with torch.cuda.device(device):
+        N.check("va_hbm_read_probe",
+                N.lib().va_hbm_read_probe(buf.data_ptr(), nbytes, int(workgroups),
+                                          sink.data_ptr(), N.current_stream(device)))
