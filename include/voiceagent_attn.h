@@ -217,6 +217,9 @@ typedef struct va_varlen_args {
   const int32_t* cu_seqlens_k; /* [num_seqs + 1]                          */
   int32_t num_seqs, total_q;
   int32_t num_heads, num_kv_heads, head_dim;
+  /* max_seqlen_q sizes the launch's query blocks and must be at least every
+   * q_len (as flash_attn_varlen_func requires): query rows past it are not
+   * computed.  max_seqlen_k is not read (key ranges come from cu_seqlens_k). */
   int32_t max_seqlen_q, max_seqlen_k;
   int32_t causal;         /* 1: bottom-right aligned causal mask          */
   float scale;

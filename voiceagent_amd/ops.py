@@ -381,6 +381,8 @@ def varlen_attention(
     j < k_len - q_len are read through ``block_tables``; the others from
     ``k``/``v`` rows aligned with the queries (all from the pool if ``k`` is
     None).  ``slot_mapping`` fuses store_kvcache of k/v into the same launch.
+    ``max_seqlen_q`` must be at least every q_len, as for flash-attn: it sizes
+    the launch, and query rows past it are not computed.
     """
     device = _check_gpu(q, k, v, cu_seqlens_q, cu_seqlens_k, k_cache, v_cache, block_tables,
                         slot_mapping, out)
