@@ -88,7 +88,14 @@ def test_decode_workspace_sizing():
     assert lib.va_paged_decode_workspace_bytes(ctypes.byref(args)) == 0
     args.max_seq_len = 385
     assert lib.va_paged_decode_workspace_bytes(ctypes.byref(args)) > 0
-    args.max_seq_len = 600
+    # With 128 pairs a split would make 2 partitions per pair: the bound
+    # scales to 8 / 2 times that, 1536 tokens.
+    args.num_seqs = 16
+    args.max_seq_len = 1536
+    assert lib.va_paged_decode_workspace_bytes(ctypes.byref(args)) == 0
+    args.max_seq_len = 1537
+    assert lib.va_paged_decode_workspace_bytes(ctypes.byref(args)) > 0
+    args.num_seqs, args.max_seq_len = 2, 600
     args.max_seq_len = 16384
     assert lib.va_paged_decode_workspace_bytes(ctypes.byref(args)) >= n
     args.split_tokens = 1  # an explicit split is honoured (rounded up to a workgroup round)

@@ -90,17 +90,20 @@ static DecodePlan plan_decode(const va_decode_args* a) {
     // size each workgroup derives from its own context length
     // (partition_tokens), so a max_seq_len that is only an upper bound (a
     // decode graph captured at max_model_len) still spreads short contexts.
-    // When no pair can hold more than kNoSplitBytes of K/V (max_seq_len
-    // tokens), nothing is split: one CU streams that much (~64 GB/s) in less
-    // time than a split, its merge launch and the lost early start-up cost.
-    // Measured at 16 query / 8 kv heads, head_dim 128: 300-token contexts
-    // run faster whole (B = 8: 6.8 against 8.7 us), 600-token contexts
-    // faster split (B = 1: 7.5 against 8.8 us).  A max_seq_len that is only
-    // an upper bound (max_model_len) keeps the split.
+    // When no pair can hold more than kNoSplitBytes * 8 / min(parts, 8) of
+    // K/V (max_seq_len tokens), nothing is split: one CU streams that much
+    // in less time than a split, its merge launch and the lost early
+    // start-up cost, and with few partitions per pair (many pairs) the whole
+    // launch is already near the HBM rate.  Fitted on 16 query / 8 kv heads,
+    // head_dim 128, B = 1..16 x 128..1024 tokens (worst choice 0.24 us off
+    // the better one): B <= 4 splits above 384 tokens, B = 8 (4 partitions)
+    // above 768, B = 16 (2 partitions) above 1536.  A max_seq_len that is
+    // only an upper bound (max_model_len) keeps the split.
     const int64_t cus = current_device_cus();
     const int64_t want = pairs >= cus ? 1 : cus / (pairs > 0 ? pairs : 1);
     int64_t parts = want;
-    if ((int64_t)max_len <= nosplit_tokens_for(a)) parts = 1;
+    if (parts > 1 && (int64_t)max_len * (parts < 8 ? parts : 8) <= (int64_t)nosplit_tokens_for(a) * 8)
+      parts = 1;
     const int64_t by_len = (max_len + kDynGrain - 1) / kDynGrain;
     if (parts > by_len) parts = by_len;
     if (parts > kMaxParts) parts = kMaxParts;
