@@ -95,6 +95,13 @@ def test_decode_workspace_sizing():
     assert lib.va_paged_decode_workspace_bytes(ctypes.byref(args)) == 0
     args.max_seq_len = 1537
     assert lib.va_paged_decode_workspace_bytes(ctypes.byref(args)) > 0
+    # The bound is in bytes: fp32 rows halve it in tokens (192 at 8 partitions).
+    args.num_seqs, args.dtype = 2, N.DTYPE_CODES[torch.float32]
+    args.max_seq_len = 192
+    assert lib.va_paged_decode_workspace_bytes(ctypes.byref(args)) == 0
+    args.max_seq_len = 193
+    assert lib.va_paged_decode_workspace_bytes(ctypes.byref(args)) > 0
+    args.dtype = N.DTYPE_CODES[torch.bfloat16]
     args.num_seqs, args.max_seq_len = 2, 600
     args.max_seq_len = 16384
     assert lib.va_paged_decode_workspace_bytes(ctypes.byref(args)) >= n
