@@ -2,7 +2,9 @@
 oracle: dtype, head_dim, group size, kv heads, block size (including block
 sizes that take the general decode kernel), pool layout, index dtypes,
 cumulative lengths, key mask, fused current-row write, and exact or
-upper-bound max_seq_len.  Each case is small enough for the CPU oracle.
+upper-bound max_seq_len; causal and bidirectional varlen; and causal prefill
+over a paged prefix with the store fused.  Each case is small enough for the
+CPU oracle.
 
 Tolerances as elsewhere: 1e-5 for fp32 inputs, 2e-2 for 16-bit inputs.
 """
@@ -111,3 +113,35 @@ def test_random_varlen_options(dev, seed):
     ref = oracle.varlen_attention(q, k, v, cu, cu, d ** -0.5, causal)
     err = (out.float().cpu() - ref.float()).abs().max().item()
     assert err <= TOL[dtype], (seed, err)
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_random_paged_prefix_with_fused_store(dev, seed):
+    # Prefix-cache hits (keys from the pool) and new tokens (from k/v, stored
+    # to their slots in the same launch), random geometry and block size.
+    from tests.test_gpu_varlen import _paged_prefill_case
+
+    r = random.Random(7000 + seed)
+    hkv = r.choice([1, 2, 8])
+    hq = hkv * r.choice([1, 2, 4, 8])
+    d = r.choice([64, 128])
+    bs = r.choice([16, 32])
+    spec = tuple((r.choice([0, 0, r.randint(1, 300)]), r.randint(1, 260))
+                 for _ in range(r.choice([1, 3, 9])))
+    slot_dtype = r.choice([torch.int32, torch.int64])
+    print(f"paged prefix case {seed}: hq={hq} hkv={hkv} d={d} bs={bs} spec={spec}", flush=True)
+    nb = sum(-(-(p + n) // bs) for p, n in spec) + 4
+    c = _paged_prefill_case(seed=8000 + seed, bs=bs, nb=nb, hq=hq, hkv=hkv, d=d,
+                            slot_dtype=slot_dtype, spec=spec)
+    kd, vd = c["kp"].to(dev), c["vp"].to(dev)
+    out = ops.varlen_attention(c["q"].to(dev), c["k"].to(dev), c["v"].to(dev), c["cu_q"].to(dev),
+                               c["cu_k"].to(dev), c["max_q"], c["max_k"], scale=d ** -0.5,
+                               causal=True, k_cache=kd, v_cache=vd,
+                               block_tables=c["table"].to(dev), slot_mapping=c["slots"].to(dev))
+    ek, ev = oracle.store_kvcache(c["k"], c["v"], c["kp"], c["vp"], c["slots"])
+    torch.cuda.synchronize()
+    assert torch.equal(kd.cpu(), ek) and torch.equal(vd.cpu(), ev)
+    ref = oracle.varlen_attention(c["q"], c["k"], c["v"], c["cu_q"], c["cu_k"], d ** -0.5, True,
+                                  k_cache=c["kp"], v_cache=c["vp"], block_tables=c["table"])
+    err = (out.float().cpu() - ref.float()).abs().max().item()
+    assert err <= 2e-2, (seed, err)
