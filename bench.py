@@ -143,33 +143,76 @@ def decode_launch_bytes(lens) -> int:
     return workloads.decode_bytes(lens) + 2 * B * workloads.HKV * workloads.HEAD_DIM * 2 + 4 * B
 
 
+PROBE_MODES = {"plain": 0, "nt": 1, "lds_dma": 2}  # include/voiceagent_bench.h
+_BENCH_LIB = None
+
+
+def bench_lib():
+    """libvoiceagent_bench.so (include/voiceagent_bench.h): bench-only probes,
+    apart from the drop-in library."""
+    global _BENCH_LIB
+    if _BENCH_LIB is None:
+        import ctypes
+
+        from voiceagent_amd.build import BENCH_LIB_PATH
+
+        lib = ctypes.CDLL(str(BENCH_LIB_PATH))
+        lib.va_bench_hbm_read.restype = ctypes.c_int
+        lib.va_bench_hbm_read.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int,
+                                          ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
+        lib.va_bench_last_error.restype = ctypes.c_char_p
+        lib.va_bench_last_error.argtypes = []
+        _BENCH_LIB = lib
+    return _BENCH_LIB
+
+
+def hbm_read(buf: torch.Tensor, workgroups: int, mode: str, sink: torch.Tensor) -> None:
+    """Stream the contiguous GPU tensor `buf` once in one launch of
+    `workgroups` workgroups through load path `mode` (va_bench_hbm_read); `sink`
+    is an int32 tensor of at least `workgroups` elements, never written."""
+    if not (buf.is_cuda and buf.is_contiguous() and sink.dtype == torch.int32 and
+            sink.numel() >= workgroups):
+        raise ValueError("hbm_read needs a contiguous GPU tensor and an int32 sink per workgroup")
+    nbytes = buf.numel() * buf.element_size()
+    rc = bench_lib().va_bench_hbm_read(buf.data_ptr(), nbytes, int(workgroups), PROBE_MODES[mode],
+                                       sink.data_ptr(), torch.cuda.current_stream().cuda_stream)
+    if rc != 0:
+        raise ValueError(bench_lib().va_bench_last_error().decode())
+
+
 def bench_floor(args, dev, stream):
-    """HBM read floor for config 2's launch size: a plain contiguous read of
-    the same number of bytes in one launch (va_hbm_read_probe), 28 launches
-    per graph replay on distinct 2 GiB-buffer windows (cold, past the 256 MB
-    MALL), at several grid sizes; the fastest grid is reported."""
+    """HBM read floor for config 2's launch size: a contiguous read of the
+    same number of bytes in one launch (va_bench_hbm_read), 28 launches per
+    graph replay on distinct windows of a 1.3 GB buffer (cold, past the 256 MB
+    MALL), through three load paths (plain loads, non-temporal loads, the
+    decode's non-temporal LDS DMA) at several grid sizes; the fastest
+    (path, grid) is reported."""
     nbytes = decode_launch_bytes(workloads.cfg2_lens(0)) // 16 * 16
     layers = workloads.LAYERS
     stride = (nbytes + 65535) // 65536 * 65536
     buf = torch.ones(stride * layers, dtype=torch.uint8, device=dev)
     sink = torch.zeros(4096, dtype=torch.int32, device=dev)
     views = [buf[i * stride:i * stride + nbytes] for i in range(layers)]
-    per_grid = {}
-    for wgs in (256, 512, 1024, 2048):
-        def step(wgs=wgs):
-            for v in views:
-                ops.hbm_read_probe(v, wgs, sink)
+    table = {}
+    for mode in PROBE_MODES:
+        for wgs in (256, 512, 1024, 2048):
+            def step(wgs=wgs, mode=mode):
+                for v in views:
+                    hbm_read(v, wgs, mode, sink)
 
-        ms, _ = timed_graph(step, args.steps, args.warmup, stream)
-        per_grid[wgs] = ms * 1000.0 / layers
-    wgs, us = min(per_grid.items(), key=lambda kv: kv[1])
+            ms, _ = timed_graph(step, args.steps, args.warmup, stream)
+            table[(mode, wgs)] = ms * 1000.0 / layers
+        log(f"[floor] {mode}: " + ", ".join(f"{w}: {table[(mode, w)]:.2f}"
+                                            for w in (256, 512, 1024, 2048)) + " us/launch")
+    (mode, wgs), us = min(table.items(), key=lambda kv: kv[1])
     gbs = nbytes / (us * 1e-6) / 1e9
-    log(f"[floor] plain read of {nbytes / 1e6:.2f} MB per launch: {us:.2f} us/launch, "
-        f"{gbs:.0f} GB/s ({wgs} workgroups; " +
-        ", ".join(f"{k}: {v:.2f}" for k, v in per_grid.items()) + ")")
-    return {"us_per_launch": round(us, 2), "gbs": round(gbs, 1), "bytes": nbytes,
-            "workgroups": wgs, "us_by_grid": {str(k): round(v, 2) for k, v in per_grid.items()},
-            "note": "va_hbm_read_probe: plain contiguous read of config 2's per-launch bytes, "
+    log(f"[floor] best: {mode} at {wgs} workgroups, {us:.2f} us/launch for "
+        f"{nbytes / 1e6:.2f} MB, {gbs:.0f} GB/s ({gbs / HBM_PEAK_GBS:.3f} of peak)")
+    return {"us_per_launch": round(us, 2), "gbs": round(gbs, 1),
+            "frac": round(gbs / HBM_PEAK_GBS, 4), "bytes": nbytes, "mode": mode,
+            "workgroups": wgs,
+            "us_by_mode_grid": {f"{m}/{w}": round(t, 2) for (m, w), t in table.items()},
+            "note": "va_bench_hbm_read: contiguous read of config 2's per-launch bytes, "
                     "28 cold launches per graph replay"}
 
 

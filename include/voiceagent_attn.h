@@ -39,7 +39,7 @@
 extern "C" {
 #endif
 
-#define VA_ATTN_ABI_VERSION 2
+#define VA_ATTN_ABI_VERSION 3
 
 /* status codes */
 #define VA_OK 0
@@ -186,6 +186,15 @@ typedef struct va_decode_args {
    * rotated at positions[b] before attention, and new_k likewise before it
    * is written and attended (its position is also positions[b]). */
   const va_qk_prologue* prologue;
+  /* Optional bounds of the attended keys, as the TTS kernel's MAX_SEQ_LEN
+   * (kernel_seq_len) and num_page_slots (kernel_page_count) bound them
+   * (qwen_tts_paged_attention.py:223-241): tokens at or past key_limit are
+   * not attended (0: no bound), and block-table columns at or past
+   * table_read_width read as block 0 when attending (0: table_width).  The
+   * current row is still written at len - 1, through the table's own entry
+   * (qwen_tts_paged_attention.py:182-221). */
+  int32_t key_limit;
+  int32_t table_read_width;
 } va_decode_args;
 
 /* Bytes of workspace va_paged_decode needs for these arguments (the
@@ -241,15 +250,6 @@ typedef struct va_varlen_args {
  * alignment (prefill, optionally over a paged prefix and with the store
  * fused), or non-causal block-diagonal (audio encoder windows). */
 int va_varlen_attention(const va_varlen_args* args, void* stream);
-
-/* ---------------------------------------------------------- diagnostics */
-/* Plain streaming read of `bytes` contiguous bytes at `src` (16-byte aligned)
- * in one launch of `workgroups` 512-lane workgroups, each reading one
- * contiguous slice; `sink` needs `workgroups` 32-bit words and is, in
- * practice, never written.  No counterpart in the reference: it measures the
- * HBM read floor that the decode kernel's bandwidth is read against (bench.py
- * --only floor). */
-int va_hbm_read_probe(const void* src, size_t bytes, int workgroups, void* sink, void* stream);
 
 /* ----------------------------------------------------------------- misc */
 const char* va_last_error(void);

@@ -1,0 +1,37 @@
+/*
+ * voiceagent_bench.h — bench-only diagnostics (libvoiceagent_bench.so).
+ *
+ * Not part of the drop-in ABI (include/voiceagent_attn.h) and with no
+ * counterpart in the reference: bench.py uses it to measure the HBM read
+ * floor that the decode kernel's bandwidth is read against.
+ */
+#ifndef VOICEAGENT_BENCH_H
+#define VOICEAGENT_BENCH_H
+
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* load paths of va_bench_hbm_read */
+#define VA_PROBE_PLAIN 0    /* plain 16-byte loads, 4 in flight per lane          */
+#define VA_PROBE_NT 1       /* non-temporal 16-byte loads, 8 in flight per lane   */
+#define VA_PROBE_LDS_DMA 2  /* non-temporal global_load_lds_dwordx4, 16 KiB in    */
+                            /* flight per wave (the decode kernel's load path)    */
+
+/* Streaming read of `bytes` contiguous bytes at `src` (16-byte aligned) in one
+ * launch of `workgroups` 512-lane workgroups, each reading one contiguous
+ * slice through load path `mode`.  `sink` needs `workgroups` 32-bit words and
+ * is, in practice, never written.  Returns 0, or -1 on a bad argument (the
+ * message is in va_bench_last_error()). */
+int va_bench_hbm_read(const void* src, size_t bytes, int workgroups, int mode, void* sink,
+                      void* stream);
+
+const char* va_bench_last_error(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* VOICEAGENT_BENCH_H */

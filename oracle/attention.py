@@ -116,24 +116,36 @@ def _masked_softmax_av(scores: torch.Tensor, values: torch.Tensor, keep: torch.T
 
 
 def paged_decode(q, k_cache, v_cache, block_tables, context_lens, scale, *, layout: str = NHD,
-                 valid_mask=None, compute_dtype=torch.float32):
+                 valid_mask=None, key_limit=None, table_read_width=None,
+                 compute_dtype=torch.float32):
     """One query token per sequence over a paged pool.  q: [B, Hq, D] -> [B, Hq, D].
 
     Per row (qwen_tts_paged_attention.py:363-379): gather the first L rows
     through the table, repeat_interleave the kv heads by G = Hq / Hkv, then
     softmax(q . K^T * scale) @ V.  ``valid_mask[b, t]`` masks token t when t is
-    inside the mask's width (tokens past it count as valid).
+    inside the mask's width (tokens past it count as valid); a masked token's
+    value row counts as 0, as the Triton kernel loads it (:258-265), so that a
+    non-finite value there does not reach the output.  ``key_limit`` and
+    ``table_read_width`` are the Triton kernel's MAX_SEQ_LEN and
+    num_page_slots (:223-241): tokens at or past key_limit are not attended,
+    and table columns at or past table_read_width read as block 0.
     """
     B, hq, d = q.shape
     outs = []
     for b in range(B):
         length = int(context_lens[b])
+        if key_limit is not None:
+            length = min(length, int(key_limit))
         if length <= 0:
             outs.append(torch.zeros(1, hq, d, dtype=compute_dtype))
             continue
         pos = torch.arange(length)
-        keys = gather_rows(k_cache, block_tables[b], pos, layout).to(compute_dtype)
-        values = gather_rows(v_cache, block_tables[b], pos, layout).to(compute_dtype)
+        table_row = block_tables[b]
+        if table_read_width is not None and table_row.shape[0] > table_read_width:
+            table_row = table_row.clone()
+            table_row[int(table_read_width):] = 0
+        keys = gather_rows(k_cache, table_row, pos, layout).to(compute_dtype)
+        values = gather_rows(v_cache, table_row, pos, layout).to(compute_dtype)
         group = hq // keys.shape[1]
         keys = keys.permute(1, 0, 2).repeat_interleave(group, dim=0)  # [Hq, L, D]
         values = values.permute(1, 0, 2).repeat_interleave(group, dim=0)
@@ -145,6 +157,7 @@ def paged_decode(q, k_cache, v_cache, block_tables, context_lens, scale, *, layo
             keep = torch.ones(length, dtype=torch.bool)
             n = min(width, length)
             keep[:n] = valid_mask[b, :n].bool()
+            values = values.masked_fill(~keep.view(1, length, 1), 0.0)
             keep = keep.view(1, 1, length)
         outs.append(_masked_softmax_av(scores, values, keep).transpose(0, 1))
     return torch.cat(outs, dim=0)

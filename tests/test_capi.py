@@ -27,7 +27,7 @@ def test_header_functions_are_exported():
     assert declared == set(N.SIGNATURES), declared ^ set(N.SIGNATURES)
     for name in declared:
         assert hasattr(lib, name), name
-    assert lib.va_abi_version() == 2
+    assert lib.va_abi_version() == 3
 
 
 @pytest.mark.parametrize(
@@ -145,3 +145,18 @@ def test_tts_api_contract_errors_on_cpu():
         paged_attention_decode(q, kp, kp, page_table, seq_lens, new_key=torch.zeros(2, 2, 1, 4))
     with pytest.raises(PagedAttentionKernelError, match="GPU"):
         paged_attention_decode(q, kp, kp, page_table, seq_lens)
+
+
+def test_bench_library_is_apart_from_the_drop_in_library():
+    # The read-floor probe lives in libvoiceagent_bench.so, declared in
+    # include/voiceagent_bench.h; the drop-in library exports no diagnostics.
+    import bench
+
+    lib = N.lib()
+    assert not hasattr(lib, "va_hbm_read_probe") and not hasattr(lib, "va_bench_hbm_read")
+    blib = bench.bench_lib()
+    assert hasattr(blib, "va_bench_hbm_read") and hasattr(blib, "va_bench_last_error")
+    rc = blib.va_bench_hbm_read(16, 15, 1, 0, 16, None)  # unaligned size: host-side reject
+    assert rc == -1 and b"aligned" in blib.va_bench_last_error()
+    rc = blib.va_bench_hbm_read(16, 16, 1, 7, 16, None)
+    assert rc == -1 and b"mode" in blib.va_bench_last_error()

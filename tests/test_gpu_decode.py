@@ -331,7 +331,7 @@ def test_graph_capture_replays_match_eager(dev):
         ops.paged_decode(b.q, b.k_pools[0], b.v_pools[0], b.block_tables, cu,
                          lens_cumulative=True, max_seq_len=max_len, scale=b.scale, out=out)
 
-    step()  # allocates the workspace outside the capture
+    step()  # eager warm-up (256 pairs run unsplit: no workspace on either stream)
     torch.cuda.synchronize()
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):

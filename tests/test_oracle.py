@@ -223,6 +223,56 @@ def test_decode_fully_masked_row_is_zero():
     assert torch.count_nonzero(out) == 0
 
 
+def test_decode_tts_bounds_closed_forms():
+    # key_limit (the Triton kernel's MAX_SEQ_LEN = kernel_seq_len) and
+    # table_read_width (num_page_slots = kernel_page_count) against closed
+    # forms: with all keys zero the softmax is uniform, so the output is the
+    # mean of the attended value rows.
+    bs, hkv, d = 4, 2, 8
+    kp = torch.zeros(16, bs, hkv, d, dtype=torch.float64)
+    vp = torch.zeros(16, bs, hkv, d, dtype=torch.float64)
+    for blk in range(16):
+        for off in range(bs):
+            vp[blk, off] = 100.0 * blk + off  # row value names its slot
+    table = torch.tensor([[5, 9, 3, 12, 7]])
+    q = torch.randn(1, 4, d, dtype=torch.float64)
+    vals = lambda blocks: [100.0 * blk + off for blk in blocks for off in range(bs)]  # noqa: E731
+    real = vals([5, 9, 3, 12, 7])
+    # key_limit 9 of a 17-token row: the mean of the first nine slots
+    out = oracle.paged_decode(q, kp, vp, table, torch.tensor([17]), 0.5, key_limit=9,
+                              compute_dtype=torch.float64)
+    assert torch.allclose(out, torch.full_like(out, sum(real[:9]) / 9))
+    # table_read_width 2: tokens of columns 2.. read block 0 (values 0..3)
+    out = oracle.paged_decode(q, kp, vp, table, torch.tensor([18]), 0.5, table_read_width=2,
+                              compute_dtype=torch.float64)
+    expect = (sum(real[:8]) + sum(vals([0, 0, 0])[:10])) / 18
+    assert torch.allclose(out, torch.full_like(out, expect))
+
+
+def test_decode_masked_nonfinite_values_are_dropped():
+    # A masked token whose K and V rows are non-finite counts as absent:
+    # the same as attending the unmasked tokens only (gathered apart here).
+    gen = torch.Generator().manual_seed(12)
+    kp, vp = _rand_pool(gen)
+    table = torch.tensor([[3, 8, 1]])
+    q = torch.randn(1, 4, 8, generator=gen, dtype=torch.float64)
+    valid = torch.tensor([[True, False, True, True, False, True, True, True, True, False, True]])
+    kbad, vbad = kp.clone(), vp.clone()
+    for t in (1, 4, 9):
+        kbad[table[0, t // 4], t % 4] = float("nan")
+        vbad[table[0, t // 4], t % 4] = float("inf")
+    out = oracle.paged_decode(q, kbad, vbad, table, torch.tensor([11]), 0.4, valid_mask=valid,
+                              compute_dtype=torch.float64)
+    keep = [t for t in range(11) if valid[0, t]]
+    keys = oracle.gather_rows(kp, table[0], torch.tensor(keep))  # [n, Hkv, D]
+    values = oracle.gather_rows(vp, table[0], torch.tensor(keep))
+    ref = torch.nn.functional.scaled_dot_product_attention(
+        q[0].unsqueeze(1), keys.permute(1, 0, 2).repeat_interleave(2, 0),
+        values.permute(1, 0, 2).repeat_interleave(2, 0), scale=0.4)
+    assert torch.isfinite(out).all()
+    assert torch.allclose(out[0], ref[:, 0])
+
+
 def test_store_kvcache_closed_form():
     gen = torch.Generator().manual_seed(10)
     kc = torch.randn(6, 4, 2, 8, generator=gen)

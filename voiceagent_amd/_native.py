@@ -20,7 +20,7 @@ VA_OK = 0
 VA_BF16, VA_F16, VA_F32 = 0, 1, 2
 VA_I32, VA_I64 = 0, 1
 VA_LENS_PER_SEQ, VA_LENS_CUMULATIVE = 0, 1
-ABI_VERSION = 2  # VA_ATTN_ABI_VERSION of the header these structs mirror
+ABI_VERSION = 3  # VA_ATTN_ABI_VERSION of the header these structs mirror
 
 DTYPE_CODES = {torch.bfloat16: VA_BF16, torch.float16: VA_F16, torch.float32: VA_F32}
 INDEX_CODES = {torch.int32: VA_I32, torch.int64: VA_I64}
@@ -142,6 +142,8 @@ class DecodeArgs(ctypes.Structure):
         ("workspace", c_void_p),
         ("workspace_bytes", c_size_t),
         ("prologue", ctypes.POINTER(QkPrologue)),
+        ("key_limit", c_int32),
+        ("table_read_width", c_int32),
     ]
 
 
@@ -189,7 +191,6 @@ SIGNATURES = {
     "va_paged_decode": (c_int32, [ctypes.POINTER(DecodeArgs), c_void_p]),
     "va_varlen_attention": (c_int32, [ctypes.POINTER(VarlenArgs), c_void_p]),
     "va_qk_norm_rope": (c_int32, [ctypes.POINTER(QkNormRopeArgs), c_void_p]),
-    "va_hbm_read_probe": (c_int32, [c_void_p, c_size_t, ctypes.c_int, c_void_p, c_void_p]),
     "va_last_error": (ctypes.c_char_p, []),
     "va_abi_version": (c_int32, []),
 }

@@ -13,9 +13,13 @@ Differences that callers can observe:
   HIP kernel (there is no torch fallback in this build).
 * ``block_n``/``num_warps`` are checked as the reference checks them and
   otherwise ignored (the kernel picks its own split).
-* ``kernel_seq_len``/``kernel_page_count`` only bound the launch grid; the
-  page table is not copied to a padded tensor — columns past its width read
-  as page 0 inside the kernel, which is what the reference's zero padding
+* ``kernel_seq_len``/``kernel_page_count`` bound the attended keys as the
+  Triton kernel's ``MAX_SEQ_LEN``/``num_page_slots`` do (:223-241): tokens at
+  or past ``kernel_seq_len`` are not attended and table columns at or past
+  ``kernel_page_count`` read as page 0, while the current row is still
+  written at ``seq_len - 1`` through the table's own entry (:182-221).  The
+  page table is not copied to a padded tensor: columns past its width read as
+  page 0 inside the kernel, which is what the reference's zero padding
   (:458-465) produces.
 * The fused current-row write uses the row's register copy for position
   ``seq_len - 1`` instead of re-reading the pool, so there is no
@@ -185,6 +189,8 @@ def paged_attention_decode(
             new_k=None if new_key is None else new_key[:, :, 0, :],
             new_v=None if new_value is None else new_value[:, :, 0, :],
             out=torch.empty_like(query)[:, :, 0, :],
+            key_limit=kernel_seq_len,
+            table_read_width=kernel_page_count,
         )
     except ops.AttentionArgumentError as exc:
         raise PagedAttentionKernelError(str(exc)) from exc

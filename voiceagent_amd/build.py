@@ -2,8 +2,10 @@
 
 ``build_native()`` runs ``hipcc --offload-arch=gfx950`` on every ``csrc/*.hip``
 file (in parallel, one object per file) and links them into
-``voiceagent_amd/lib/libvoiceagent_attn.so``.  It always recompiles; the GPU
-box loads the library built here and never compiles.
+``voiceagent_amd/lib/libvoiceagent_attn.so``, the drop-in library.  The
+bench-only diagnostics in ``csrc/bench/*.hip`` (include/voiceagent_bench.h)
+link into ``voiceagent_amd/lib/libvoiceagent_bench.so``.  It always
+recompiles; the GPU box loads the libraries built here and never compiles.
 """
 
 from __future__ import annotations
@@ -20,6 +22,7 @@ LIB_DIR = PACKAGE_DIR / "lib"
 OBJ_DIR = PACKAGE_DIR / "_build"
 LIB_NAME = "libvoiceagent_attn.so"
 LIB_PATH = LIB_DIR / LIB_NAME
+BENCH_LIB_PATH = LIB_DIR / "libvoiceagent_bench.so"
 OFFLOAD_ARCH = "gfx950"
 
 # Packed-fp32 VALU ops are disabled for every HIP object: ordinary float code
@@ -68,34 +71,45 @@ def _compile(hipcc: str, src: Path, obj: Path) -> tuple[Path, str]:
     return obj, log
 
 
+def _link(hipcc: str, objects: list[Path], target: Path) -> None:
+    tmp = target.with_suffix(".so.tmp")
+    cmd = [hipcc, f"--offload-arch={OFFLOAD_ARCH}", "-shared", "-fPIC", "-Wl,--no-undefined",
+           "-o", str(tmp)]
+    cmd += [str(o) for o in objects]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"link of {target.name} failed:\n{proc.stdout}{proc.stderr}")
+    os.replace(tmp, target)
+
+
 def build_native(verbose: bool = False) -> Path:
-    """Compile every HIP source and link the shared library; returns its path."""
+    """Compile every HIP source and link both shared libraries; returns the
+    drop-in library's path."""
     hipcc = _hipcc()
     sources = sorted(CSRC_DIR.glob("*.hip"))
+    bench_sources = sorted((CSRC_DIR / "bench").glob("*.hip"))
     if not sources:
         raise RuntimeError(f"no HIP sources under {CSRC_DIR}")
     OBJ_DIR.mkdir(parents=True, exist_ok=True)
     LIB_DIR.mkdir(parents=True, exist_ok=True)
-    jobs = max(1, min(len(sources), int(os.environ.get("MAX_JOBS", os.cpu_count() or 4))))
-    objects = []
+    every = sources + bench_sources
+    jobs = max(1, min(len(every), int(os.environ.get("MAX_JOBS", os.cpu_count() or 4))))
+    objects: dict[Path, Path] = {}
     with concurrent.futures.ThreadPoolExecutor(max_workers=jobs) as pool:
-        futures = [
-            pool.submit(_compile, hipcc, src, OBJ_DIR / (src.stem + ".o")) for src in sources
-        ]
-        for fut in futures:
+        futures = {
+            src: pool.submit(_compile, hipcc, src,
+                             OBJ_DIR / (("bench_" if src in bench_sources else "") + src.stem + ".o"))
+            for src in every
+        }
+        for src, fut in futures.items():
             obj, log = fut.result()
-            objects.append(obj)
+            objects[src] = obj
             if verbose and log.strip():
                 print(log)
-    tmp = LIB_PATH.with_suffix(".so.tmp")
-    cmd = [hipcc, f"--offload-arch={OFFLOAD_ARCH}", "-shared", "-fPIC", "-o", str(tmp)]
-    cmd += [str(o) for o in objects]
-    proc = subprocess.run(cmd, capture_output=True, text=True)
-    if proc.returncode != 0:
-        raise RuntimeError(f"link failed:\n{proc.stdout}{proc.stderr}")
-    os.replace(tmp, LIB_PATH)
+    _link(hipcc, [objects[s] for s in sources], LIB_PATH)
+    _link(hipcc, [objects[s] for s in bench_sources], BENCH_LIB_PATH)
     if verbose:
-        print(f"built {LIB_PATH}")
+        print(f"built {LIB_PATH} and {BENCH_LIB_PATH.name}")
     return LIB_PATH
 
 

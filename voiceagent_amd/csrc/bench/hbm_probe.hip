@@ -1,0 +1,125 @@
+// HBM read floor: a streaming read of `bytes` contiguous bytes in one launch,
+// through one of three load paths.  It gives the decode kernel's bandwidth a
+// machine-measured reference: what one launch reading the same number of
+// bytes, with nothing else to do, reaches on this GPU.  Bench-only (built
+// into libvoiceagent_bench.so, declared in include/voiceagent_bench.h); it
+// has no counterpart in the reference.
+//
+// Workgroup w (8 wave64s) reads the contiguous slice [w per_wg, (w + 1)
+// per_wg) of 16-byte words:
+//   VA_PROBE_PLAIN    each lane keeps four plain 16-byte loads in flight;
+//   VA_PROBE_NT       each lane keeps eight non-temporal 16-byte loads in
+//                     flight;
+//   VA_PROBE_LDS_DMA  1 KiB units of the slice go round robin to the waves,
+//                     each copied by one non-temporal global_load_lds_dwordx4
+//                     into a 16-unit LDS ring per wave, 16 KiB in flight per
+//                     wave (the decode kernel's load path and depth).
+// Register loads are XOR-folded and the fold is written to sink[w] only when
+// it equals a fixed value, so the loads cannot be removed and, in practice,
+// nothing is written; the DMA path writes only LDS.
+#include <stdarg.h>
+#include <stdio.h>
+
+#include "../common.h"
+#include "../../../include/voiceagent_bench.h"
+
+namespace va {
+namespace {
+
+thread_local char g_bench_error[256] = "";
+
+int bench_fail(const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_bench_error, sizeof(g_bench_error), fmt, ap);
+  va_end(ap);
+  return -1;
+}
+
+constexpr int kProbeThreads = 512;
+constexpr uint32_t kProbeMagic = 0x9e3779b9u;
+
+template <int kUnroll, bool kNt>
+__global__ __launch_bounds__(kProbeThreads) void hbm_read_probe_kernel(
+    const uint4* __restrict__ src, int64_t nvec, int64_t per_wg, uint32_t* sink) {
+  const int64_t beg = (int64_t)blockIdx.x * per_wg;
+  const int64_t end = beg + per_wg < nvec ? beg + per_wg : nvec;
+  uint32_t acc = 0;
+  for (int64_t i = beg + threadIdx.x; i < end; i += kUnroll * kProbeThreads) {
+    uint4 w[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const int64_t j = i + (int64_t)u * kProbeThreads;
+      if (j < end)
+        w[u] = kNt ? ld16_nt(src + j) : src[j];
+      else
+        w[u] = make_uint4(0u, 0u, 0u, 0u);
+    }
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) acc ^= w[u].x ^ w[u].y ^ w[u].z ^ w[u].w;
+  }
+  if (acc == kProbeMagic) sink[blockIdx.x] = acc;
+}
+
+constexpr int kDmaRing = 16;  // 1 KiB units in flight per wave
+
+__global__ __launch_bounds__(kProbeThreads) void hbm_read_probe_dma_kernel(const char* src,
+                                                                           int64_t nvec,
+                                                                           int64_t per_wg) {
+  __shared__ __align__(1024) char ring[kProbeThreads / 64 * kDmaRing * 1024];
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int64_t beg = (int64_t)blockIdx.x * per_wg;
+  const int64_t end = beg + per_wg < nvec ? beg + per_wg : nvec;
+  const int64_t units = end > beg ? (end - beg + 63) / 64 : 0;  // 64 words per unit
+  const uint32_t lds = __builtin_amdgcn_readfirstlane(
+      (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)(ring +
+                                                                     wave * kDmaRing * 1024));
+  int issued = 0;
+  for (int64_t u = wave; u < units; u += kProbeThreads / 64) {
+    // Lane l copies word beg + 64 u + l; past the slice it re-reads the
+    // slice's last word, so every address stays inside the buffer.
+    int64_t word = beg + 64 * u + lane;
+    if (word >= end) word = end - 1;
+    const char* base = uniform_ptr(src + (beg + 64 * u) * 16);
+    const uint32_t off = (uint32_t)((word - (beg + 64 * u)) * 16);
+    dma16_nt(off, base, lds + (uint32_t)((issued % kDmaRing) * 1024));
+    ++issued;
+    if (issued >= kDmaRing) wait_vmcnt<kDmaRing - 1>();
+  }
+  wait_vmcnt<0>();
+}
+
+}  // namespace
+}  // namespace va
+
+extern "C" int va_bench_hbm_read(const void* src, size_t bytes, int workgroups, int mode,
+                                 void* sink, void* stream) {
+  using namespace va;
+  if (src == nullptr || sink == nullptr) return bench_fail("va_bench_hbm_read: null pointer");
+  if ((uintptr_t)src % 16 != 0 || bytes % 16 != 0)
+    return bench_fail("va_bench_hbm_read: src and bytes must be 16-byte aligned");
+  if (workgroups < 1 || workgroups > 65536)
+    return bench_fail("va_bench_hbm_read: workgroups must be in [1, 65536]");
+  if (mode != VA_PROBE_PLAIN && mode != VA_PROBE_NT && mode != VA_PROBE_LDS_DMA)
+    return bench_fail("va_bench_hbm_read: unknown mode %d", mode);
+  if (bytes == 0) return 0;
+  const int64_t nvec = (int64_t)(bytes / 16);
+  const int64_t per_wg = (nvec + workgroups - 1) / workgroups;
+  const hipStream_t s = (hipStream_t)stream;
+  const dim3 grid((unsigned)workgroups), block(kProbeThreads);
+  const uint4* v = reinterpret_cast<const uint4*>(src);
+  uint32_t* out = reinterpret_cast<uint32_t*>(sink);
+  if (mode == VA_PROBE_PLAIN)
+    hipLaunchKernelGGL((hbm_read_probe_kernel<4, false>), grid, block, 0, s, v, nvec, per_wg, out);
+  else if (mode == VA_PROBE_NT)
+    hipLaunchKernelGGL((hbm_read_probe_kernel<8, true>), grid, block, 0, s, v, nvec, per_wg, out);
+  else
+    hipLaunchKernelGGL(hbm_read_probe_dma_kernel, grid, block, 0, s,
+                       reinterpret_cast<const char*>(src), nvec, per_wg);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return bench_fail("va_bench_hbm_read: launch failed: %s", hipGetErrorString(e));
+  return 0;
+}
+
+extern "C" const char* va_bench_last_error(void) { return va::g_bench_error; }

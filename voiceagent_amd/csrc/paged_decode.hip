@@ -80,7 +80,8 @@ static DecodePlan plan_decode(const va_decode_args* a) {
   int unit = use_mfma_decode(a) ? mfma_unit_for(a->head_dim)
                                 : decode_unit_for(a->dtype, a->head_dim, G);
   if (unit <= 0) unit = 128;
-  const int max_len = a->max_seq_len > 0 ? a->max_seq_len : 1;
+  int max_len = a->max_seq_len > 0 ? a->max_seq_len : 1;
+  if (a->key_limit > 0 && a->key_limit < max_len) max_len = a->key_limit;
   int P = a->split_tokens;
   const int64_t pairs = (int64_t)a->num_seqs * a->num_kv_heads;
   if (P <= 0) {
@@ -204,6 +205,8 @@ extern "C" int va_paged_decode(const va_decode_args* a, void* stream) {
                "va_paged_decode: new_slots_dtype");
   VA_CHECK_ARG(a->max_seq_len >= 0, "va_paged_decode: max_seq_len < 0");
   VA_CHECK_ARG(a->table_width >= 0, "va_paged_decode: table_width < 0");
+  VA_CHECK_ARG(a->key_limit >= 0 && a->table_read_width >= 0,
+               "va_paged_decode: key_limit and table_read_width must be non-negative");
   VA_CHECK_ARG(a->valid_mask == nullptr || (a->valid_len >= 0 && a->valid_stride_seq >= 0),
                "va_paged_decode: valid_len and valid_stride_seq must be non-negative");
   const int64_t strides[] = {a->q_stride_seq,        a->q_stride_head,        a->out_stride_seq,
@@ -258,7 +261,11 @@ extern "C" int va_paged_decode(const va_decode_args* a, void* stream) {
   p.table = a->block_tables;
   p.t_sb = a->table_stride_seq;
   p.table_i64 = a->table_dtype == VA_I64;
-  p.table_width = a->table_width;
+  p.table_width_full = a->table_width;
+  p.table_width = (a->table_read_width > 0 && a->table_read_width < a->table_width)
+                      ? a->table_read_width
+                      : a->table_width;
+  p.key_limit = a->key_limit;
   p.lens = a->lens;
   p.lens_i64 = a->lens_dtype == VA_I64;
   p.lens_cum = a->lens_kind == VA_LENS_CUMULATIVE;

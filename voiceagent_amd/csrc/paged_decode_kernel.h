@@ -56,7 +56,9 @@ struct DecodeParams {
   const void* table;
   int64_t t_sb;  // elements
   int32_t table_i64;
-  int32_t table_width;
+  int32_t table_width;       // columns attention reads (past it: block 0)
+  int32_t table_width_full;  // columns the current-row write may read
+  int32_t key_limit;         // > 0: tokens at or past it are not attended
   const void* lens;
   int32_t lens_i64, lens_cum;
   const uint8_t* valid;
@@ -93,6 +95,47 @@ constexpr float kNegBig = -1.0e30f;
 // tokens.  The dynamic form serves launches whose max_seq_len is only an
 // upper bound, such as a decode graph captured at max_model_len.
 constexpr int kDynGrain = 64;
+
+// Attended length of a context of L tokens: L, or key_limit when that is
+// smaller (the TTS kernel's MAX_SEQ_LEN = kernel_seq_len bound,
+// qwen_tts_paged_attention.py:223-230).
+__device__ inline int attend_len(const DecodeParams& p, int L) {
+  return (p.key_limit > 0 && L > p.key_limit) ? p.key_limit : L;
+}
+
+// Where the current row (position L - 1) goes when it is not attended in
+// place: past key_limit, or (written through the table) in a column at or
+// past the attention's read width but inside the table, where attention
+// reads block 0 while the write takes the table's entry
+// (qwen_tts_paged_attention.py:182-187 reads the table unbounded, :236-241
+// bounds the attention's reads by num_page_slots).
+__device__ inline bool current_row_detached(const DecodeParams& p, int L, int La, int col_new) {
+  if (p.new_k == nullptr || L < 1) return false;
+  if (L - 1 >= La) return true;
+  return p.new_slots == nullptr && col_new >= p.table_width && col_new < p.table_width_full;
+}
+
+// The detached current-row write: this lane's 16 bytes (at byte column
+// `col16`) of kv head h's row go to new_slots[b], or to the slot of
+// position L - 1 through the table's own entry (block 0 past the table);
+// a slot outside the pool skips the write.
+__device__ inline void store_detached_row(const DecodeParams& p, int h, int64_t table_row, int L,
+                                          int col_new, int64_t new_slot, int col16, uint4 kr,
+                                          uint4 vr) {
+  int64_t slot = new_slot;
+  if (p.new_slots == nullptr) {
+    const int64_t blk =
+        col_new < p.table_width_full ? load_index(p.table, table_row + col_new, p.table_i64) : 0;
+    slot = (blk >= 0 && blk < p.num_blocks) ? blk * p.block_size + (L - 1) % p.block_size : -1;
+  }
+  if (slot < 0 || slot >= (int64_t)p.num_blocks * p.block_size) return;
+  const int64_t sb = slot / p.block_size;
+  const int64_t dst =
+      sb * p.s_blk + (slot - sb * p.block_size) * p.s_slot + (int64_t)h * p.s_head + col16;
+  st16(p.kp + dst, kr);
+  st16(p.vp + dst, vr);
+}
+
 __device__ inline int partition_tokens(const DecodeParams& p, int L) {
   if (!p.dyn_split) return p.split_tokens;
   int P = (L + p.max_parts - 1) / p.max_parts;
@@ -186,6 +229,11 @@ __global__ __launch_bounds__((DecodeShape<ET, D, G>::NW * 64),
   int64_t pos = 0;
   if (kProlog) pos = load_index(p.pro.pos, b, p.pro.pos_i64);
   L = __builtin_amdgcn_readfirstlane(L);
+  // L becomes the attended length; the current row sits at Lr - 1.
+  const int Lr = L;
+  L = attend_len(p, L);
+  const int col_new = Lr >= 1 ? (Lr - 1) / p.block_size : 0;
+  const bool detached = current_row_detached(p, Lr, L, col_new);
 
   if (L <= 0) {
     // Nothing to attend: the output is defined as 0.
@@ -222,7 +270,8 @@ __global__ __launch_bounds__((DecodeShape<ET, D, G>::NW * 64),
   // block-table slot of L - 1 (resolved at the row's chunk from the same
   // block id its loads use).  A slot < 0 skips the write and the
   // substitution.
-  const int new_tok = (p.new_k != nullptr && L - 1 >= start && L - 1 < end) ? L - 1 : -1;
+  const int new_tok =
+      (!detached && p.new_k != nullptr && L - 1 >= start && L - 1 < end) ? L - 1 : -1;
   const int64_t cap = (int64_t)p.num_blocks * p.block_size;
 
   // Prologue factors of this lane's slice (the math runs once the first
@@ -235,6 +284,19 @@ __global__ __launch_bounds__((DecodeShape<ET, D, G>::NW * 64),
                                  col * E);
     pos = pos < 0 ? 0 : (pos >= p.pro.max_pos ? p.pro.max_pos - 1 : pos);
     load_rotary<E, LPR>(p.pro, pos, col, D, pro_c, pro_s);
+  }
+  if (detached && part == 0 && wave == 0) {
+    // The current row is not attended in place: wave 0 of the first
+    // partition writes it (after the prologue, when there is one).
+    uint4 kw = kcur;
+    if constexpr (kProlog) {
+      float w[E], x[E];
+      convert_weights<E>(pro_wk, p.pro.w_dtype, w);
+      ET::unpack(kw, x);
+      qk_prologue<ET, LPR, E>(x, w, p.pro.eps, D, pro_c, pro_s, col < LPR / 2);
+      kw = ET::pack(x);
+    }
+    if (rg == 0) store_detached_row(p, h, table_row, Lr, col_new, new_slot, col * 16, kw, vcur);
   }
 
   constexpr bool kScaleAfter = ET::kBytes == 2;
@@ -447,6 +509,13 @@ __global__ __launch_bounds__((DecodeShape<ET, D, G>::NW * 64),
           if (tok < p.valid_len && byte == 0) valid[j] &= ~(1u << r);
         }
       }
+      // Masked rows were loaded: zero their values, so that a non-finite
+      // value in a masked slot cannot reach the output through 0 * inf.
+#pragma unroll
+      for (int j = 0; j < CPW; ++j)
+#pragma unroll
+        for (int r = 0; r < NR; ++r)
+          if (!((valid[j] >> r) & 1u)) vr[j][r] = make_uint4(0, 0, 0, 0);
     }
     if (first) prepare_query();
 #pragma unroll
@@ -572,7 +641,7 @@ __global__ __launch_bounds__(256) void paged_decode_merge_kernel(DecodeParams p)
       oq[j] = p.part_o[((pair_slot0 + q) * G + g) * D + d];
     }
     int L = (int)(p.lens_cum ? len_hi - len_lo : len_lo);
-    L = __builtin_amdgcn_readfirstlane(L);
+    L = attend_len(p, __builtin_amdgcn_readfirstlane(L));
     if (L <= 0) return;
     const int P = partition_tokens(p, L);
     int nparts = (L + P - 1) / P;

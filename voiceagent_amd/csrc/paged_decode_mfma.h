@@ -340,6 +340,11 @@ __global__ __launch_bounds__(MfmaDecodeShape<D>::W * 64, 1) void paged_decode_mf
 
   int L = (int)(p.lens_cum ? len_hi - len_lo : len_lo);
   L = __builtin_amdgcn_readfirstlane(L);
+  // L becomes the attended length; the current row sits at Lr - 1.
+  const int Lr = L;
+  L = attend_len(p, L);
+  const int col_new = Lr >= 1 ? (int)fast_div((uint32_t)(Lr - 1), p.bs_div) : 0;
+  const bool detached = current_row_detached(p, Lr, L, col_new);
   const int64_t new_slot = p.new_slots_i64 ? (int64_t)(((uint64_t)slot_hi << 32) | slot_lo)
                                            : (int64_t)(int32_t)slot_lo;
 
@@ -377,7 +382,8 @@ __global__ __launch_bounds__(MfmaDecodeShape<D>::W * 64, 1) void paged_decode_mf
 
   // The current row is position L - 1 when this partition holds it: it is
   // stored to its slot and replaces the pool row in the staged tile.
-  const int new_tok = (p.new_k != nullptr && L - 1 >= start && L - 1 < end) ? L - 1 : -1;
+  const int new_tok =
+      (!detached && p.new_k != nullptr && L - 1 >= start && L - 1 < end) ? L - 1 : -1;
   const int new_tile = new_tok >= 0 ? (new_tok - start) / kChunk : -1;  // partition chunk
   const int64_t cap = (int64_t)p.num_blocks * p.block_size;
 
@@ -394,7 +400,7 @@ __global__ __launch_bounds__(MfmaDecodeShape<D>::W * 64, 1) void paged_decode_mf
       qk_prologue<ET, LPR, E>(x, w, p.pro.eps, D, pro_c, pro_s, first_half);
       qrow[k] = ET::pack(x);
     }
-    if (new_tok >= 0) {
+    if (new_tok >= 0 || (detached && part == 0 && wave == 0)) {
       convert_weights<E>(pro_wk, p.pro.w_dtype, w);
       float x[E];
       ET::unpack(kcur, x);
@@ -412,6 +418,11 @@ __global__ __launch_bounds__(MfmaDecodeShape<D>::W * 64, 1) void paged_decode_mf
                                                          (4 * j + c4) * 16)
                       : make_uint4(0, 0, 0, 0);
   }
+
+  // The current row is not attended in place: wave 0 of the first partition
+  // writes it.
+  if (detached && part == 0 && wave == 0 && rg == 0)
+    store_detached_row(p, h, table_row, Lr, col_new, new_slot, col * 16, kcur, vcur);
 
   if (!early) {
     for (int k = 0; k < S; ++k)
@@ -478,15 +489,23 @@ __global__ __launch_bounds__(MfmaDecodeShape<D>::W * 64, 1) void paged_decode_mf
     }
     float sv[4];
     const int rel = blk_ok ? end - tb - 4 * c4 : 0;  // token 4 c4 + i is live iff i < rel
+    uint32_t live = 0;  // bit i: token 4 c4 + i is attended
+#pragma unroll
+    for (int i = 0; i < 4; ++i) live |= (i < rel ? 1u : 0u) << i;
     if (has_mask) {
       // Validity bits of tokens 4 c4 .. 4 c4 + 3 of this tile.
       const uint32_t mb = (uint32_t)__builtin_amdgcn_readlane((int)mbits_proc, k & 63) >> (4 * c4);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) sv[i] = i < rel && ((mb >> i) & 1u) ? sacc[i] : -INFINITY;
-    } else {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) sv[i] = i < rel ? sacc[i] : -INFINITY;
+      live &= mb;
     }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) sv[i] = ((live >> i) & 1u) ? sacc[i] : -INFINITY;
+    // Dead tokens (past the context, masked) keep their staged V rows, which
+    // may hold anything, non-finite values included: their P is 0, and the
+    // V^T operand elements of this lane (tokens 4 c4 .. 4 c4 + 3, the same
+    // tokens as its scores) are zeroed for them so that 0 * inf never enters
+    // the sum.
+    const uint32_t keep0 = ((live & 1u) ? 0xffffu : 0u) | ((live & 2u) ? 0xffff0000u : 0u);
+    const uint32_t keep1 = ((live & 4u) ? 0xffffu : 0u) | ((live & 8u) ? 0xffff0000u : 0u);
     float mx = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
     mx = fmaxf(mx, lane_xor16(mx));
     mx = fmaxf(mx, lane_xor32(mx));
@@ -513,8 +532,11 @@ __global__ __launch_bounds__(MfmaDecodeShape<D>::W * 64, 1) void paged_decode_mf
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) {
       const int off = vrow * ROWB + (((2 * dt + ((r16 >> 1) & 1)) ^ vswz) << 4) + ((r16 & 1) << 3);
-      const mf_s16x4 a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((mf_lds_s16x4*)(sV + off));
-      o[dt] = M::pv(a, pb, o[dt]);
+      uint2 au = __builtin_bit_cast(
+          uint2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((mf_lds_s16x4*)(sV + off)));
+      au.x &= keep0;
+      au.y &= keep1;
+      o[dt] = M::pv(__builtin_bit_cast(mf_s16x4, au), pb, o[dt]);
     }
     // The stage is free once its LDS reads have returned.
     wait_lgkmcnt0();

@@ -218,33 +218,66 @@ def qk_norm_rope(
 
 # -------------------------------------------------------------------- decode
 _WORKSPACES: dict[tuple[int, int], torch.Tensor] = {}
+# Workspaces replaced by a larger one.  They are never freed: a HIP graph
+# captured while one was current keeps its address, and memory returned to
+# torch's allocator (a graph's private pool included) could be handed to
+# another tensor that the graph's replays would then overwrite.
+_RETIRED: list[torch.Tensor] = []
+_CUS: dict[int, int] = {}  # compute units per device index
 
 
 def _device_index(device: torch.device) -> int:
     return device.index if device.index is not None else torch.cuda.current_device()
 
 
-def decode_workspace(device: torch.device, nbytes: int) -> torch.Tensor | None:
-    """Partial-result workspace of the decode launches on the current stream
-    of `device` (no initialisation needed; grows by doubling).  One per
-    stream: launches on one stream are ordered, while decodes on two streams
-    (an ASR engine and a TTS talker, say) may run at once and must not share
-    their partials."""
+def decode_workspace_bound(device: torch.device, num_heads: int, num_kv_heads: int,
+                           head_dim: int) -> int:
+    """Bytes that covers every automatic split (split_tokens = 0) of a decode
+    with these heads on `device`, whatever the batch and lengths: the split
+    gives at most one partition per compute unit over all (sequence, kv head)
+    pairs, each holding (m, l) and head_dim floats per query head of the
+    group, with the (m, l) block rounded to 256 bytes."""
+    index = _device_index(device)
+    cus = _CUS.get(index)
+    if cus is None:
+        cus = _CUS[index] = torch.cuda.get_device_properties(index).multi_processor_count
+    group = max(1, num_heads // max(1, num_kv_heads))
+    return (cus * group * 2 * 4 + 255) // 256 * 256 + cus * group * head_dim * 4
+
+
+def decode_workspace(device: torch.device, nbytes: int, floor: int = 0,
+                     stream: torch.cuda.Stream | None = None) -> torch.Tensor | None:
+    """Partial-result workspace of the decode launches on `stream` (torch's
+    current stream of `device` by default): no initialisation needed.  One
+    per stream: launches on one stream are ordered, while decodes on two
+    streams (an ASR engine and a TTS talker, say) may run at once and must not
+    share their partials.  The first allocation takes at least `floor` bytes;
+    a later, larger need allocates anew (doubling) and retires, without
+    freeing, the old buffer."""
     if nbytes == 0:
         return None
-    key = (_device_index(device), torch.cuda.current_stream(device).cuda_stream)
+    if stream is None:
+        stream = torch.cuda.current_stream(device)
+    key = (_device_index(device), stream.cuda_stream)
     ws = _WORKSPACES.get(key)
     if ws is None or ws.numel() < nbytes:
-        size = max(nbytes, 0 if ws is None else 2 * ws.numel())
+        size = max(nbytes, floor if ws is None else 2 * ws.numel())
+        if ws is not None:
+            _RETIRED.append(ws)
         ws = torch.empty(size, dtype=torch.uint8, device=device)
         _WORKSPACES[key] = ws
     return ws
 
 
-def reserve_decode_workspace(device: torch.device, nbytes: int) -> None:
-    """Allocate the decode workspace of the current stream up front (before
-    HIP graph capture on that stream)."""
-    decode_workspace(torch.device(device), nbytes)
+def reserve_decode_workspace(device: torch.device, num_heads: int, num_kv_heads: int,
+                             head_dim: int, stream: torch.cuda.Stream | None = None) -> None:
+    """Allocate the decode workspace of `stream` (torch's current stream by
+    default) up front, at the size every automatic split needs, e.g. before
+    HIP graph capture.  ``torch.cuda.graph`` captures on a stream of its own
+    unless it is given one: pass that stream here to reserve for it."""
+    device = torch.device(device)
+    bound = decode_workspace_bound(device, num_heads, num_kv_heads, head_dim)
+    decode_workspace(device, bound, floor=bound, stream=stream)
 
 
 def paged_decode(
@@ -265,6 +298,8 @@ def paged_decode(
     out: torch.Tensor | None = None,
     split_tokens: int = 0,
     prologue: QKPrologue | None = None,
+    key_limit: int = 0,
+    table_read_width: int = 0,
 ) -> torch.Tensor:
     """One-token paged GQA attention.
 
@@ -273,7 +308,11 @@ def paged_decode(
     ``new_k``/``new_v`` ([B, Hkv, D]) are written at position len-1 (or at
     ``new_slots[b]``) and used for that position in the same launch.  With a
     ``prologue``, q and new_k are raw projections, normalised and rotated at
-    ``prologue.positions[b]`` inside the launch.
+    ``prologue.positions[b]`` inside the launch.  ``key_limit`` (> 0) leaves
+    tokens at or past it unattended and ``table_read_width`` (> 0) makes the
+    attention read block 0 for table columns at or past it (the TTS kernel's
+    kernel_seq_len / kernel_page_count bounds); the current row is written at
+    len - 1 either way.
     """
     device = _check_gpu(q, k_cache, v_cache, block_tables, lens, valid_mask, new_k, new_v,
                         new_slots, out)
@@ -342,12 +381,16 @@ def paged_decode(
     args.max_seq_len = int(max_seq_len)
     args.split_tokens = int(split_tokens)
     args.scale = float(scale)
+    _require(key_limit >= 0 and table_read_width >= 0,
+             "key_limit and table_read_width must be non-negative")
+    args.key_limit = int(key_limit)
+    args.table_read_width = int(table_read_width)
     if prologue is not None:
         pro_struct = _prologue_struct(prologue, d, B)  # kept alive through the call
         args.prologue = ctypes.pointer(pro_struct)
     with torch.cuda.device(device):  # the split plan depends on the device's CU count
         nbytes = N.lib().va_paged_decode_workspace_bytes(ctypes.byref(args))
-    ws = decode_workspace(device, nbytes)
+    ws = decode_workspace(device, nbytes, floor=decode_workspace_bound(device, hq, hkv, d))
     if ws is not None:
         args.workspace = ws.data_ptr()
         args.workspace_bytes = ws.numel()
@@ -457,22 +500,3 @@ def varlen_attention(
 
 def default_scale(head_dim: int) -> float:
     return 1.0 / math.sqrt(head_dim)
-
-
-# --------------------------------------------------------------- diagnostics
-def hbm_read_probe(buf: torch.Tensor, workgroups: int, sink: torch.Tensor) -> None:
-    """Plain streaming read of the contiguous GPU tensor `buf` in one launch of
-    `workgroups` workgroups (va_hbm_read_probe): the HBM read floor that the
-    decode kernel's bandwidth is read against.  `sink` is an int32 tensor of
-    at least `workgroups` elements; nothing is computed."""
-    device = _check_gpu(buf, sink)
-    _require(buf.is_contiguous(), "the probe reads a contiguous tensor")
-    nbytes = buf.numel() * buf.element_size()
-    _require(buf.data_ptr() % 16 == 0 and nbytes % 16 == 0,
-             "the probe reads 16-byte aligned whole 16-byte words")
-    _require(sink.dtype == torch.int32 and sink.numel() >= workgroups,
-             "sink must be int32 with one element per workgroup")
-    with torch.cuda.device(device):
-        N.check("va_hbm_read_probe",
-                N.lib().va_hbm_read_probe(buf.data_ptr(), nbytes, int(workgroups),
-                                          sink.data_ptr(), N.current_stream(device)))
