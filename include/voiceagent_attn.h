@@ -210,6 +210,22 @@ size_t va_paged_decode_workspace_bytes(const va_decode_args* args);
  * paged_attention_decode (qwen_tts_paged_attention.py:383-516). */
 int va_paged_decode(const va_decode_args* args, void* stream);
 
+/* Size of the scratch buffer of va_paged_decode_noalloc, per GPU. */
+#define VA_DECODE_NOALLOC_SCRATCH_BYTES ((size_t)4 << 20)
+
+/* va_paged_decode without a caller workspace and without any allocation: the
+ * split-context partials live in a scratch buffer of
+ * VA_DECODE_NOALLOC_SCRATCH_BYTES that the library holds in device memory, one
+ * per GPU, for the life of the process (its address is looked up on the first
+ * call on each device).  The args' workspace fields are ignored.  A split
+ * needing more than the buffer (only an explicit split_tokens can; every
+ * automatic split fits) fails with VA_ERR_WORKSPACE.  Calls that overlap on
+ * one GPU (on two streams, say) share the buffer and race: order them.  No
+ * counterpart in the reference: it is for callers that cannot allocate, such
+ * as code under HIP graph capture that must not touch an allocator, tight
+ * serving loops and harnesses that forbid hipMalloc. */
+int va_paged_decode_noalloc(const va_decode_args* args, void* stream);
+
 /* --------------------------------------------------------------- varlen */
 typedef struct va_varlen_args {
   uint32_t struct_size;   /* sizeof(va_varlen_args)                       */

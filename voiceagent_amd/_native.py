@@ -21,6 +21,7 @@ VA_BF16, VA_F16, VA_F32 = 0, 1, 2
 VA_I32, VA_I64 = 0, 1
 VA_LENS_PER_SEQ, VA_LENS_CUMULATIVE = 0, 1
 ABI_VERSION = 3  # VA_ATTN_ABI_VERSION of the header these structs mirror
+DECODE_NOALLOC_SCRATCH_BYTES = 4 << 20  # VA_DECODE_NOALLOC_SCRATCH_BYTES
 
 DTYPE_CODES = {torch.bfloat16: VA_BF16, torch.float16: VA_F16, torch.float32: VA_F32}
 INDEX_CODES = {torch.int32: VA_I32, torch.int64: VA_I64}
@@ -189,6 +190,7 @@ SIGNATURES = {
     "va_store_kvcache": (c_int32, [ctypes.POINTER(StoreArgs), c_void_p]),
     "va_paged_decode_workspace_bytes": (c_size_t, [ctypes.POINTER(DecodeArgs)]),
     "va_paged_decode": (c_int32, [ctypes.POINTER(DecodeArgs), c_void_p]),
+    "va_paged_decode_noalloc": (c_int32, [ctypes.POINTER(DecodeArgs), c_void_p]),
     "va_varlen_attention": (c_int32, [ctypes.POINTER(VarlenArgs), c_void_p]),
     "va_qk_norm_rope": (c_int32, [ctypes.POINTER(QkNormRopeArgs), c_void_p]),
     "va_last_error": (ctypes.c_char_p, []),

@@ -3,6 +3,7 @@
 // instantiated per element type in paged_decode_{bf16,f16,f32}.hip).
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
 
 #include "paged_decode_mfma.h"
 
@@ -173,7 +174,88 @@ extern "C" size_t va_paged_decode_workspace_bytes(const va_decode_args* a) {
   return va::plan_decode(a).total_bytes;
 }
 
+namespace va {
+
+// The body of va_paged_decode; the workspace comes from the arguments.
+static int paged_decode_impl(const va_decode_args* a, void* stream);
+
+// ------------------------------------------------- allocation-free variant
+// Scratch memory of va_paged_decode_noalloc: the split-context partials,
+// `kDecodeScratchBytes` per GPU, in the library's own device memory (the
+// loaded code object holds it for the life of the process).  Every
+// automatic split needs at most (compute units) x group x (head_dim + 2) x 4
+// bytes plus 256 of rounding: 2.1 MB at 256 compute units, group 8 and
+// head_dim 256.  Host code never uses the array's name as an address: each
+// device's copy is reached through the pointer hipGetSymbolAddress returns
+// with that device current.
+constexpr size_t kDecodeScratchBytes = VA_DECODE_NOALLOC_SCRATCH_BYTES;
+static __device__ __align__(256) char scratch[kDecodeScratchBytes];
+
+constexpr int kMaxScratchDevices = 64;
+static void* g_scratch_ptr[kMaxScratchDevices];
+static hipError_t g_scratch_status[kMaxScratchDevices];
+static std::once_flag g_scratch_once[kMaxScratchDevices];
+
+// The current device's copy of `scratch` (looked up once per device), or
+// nullptr with the error set.
+static void* device_scratch() {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxScratchDevices) {
+    (void)hipGetLastError();
+    set_error("va_paged_decode_noalloc: no usable current device (%d)", dev);
+    return nullptr;
+  }
+  std::call_once(g_scratch_once[dev], [dev] {
+    void* ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    g_scratch_status[dev] = e;
+    g_scratch_ptr[dev] = e == hipSuccess ? ptr : nullptr;
+    if (e != hipSuccess) (void)hipGetLastError();
+  });
+  if (g_scratch_ptr[dev] == nullptr) {
+    set_error("va_paged_decode_noalloc: hipGetSymbolAddress of the scratch buffer failed on "
+              "device %d: %s",
+              dev, hipGetErrorString(g_scratch_status[dev]));
+    return nullptr;
+  }
+  return g_scratch_ptr[dev];
+}
+
+}  // namespace va
+
+extern "C" int va_paged_decode_noalloc(const va_decode_args* a, void* stream) {
+  using namespace va;
+  VA_CHECK_ARG(a != nullptr, "va_paged_decode_noalloc: null args");
+  VA_CHECK_ARG(a->struct_size == sizeof(va_decode_args),
+               "va_paged_decode_noalloc: struct_size %u != %zu (header/library mismatch)",
+               a->struct_size, sizeof(va_decode_args));
+  va_decode_args b = *a;
+  b.workspace = nullptr;
+  b.workspace_bytes = 0;
+  if (b.num_seqs > 0) {
+    const size_t need = plan_decode(&b).total_bytes;
+    if (need > kDecodeScratchBytes) {
+      set_error("va_paged_decode_noalloc: the split needs %zu bytes of workspace, above the "
+                "%zu-byte scratch buffer (use va_paged_decode with a workspace, or a larger "
+                "split_tokens)",
+                need, kDecodeScratchBytes);
+      return VA_ERR_WORKSPACE;
+    }
+    if (need > 0) {
+      void* ptr = device_scratch();
+      if (ptr == nullptr) return VA_ERR_WORKSPACE;
+      b.workspace = ptr;
+      b.workspace_bytes = kDecodeScratchBytes;
+    }
+  }
+  return paged_decode_impl(&b, stream);
+}
+
 extern "C" int va_paged_decode(const va_decode_args* a, void* stream) {
+  return va::paged_decode_impl(a, stream);
+}
+
+int va::paged_decode_impl(const va_decode_args* a, void* stream) {
   using namespace va;
   VA_CHECK_ARG(a != nullptr, "va_paged_decode: null args");
   VA_CHECK_ARG(a->struct_size == sizeof(va_decode_args),

@@ -300,6 +300,7 @@ def paged_decode(
     prologue: QKPrologue | None = None,
     key_limit: int = 0,
     table_read_width: int = 0,
+    no_alloc: bool = False,
 ) -> torch.Tensor:
     """One-token paged GQA attention.
 
@@ -312,10 +313,13 @@ def paged_decode(
     tokens at or past it unattended and ``table_read_width`` (> 0) makes the
     attention read block 0 for table columns at or past it (the TTS kernel's
     kernel_seq_len / kernel_page_count bounds); the current row is written at
-    len - 1 either way.
+    len - 1 either way.  ``no_alloc`` launches va_paged_decode_noalloc, which
+    keeps the split partials in the library's own scratch buffer instead of a
+    workspace; ``out`` must then be given, so that nothing is allocated.
     """
     device = _check_gpu(q, k_cache, v_cache, block_tables, lens, valid_mask, new_k, new_v,
                         new_slots, out)
+    _require(not no_alloc or out is not None, "no_alloc needs the output tensor (out=...)")
     if prologue is not None:
         _check_gpu(q, prologue.q_norm_weight, prologue.k_norm_weight, prologue.cos_sin_cache,
                    prologue.positions)
@@ -388,6 +392,9 @@ def paged_decode(
     if prologue is not None:
         pro_struct = _prologue_struct(prologue, d, B)  # kept alive through the call
         args.prologue = ctypes.pointer(pro_struct)
+    if no_alloc:
+        N.call("va_paged_decode_noalloc", args, device)
+        return out
     with torch.cuda.device(device):  # the split plan depends on the device's CU count
         nbytes = N.lib().va_paged_decode_workspace_bytes(ctypes.byref(args))
     ws = decode_workspace(device, nbytes, floor=decode_workspace_bound(device, hq, hkv, d))
