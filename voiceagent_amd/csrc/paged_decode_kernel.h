@@ -351,7 +351,11 @@ __global__ __launch_bounds__((DecodeShape<ET, D, G>::NW * 64),
   };
 
   // The chunk holding the current row: substitute the register copy for the
-  // row and write it to its slot (exactly one lane group in the grid does).
+  // row and note its slot's pool offset (exactly one lane group in the grid
+  // does).  The pool write itself comes after the last workgroup barrier: a
+  // barrier waits for every store the wave has in flight, so a write issued
+  // here would hold up the merge by a whole HBM write round trip.
+  int64_t cur_dst = -1;
   auto current_row = [&](int k, int32_t cb, const int32_t* rbk, uint4 (&kr)[NR],
                          uint4 (&vr)[NR]) {
     const int tb = start + (wave + NW * k) * kChunk;
@@ -369,9 +373,7 @@ __global__ __launch_bounds__((DecodeShape<ET, D, G>::NW * 64),
         kr[r] = kcur;
         vr[r] = vcur;
         const int64_t blk = slot / p.block_size;
-        const int64_t dst = blk * p.s_blk + (slot - blk * p.block_size) * p.s_slot + head_off;
-        st16(p.kp + dst, kcur);
-        st16(p.vp + dst, vcur);
+        cur_dst = blk * p.s_blk + (slot - blk * p.block_size) * p.s_slot + head_off;
       }
     }
   };
@@ -586,6 +588,10 @@ __global__ __launch_bounds__((DecodeShape<ET, D, G>::NW * 64),
         p.part_ml[slot * 2 + 1] = Lt;
       }
     }
+  }
+  if (cur_dst >= 0) {
+    st16(p.kp + cur_dst, kcur);
+    st16(p.vp + cur_dst, vcur);
   }
 }
 

@@ -140,12 +140,20 @@ __global__ __launch_bounds__(MfmaDecodeShape<D>::W * 64, 1) void paged_decode_mf
   constexpr int NT = W * 64;
   constexpr int QROWS = (G + RPL - 1) / RPL;  // query rows per lane in the row layout
   static_assert(G <= 16, "at most 16 query heads per kv head");
-  static_assert(W * G * D * 4 + 2 * W * G * 4 <= W * Sh::WAVE_B, "merge scratch");
+  // The waves' partial results for the merge: o [W][G][D], then m and l
+  // [G][W].  They get their own LDS beside the tile ring when it fits, so a
+  // wave can write its partial as soon as its loop ends; otherwise they
+  // reuse the ring once every wave is done with it.
+  constexpr int MERGE_B = W * G * D * 4 + 2 * G * W * 4;
+  constexpr int Q_B = kProlog ? W * G * ROWB : 16;
+  constexpr bool kOwnMerge = W * Sh::WAVE_B + MERGE_B + Q_B <= 160 * 1024;
+  static_assert(MERGE_B <= W * Sh::WAVE_B, "merge scratch");
 
   __shared__ __align__(1024) char s_buf[W * Sh::WAVE_B];
   // Apart from the tile ring, so that early tile DMAs cannot land on them:
   // the query rows of the prologue (per wave).
-  __shared__ __align__(16) char s_q[kProlog ? W * G * ROWB : 16];
+  __shared__ __align__(16) char s_q[Q_B];
+  __shared__ __align__(16) char s_mrg[kOwnMerge ? MERGE_B : 16];
 
   const int b = blockIdx.x;
   const int h = blockIdx.y;
@@ -439,6 +447,11 @@ __global__ __launch_bounds__(MfmaDecodeShape<D>::W * 64, 1) void paged_decode_mf
   mf_f32x4 o[DT];
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt) o[dt] = mf_f32x4{0.f, 0.f, 0.f, 0.f};
+  // Pool offset of this lane's 16 bytes of the current row (-1: none).  The
+  // row is written after the last workgroup barrier: a barrier waits for
+  // every store the wave has in flight, so a write issued in the loop would
+  // hold up the merge below by a whole HBM write round trip.
+  int64_t cur_dst = -1;
   const int kswz = dec_swz<D>(r16);
   const int vrow = 4 * c4 + (r16 >> 2);
   const int vswz = dec_swz<D>(vrow);
@@ -460,8 +473,9 @@ __global__ __launch_bounds__(MfmaDecodeShape<D>::W * 64, 1) void paged_decode_mf
     const bool blk_ok = blk >= 0 && blk < p.num_blocks;
 
     if (c == new_tile) {
-      // The current row: write it to its slot (new_slots[b], or the table
-      // slot of L - 1) and put it in place of the staged pool row.
+      // The current row: put it in place of the staged pool row, and note
+      // its slot (new_slots[b], or the table slot of L - 1) for the pool
+      // write at the end.
       int64_t slot = new_slot;
       if (p.new_slots == nullptr)
         slot = blk_ok ? (int64_t)blk * p.block_size + fast_mod((uint32_t)new_tok, p.bs_div) : -1;
@@ -472,10 +486,7 @@ __global__ __launch_bounds__(MfmaDecodeShape<D>::W * 64, 1) void paged_decode_mf
         *reinterpret_cast<uint4*>(sV + r * ROWB + pos16) = vcur;
         const int64_t sb = p.slot_small ? (int64_t)fast_div((uint32_t)slot, p.bs_div)
                                         : slot / p.block_size;
-        const int64_t dst = sb * p.s_blk + (slot - sb * p.block_size) * p.s_slot + head_off +
-                            col * 16;
-        st16(p.kp + dst, kcur);
-        st16(p.vp + dst, vcur);
+        cur_dst = sb * p.s_blk + (slot - sb * p.block_size) * p.s_slot + head_off + col * 16;
       }
     }
 
@@ -549,50 +560,66 @@ __global__ __launch_bounds__(MfmaDecodeShape<D>::W * 64, 1) void paged_decode_mf
   wait_vmcnt<0>();
   l += lane_xor16(l);
   l += lane_xor32(l);
-  __syncthreads();  // every wave is done with its stages
-  float* s_o = reinterpret_cast<float*>(s_buf);              // [W][G][D]
-  float* s_m = s_o + W * G * D;                               // [W][G]
-  float* s_l = s_m + W * G;                                   // [W][G]
+  if constexpr (!kOwnMerge) __syncthreads();  // every wave is done with its stages
+  float* s_o = reinterpret_cast<float*>(kOwnMerge ? s_mrg : s_buf);  // [W][G][D]
+  float* s_m = s_o + W * G * D;                                       // [G][W]
+  float* s_l = s_m + G * W;                                           // [G][W]
   if (r16 < G) {
+    // Lane (r16, c4) holds o of head r16 at d = 16 dt + 4 c4 + i.
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) s_o[(wave * G + r16) * D + 16 * dt + 4 * c4 + i] = o[dt][i];
+      *reinterpret_cast<mf_f32x4*>(s_o + (wave * G + r16) * D + 16 * dt + 4 * c4) = o[dt];
     if (c4 == 0) {
-      s_m[wave * G + r16] = ntw > 0 ? m : kNegBig;
-      s_l[wave * G + r16] = ntw > 0 ? l : 0.f;
+      s_m[r16 * W + wave] = ntw > 0 ? m : kNegBig;
+      s_l[r16 * W + wave] = ntw > 0 ? l : 0.f;
     }
   }
   __syncthreads();
 
+  // Each lane combines four consecutive outputs of one query head.
   const int64_t pair = (int64_t)b * p.num_kv_heads + h;
-  for (int idx = tid; idx < G * D; idx += NT) {
-    const int g = idx / D, d = idx % D;
+  for (int qd = tid; qd < G * D / 4; qd += NT) {
+    const int g = qd / (D / 4), d = (qd % (D / 4)) * 4;
+    float mw[W], lw[W];
+#pragma unroll
+    for (int w = 0; w < W; w += 4) {
+      const mf_f32x4 mv = *reinterpret_cast<const mf_f32x4*>(s_m + g * W + w);
+      const mf_f32x4 lv = *reinterpret_cast<const mf_f32x4*>(s_l + g * W + w);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        mw[w + i] = mv[i];
+        lw[w + i] = lv[i];
+      }
+    }
     float Mx = kNegBig;
 #pragma unroll
-    for (int w = 0; w < W; ++w) Mx = fmaxf(Mx, s_m[w * G + g]);
-    float Lt = 0.f, Ot = 0.f;
+    for (int w = 0; w < W; ++w) Mx = fmaxf(Mx, mw[w]);
+    float Lt = 0.f;
+    mf_f32x4 acc = mf_f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int w = 0; w < W; ++w) {
-      const float f = fast_exp2(s_m[w * G + g] - Mx);
-      Lt += s_l[w * G + g] * f;
-      Ot += s_o[(w * G + g) * D + d] * f;
+      const float f = fast_exp2(mw[w] - Mx);
+      Lt += lw[w] * f;
+      acc += f * *reinterpret_cast<const mf_f32x4*>(s_o + (w * G + g) * D + d);
     }
     if (nparts == 1) {
-      const float val = Lt > 0.f ? Ot / Lt : 0.f;
-      char* dst = p.out + b * p.o_sb + (int64_t)(h * G + g) * p.o_sh + d * 2;
-      float tmp[E] = {};
-      tmp[0] = val;
-      const uint4 u = ET::pack(tmp);
-      *reinterpret_cast<uint16_t*>(dst) = (uint16_t)(u.x & 0xffffu);
+      const float inv = Lt > 0.f ? 1.f / Lt : 0.f;
+      uint2 u;
+      u.x = M::pack2(acc[0] * inv, acc[1] * inv);
+      u.y = M::pack2(acc[2] * inv, acc[3] * inv);
+      *reinterpret_cast<uint2*>(p.out + b * p.o_sb + (int64_t)(h * G + g) * p.o_sh + d * 2) = u;
     } else {
       const int64_t slot = (pair * p.max_parts + part) * G + g;
-      p.part_o[slot * D + d] = Ot;
+      *reinterpret_cast<mf_f32x4*>(p.part_o + slot * D + d) = acc;
       if (d == 0) {
         p.part_ml[slot * 2] = Mx;
         p.part_ml[slot * 2 + 1] = Lt;
       }
     }
+  }
+  if (cur_dst >= 0) {
+    st16(p.kp + cur_dst, kcur);
+    st16(p.vp + cur_dst, vcur);
   }
 }
 
