@@ -39,7 +39,7 @@
 extern "C" {
 #endif
 
-#define VA_ATTN_ABI_VERSION 3
+#define VA_ATTN_ABI_VERSION 4
 
 /* status codes */
 #define VA_OK 0
@@ -56,6 +56,10 @@ extern "C" {
 /* index types */
 #define VA_I32 0
 #define VA_I64 1
+
+/* KV pool element formats (va_kv_pool.kv_format) */
+#define VA_KV_NATIVE 0   /* the entry point's dtype (bf16 / f16 / f32)              */
+#define VA_KV_FP8_E4M3 1 /* OCP float8 e4m3 (float8_e4m3fn); element = code * scale */
 
 /* how va_decode_args.lens is read */
 #define VA_LENS_PER_SEQ 0    /* lens[b] = context length of sequence b           */
@@ -80,6 +84,15 @@ typedef struct va_kv_pool {
   int32_t block_size;     /* tokens per block (any positive value)       */
   int32_t num_blocks;     /* blocks in the pool; out-of-range ids are    */
                           /* treated as masked and never dereferenced    */
+  /* Element format (VA_KV_*).  An FP8 pool holds OCP e4m3 codes (strides
+   * count bytes); a key element's value is code * k_scale, a value
+   * element's code * v_scale (one scale per pool, > 0).  Every store into
+   * it quantises: code = e4m3_rne(clamp(x * (1 / scale), -448, 448)), with
+   * 1 / scale and the product rounded to fp32.  FP8 pools need 16-bit
+   * q / k / v and, for decode, a block size that is a multiple of 16. */
+  int32_t kv_format;
+  float k_scale;
+  float v_scale;
 } va_kv_pool;
 
 /* ---------------------------------------------------------------- store */
@@ -260,12 +273,23 @@ typedef struct va_varlen_args {
    * slot_mapping[i] (slot < 0 skips), as store_kvcache would. */
   const void* slot_mapping;
   int32_t slot_dtype;
+  /* Scratch for an FP8 pool's paged prefix (see va_varlen_workspace_bytes;
+   * no initialisation needed).  The prefix keys are dequantised into it
+   * (bf16 / f16) before attention; with an FP8 pool, max_seqlen_k must
+   * bound every k_len. */
+  void* workspace;
+  size_t workspace_bytes;
 } va_varlen_args;
 
 /* Variable-length attention over packed sequences: causal with bottom-right
  * alignment (prefill, optionally over a paged prefix and with the store
  * fused), or non-causal block-diagonal (audio encoder windows). */
 int va_varlen_attention(const va_varlen_args* args, void* stream);
+
+/* Bytes of workspace va_varlen_attention needs (0 unless the pool is FP8 and
+ * keys come from it): num_seqs x ceil(max_seqlen_k / block_size) blocks of
+ * dequantised prefix rows plus their block table. */
+size_t va_varlen_workspace_bytes(const va_varlen_args* args);
 
 /* ----------------------------------------------------------------- misc */
 const char* va_last_error(void);

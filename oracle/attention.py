@@ -17,6 +17,13 @@ in plain PyTorch on the CPU, evaluated in float32 (or float64 when asked):
   92-107), non-causal block-diagonal windows (:121-139); equal to upstream
   eager_attention_forward + the causal or _prepare_attention_mask masks
   (reference/modeling_qwen3_asr.py:90-113, 649-667).
+* :func:`quantize_fp8`, :func:`dequantize_fp8` — the FP8 KV pool format, OCP
+  e4m3 (float8_e4m3fn) codes with one scale per pool: code =
+  e4m3_rne(clamp(x * (1/scale), -448, 448)), value = code * scale.  The
+  reference engine keeps K/V in the model dtype; this is the KV-quantisation
+  lever its README names (README.md:427-435), with vLLM's per-tensor scale
+  convention.  :func:`store_kvcache`, :func:`paged_decode` and
+  :func:`varlen_attention` read and write FP8 pools through these two.
 * :func:`rms_norm`, :func:`rope_cache`, :func:`apply_rope`, :func:`qk_norm_rope` —
   Qwen3's q/k prologue: RMSNorm._norm (qwen_asr_vllm/layers/layernorm.py:19-25),
   RotaryEmbedding's cache and apply_rotary_emb
@@ -46,6 +53,26 @@ import torch
 
 NHD = "nhd"  # [num_blocks, block_size, Hkv, D]
 HND = "hnd"  # [pages, Hkv, page_size, D]
+FP8 = torch.float8_e4m3fn
+FP8_MAX = 448.0
+
+
+def quantize_fp8(x: torch.Tensor, scale: float) -> torch.Tensor:
+    """OCP e4m3 codes of x / scale: x * (1/scale) in fp32 (1/scale itself
+    rounded to fp32), saturated to +-448, rounded to nearest even by torch's
+    float8_e4m3fn conversion."""
+    inv = torch.tensor(1.0, dtype=torch.float32) / torch.tensor(scale, dtype=torch.float32)
+    y = x.float() * inv
+    return y.clamp(-FP8_MAX, FP8_MAX).to(FP8)
+
+
+def dequantize_fp8(codes: torch.Tensor, scale: float) -> torch.Tensor:
+    """Values of e4m3 codes: code * scale, in fp32."""
+    return codes.float() * torch.tensor(scale, dtype=torch.float32)
+
+
+def _as_values(pool: torch.Tensor, scale: float | None) -> torch.Tensor:
+    return dequantize_fp8(pool, scale) if pool.dtype == FP8 else pool
 
 
 def _block_size(pool: torch.Tensor, layout: str) -> int:
@@ -67,12 +94,16 @@ def gather_rows(pool: torch.Tensor, table_row: torch.Tensor, positions: torch.Te
     return pool[pages, :, offsets, :]
 
 
-def store_kvcache(key, value, k_cache, v_cache, slot_mapping, layout: str = NHD):
+def store_kvcache(key, value, k_cache, v_cache, slot_mapping, layout: str = NHD,
+                  k_scale: float = 1.0, v_scale: float = 1.0):
     """Return copies of the pools after the store (slot -1 skips; others must be valid).
 
-    cache.view(-1, Hkv * D)[slot] = key[i]   (layers/attention.py:42-49)
+    cache.view(-1, Hkv * D)[slot] = key[i]   (layers/attention.py:42-49); an
+    FP8 pool receives quantize_fp8(key[i], k_scale) (and v_scale for values).
     """
     kc, vc = k_cache.clone(), v_cache.clone()
+    if kc.dtype == FP8:
+        key, value = quantize_fp8(key, k_scale), quantize_fp8(value, v_scale)
     bs = _block_size(kc, layout)
     for i, slot in enumerate(slot_mapping.tolist()):
         if slot == -1:
@@ -88,10 +119,13 @@ def store_kvcache(key, value, k_cache, v_cache, slot_mapping, layout: str = NHD)
 
 
 def write_current_kv(key_pool, value_pool, page_table, seq_lens, new_key, new_value,
-                     layout: str = HND):
+                     layout: str = HND, k_scale: float = 1.0, v_scale: float = 1.0):
     """Copies of the pools with row seq_len-1 of every sequence replaced
-    (qwen_tts_paged_attention.py:519-532).  new_key: [B, Hkv, D]."""
+    (qwen_tts_paged_attention.py:519-532).  new_key: [B, Hkv, D]; an FP8
+    pool receives the quantised rows."""
     kp, vp = key_pool.clone(), value_pool.clone()
+    if kp.dtype == FP8:
+        new_key, new_value = quantize_fp8(new_key, k_scale), quantize_fp8(new_value, v_scale)
     bs = _block_size(kp, layout)
     for row in range(new_key.shape[0]):
         position = int(seq_lens[row]) - 1
@@ -117,7 +151,7 @@ def _masked_softmax_av(scores: torch.Tensor, values: torch.Tensor, keep: torch.T
 
 def paged_decode(q, k_cache, v_cache, block_tables, context_lens, scale, *, layout: str = NHD,
                  valid_mask=None, key_limit=None, table_read_width=None,
-                 compute_dtype=torch.float32):
+                 compute_dtype=torch.float32, k_scale: float = 1.0, v_scale: float = 1.0):
     """One query token per sequence over a paged pool.  q: [B, Hq, D] -> [B, Hq, D].
 
     Per row (qwen_tts_paged_attention.py:363-379): gather the first L rows
@@ -128,8 +162,10 @@ def paged_decode(q, k_cache, v_cache, block_tables, context_lens, scale, *, layo
     non-finite value there does not reach the output.  ``key_limit`` and
     ``table_read_width`` are the Triton kernel's MAX_SEQ_LEN and
     num_page_slots (:223-241): tokens at or past key_limit are not attended,
-    and table columns at or past table_read_width read as block 0.
+    and table columns at or past table_read_width read as block 0.  FP8
+    pools are read as dequantize_fp8(code, k_scale / v_scale).
     """
+    k_cache, v_cache = _as_values(k_cache, k_scale), _as_values(v_cache, v_scale)
     B, hq, d = q.shape
     outs = []
     for b in range(B):
@@ -165,7 +201,7 @@ def paged_decode(q, k_cache, v_cache, block_tables, context_lens, scale, *, layo
 
 def varlen_attention(q, k, v, cu_seqlens_q, cu_seqlens_k, scale, causal, *, k_cache=None,
                      v_cache=None, block_tables=None, layout: str = NHD,
-                     compute_dtype=torch.float32):
+                     compute_dtype=torch.float32, k_scale: float = 1.0, v_scale: float = 1.0):
     """Packed variable-length attention.  q: [total_q, Hq, D] -> same shape.
 
     Sequence s owns queries [cu_q[s], cu_q[s+1]) and k_len = cu_k[s+1]-cu_k[s]
@@ -174,7 +210,10 @@ def varlen_attention(q, k, v, cu_seqlens_q, cu_seqlens_k, scale, causal, *, k_ca
     k/v rows [cu_k[s], cu_k[s+1]) without a pool; with a pool, keys
     j < k_len - q_len are read through ``block_tables`` and the rest from k/v
     rows aligned with the queries (from the pool as well when k is None).
+    FP8 pools are read as dequantize_fp8(code, k_scale / v_scale).
     """
+    if k_cache is not None:
+        k_cache, v_cache = _as_values(k_cache, k_scale), _as_values(v_cache, v_scale)
     total_q, hq, d = q.shape
     out = torch.zeros(total_q, hq, d, dtype=compute_dtype)
     cq = [int(x) for x in cu_seqlens_q]

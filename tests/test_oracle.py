@@ -475,3 +475,75 @@ def test_prologue_planted_mistakes_fail():
     qn, kn = oracle.qk_norm_rope(x, x[:, :1], pos, w, w, 1e-6, cs)
     assert torch.allclose(qn.double(), _rope_complex(oracle.rms_norm(x, w, 1e-6), pos, base),
                           atol=2e-3)
+
+
+# ------------------------------------------------------------------ FP8 pools
+def test_fp8_quantize_known_values_of_the_ocp_e4m3_format():
+    # Codes from the OCP 8-bit floating point specification (E4M3, bias 7, no
+    # infinities, 0x7f/0xff NaN): exponent/mantissa fields read off by hand.
+    cases = [(1.0, 0x38), (-1.0, 0xB8), (448.0, 0x7E), (-448.0, 0xFE), (2.0 ** -9, 0x01),
+             (2.0 ** -6, 0x08), (7 * 2.0 ** -9, 0x07), (240.0, 0x77), (0.5, 0x30),
+             (1.125, 0x39), (1.25, 0x3A), (3.5, 0x46), (0.0, 0x00)]
+    x = torch.tensor([c[0] for c in cases])
+    got = oracle.quantize_fp8(x, 1.0).view(torch.uint8).tolist()
+    assert got == [c[1] for c in cases]
+    # saturation, not NaN, past the largest finite value
+    big = oracle.quantize_fp8(torch.tensor([500.0, 1e30, float("inf"), -float("inf")]), 1.0)
+    assert big.view(torch.uint8).tolist() == [0x7E, 0x7E, 0x7E, 0xFE]
+    # halfway cases round to the even mantissa
+    ties = torch.tensor([1.0625, 1.1875, 2.0 ** -10, 3 * 2.0 ** -10, 464.0 - 1e-3])
+    assert oracle.quantize_fp8(ties, 1.0).view(torch.uint8).tolist() == [0x38, 0x3A, 0x00, 0x02,
+                                                                         0x7E]
+
+
+def test_fp8_every_finite_code_round_trips_and_scales():
+    codes = torch.arange(256, dtype=torch.uint8)
+    finite = codes[(codes & 0x7F) != 0x7F]  # 0x7f / 0xff are NaN
+    vals = oracle.dequantize_fp8(finite.view(oracle.FP8), 1.0)
+    assert torch.isfinite(vals).all()
+    assert torch.equal(oracle.quantize_fp8(vals, 1.0).view(torch.uint8), finite)
+    # the positive codes are ordered like their values
+    pos = torch.arange(0x00, 0x7F, dtype=torch.uint8)
+    pv = oracle.dequantize_fp8(pos.view(oracle.FP8), 1.0)
+    assert torch.all(pv[1:] > pv[:-1])
+    # a power-of-two scale moves values without changing codes
+    assert torch.equal(oracle.quantize_fp8(vals * 0.25, 0.25).view(torch.uint8), finite)
+    # quantisation error is at most half a step: 2^-4 relative in the normal range
+    x = torch.randn(4096, generator=torch.Generator().manual_seed(2)) * 30
+    r = oracle.dequantize_fp8(oracle.quantize_fp8(x, 0.7), 0.7)
+    normal = x.abs() > 2.0 ** -6 * 0.7
+    assert ((r - x).abs()[normal] <= x.abs()[normal] * 2.0 ** -4 + 1e-7).all()
+
+
+def test_fp8_decode_on_grid_values_equals_the_16_bit_decode():
+    # K/V drawn from the e4m3 grid are stored exactly by FP8 and by bf16:
+    # the FP8 decode (scale 1) must equal the decode of the bf16 pools, which
+    # the golden vectors above pin.
+    gen = torch.Generator().manual_seed(21)
+    codes = torch.randint(0, 0x7F, (12, 4, 2, 8), generator=gen, dtype=torch.uint8)
+    sign = torch.randint(0, 2, codes.shape, generator=gen, dtype=torch.uint8) << 7
+    kc = (codes | sign).view(oracle.FP8)
+    vc = torch.randint(0, 0x7F, (12, 4, 2, 8), generator=gen, dtype=torch.uint8).view(oracle.FP8)
+    kb = oracle.dequantize_fp8(kc, 1.0).to(torch.bfloat16)
+    vb = oracle.dequantize_fp8(vc, 1.0).to(torch.bfloat16)
+    assert torch.equal(kb.float(), oracle.dequantize_fp8(kc, 1.0))  # bf16 holds them exactly
+    table = torch.tensor([[3, 7, 1], [5, 0, 11]])
+    lens = torch.tensor([10, 7])
+    q = torch.randn(2, 4, 8, generator=gen) * 0.05
+    a = oracle.paged_decode(q, kc, vc, table, lens, 0.3)
+    b = oracle.paged_decode(q, kb, vb, table, lens, 0.3)
+    assert torch.equal(a, b)
+    # scales: K scale multiplies the logits, V scale the output
+    a2 = oracle.paged_decode(q, kc, vc, table, lens, 0.3, k_scale=2.0, v_scale=0.5)
+    b2 = oracle.paged_decode(q * 2.0, kb, vb, table, lens, 0.3) * 0.5
+    assert torch.allclose(a2, b2, atol=1e-6)
+    # a store into an FP8 pool writes the quantised rows and nothing else
+    key = torch.randn(3, 2, 8, generator=gen)
+    ek, ev = oracle.store_kvcache(key, key * 2, kc, vc, torch.tensor([5, -1, 17]), k_scale=0.5,
+                                  v_scale=4.0)
+    assert torch.equal(ek[1, 1].view(torch.uint8), oracle.quantize_fp8(key[0], 0.5).view(torch.uint8))
+    assert torch.equal(ev[4, 1].view(torch.uint8),
+                       oracle.quantize_fp8(key[2] * 2, 4.0).view(torch.uint8))
+    untouched = torch.ones(12, 4, dtype=torch.bool)
+    untouched[1, 1] = untouched[4, 1] = False
+    assert torch.equal(ek.view(torch.uint8)[untouched], kc.view(torch.uint8)[untouched])

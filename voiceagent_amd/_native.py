@@ -20,7 +20,8 @@ VA_OK = 0
 VA_BF16, VA_F16, VA_F32 = 0, 1, 2
 VA_I32, VA_I64 = 0, 1
 VA_LENS_PER_SEQ, VA_LENS_CUMULATIVE = 0, 1
-ABI_VERSION = 3  # VA_ATTN_ABI_VERSION of the header these structs mirror
+VA_KV_NATIVE, VA_KV_FP8_E4M3 = 0, 1
+ABI_VERSION = 4  # VA_ATTN_ABI_VERSION of the header these structs mirror
 DECODE_NOALLOC_SCRATCH_BYTES = 4 << 20  # VA_DECODE_NOALLOC_SCRATCH_BYTES
 
 DTYPE_CODES = {torch.bfloat16: VA_BF16, torch.float16: VA_F16, torch.float32: VA_F32}
@@ -44,6 +45,9 @@ class KvPool(ctypes.Structure):
         ("stride_head", c_int64),
         ("block_size", c_int32),
         ("num_blocks", c_int32),
+        ("kv_format", c_int32),
+        ("k_scale", c_float),
+        ("v_scale", c_float),
     ]
 
 
@@ -182,6 +186,8 @@ class VarlenArgs(ctypes.Structure):
         ("table_width", c_int32),
         ("slot_mapping", c_void_p),
         ("slot_dtype", c_int32),
+        ("workspace", c_void_p),
+        ("workspace_bytes", c_size_t),
     ]
 
 
@@ -192,6 +198,7 @@ SIGNATURES = {
     "va_paged_decode": (c_int32, [ctypes.POINTER(DecodeArgs), c_void_p]),
     "va_paged_decode_noalloc": (c_int32, [ctypes.POINTER(DecodeArgs), c_void_p]),
     "va_varlen_attention": (c_int32, [ctypes.POINTER(VarlenArgs), c_void_p]),
+    "va_varlen_workspace_bytes": (c_size_t, [ctypes.POINTER(VarlenArgs)]),
     "va_qk_norm_rope": (c_int32, [ctypes.POINTER(QkNormRopeArgs), c_void_p]),
     "va_last_error": (ctypes.c_char_p, []),
     "va_abi_version": (c_int32, []),

@@ -138,6 +138,24 @@ struct F32 {
   }
 };
 
+// ------------------------------------------------------------- FP8 pools
+// OCP e4m3 (float8_e4m3fn) codes of FP8 KV pools.  Quantisation saturates to
+// +-448, the largest finite e4m3 value, before gfx950's round-to-nearest-even
+// conversion (v_cvt_pk_fp8_f32); a NaN stays NaN.  Every e4m3 value is
+// exactly representable in bf16 and f16, so dequantisation to either
+// (v_cvt_scalef32_pk_{bf16,f16}_fp8 with a unit scale) is exact.
+constexpr float kF8Max = 448.0f;
+__device__ inline float f8_sat(float x) {
+  return x > kF8Max ? kF8Max : (x < -kF8Max ? -kF8Max : x);
+}
+// Four floats (already multiplied by 1 / scale) to four e4m3 bytes, the
+// first in the low byte.
+__device__ inline uint32_t f8_pack4(float a, float b, float c, float d) {
+  int w = __builtin_amdgcn_cvt_pk_fp8_f32(f8_sat(a), f8_sat(b), 0, false);
+  w = __builtin_amdgcn_cvt_pk_fp8_f32(f8_sat(c), f8_sat(d), w, true);
+  return (uint32_t)w;
+}
+
 // ------------------------------------------------------------ memory access
 __device__ inline uint4 ld16(const void* p) { return *reinterpret_cast<const uint4*>(p); }
 // Non-temporal 16-byte load (the nt cache policy): for data read exactly once,
@@ -153,6 +171,34 @@ __device__ inline void st16(void* p, uint4 v) { *reinterpret_cast<uint4*>(p) = v
 __device__ inline int64_t load_index(const void* p, int64_t i, int is_i64) {
   return is_i64 ? reinterpret_cast<const int64_t*>(p)[i]
                 : (int64_t)reinterpret_cast<const int32_t*>(p)[i];
+}
+
+// The 16-bit word u of 8 elements of ET (BF16 or F16), each multiplied by
+// inv in fp32, as 8 e4m3 codes (element i in byte i).
+template <typename ET>
+__device__ inline uint2 f8_quant8(uint4 u, float inv) {
+  float f[8];
+  ET::unpack(u, f);
+  return make_uint2(f8_pack4(f[0] * inv, f[1] * inv, f[2] * inv, f[3] * inv),
+                    f8_pack4(f[4] * inv, f[5] * inv, f[6] * inv, f[7] * inv));
+}
+// 8 e4m3 codes (byte i = element i) as 8 elements of ET (BF16 or F16),
+// exactly.
+template <typename ET>
+__device__ inline uint4 f8_dequant8(uint2 c) {
+  uint32_t w[4];
+  if constexpr (ET::kIsBF16) {
+    w[0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(c.x, 1.0f, false));
+    w[1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(c.x, 1.0f, true));
+    w[2] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(c.y, 1.0f, false));
+    w[3] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(c.y, 1.0f, true));
+  } else {
+    w[0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(c.x, 1.0f, false));
+    w[1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(c.x, 1.0f, true));
+    w[2] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(c.y, 1.0f, false));
+    w[3] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(c.y, 1.0f, true));
+  }
+  return make_uint4(w[0], w[1], w[2], w[3]);
 }
 
 // ------------------------------------------------------- lane reductions

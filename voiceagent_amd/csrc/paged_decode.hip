@@ -42,6 +42,7 @@ static bool general_kernel_forced() {
 
 static bool use_mfma_decode(const va_decode_args* a) {
   if (a->dtype != VA_BF16 && a->dtype != VA_F16) return false;
+  const int64_t kv_eb = a->pool.kv_format == VA_KV_FP8_E4M3 ? 1 : 2;
   if (a->pool.block_size <= 0 || a->pool.block_size % kChunk != 0) return false;
   if (a->head_dim != 64 && a->head_dim != 128 && a->head_dim != 256) return false;
   if (a->num_kv_heads <= 0 || a->num_heads % a->num_kv_heads != 0) return false;
@@ -49,9 +50,11 @@ static bool use_mfma_decode(const va_decode_args* a) {
   if (G != 1 && G != 2 && G != 4 && G != 8) return false;
   // Per-lane DMA offsets inside a 16-row tile are 32-bit.
   if (a->pool.stride_slot < 0 ||
-      (kChunk - 1) * a->pool.stride_slot * 2 + (int64_t)a->head_dim * 2 >= ((int64_t)1 << 31))
+      (kChunk - 1) * a->pool.stride_slot * kv_eb + (int64_t)a->head_dim * kv_eb >=
+          ((int64_t)1 << 31))
     return false;
-  return !general_kernel_forced();
+  // FP8 pools have no general-kernel path, so forcing it does not apply.
+  return a->pool.kv_format == VA_KV_FP8_E4M3 || !general_kernel_forced();
 }
 
 static int mfma_unit_for(int D) {
@@ -263,6 +266,12 @@ int va::paged_decode_impl(const va_decode_args* a, void* stream) {
                sizeof(va_decode_args));
   const int eb = elem_bytes_of(a->dtype);
   VA_CHECK_ARG(eb != 0, "va_paged_decode: unknown dtype %d", a->dtype);
+  const bool f8 = a->pool.kv_format == VA_KV_FP8_E4M3;
+  VA_CHECK_ARG(a->pool.kv_format == VA_KV_NATIVE || f8, "va_paged_decode: unknown kv_format %d",
+               a->pool.kv_format);
+  VA_CHECK_ARG(!f8 || (a->pool.k_scale > 0.f && a->pool.v_scale > 0.f),
+               "va_paged_decode: FP8 pool scales must be positive");
+  const int kv_eb = f8 ? 1 : eb;  // bytes per pool element
   VA_CHECK_ARG(a->num_seqs >= 0, "va_paged_decode: num_seqs < 0");
   if (a->num_seqs == 0) return VA_OK;
   VA_CHECK_ARG(a->num_seqs <= 65535, "va_paged_decode: num_seqs > 65535");  // merge grid.y
@@ -291,12 +300,14 @@ int va::paged_decode_impl(const va_decode_args* a, void* stream) {
                "va_paged_decode: key_limit and table_read_width must be non-negative");
   VA_CHECK_ARG(a->valid_mask == nullptr || (a->valid_len >= 0 && a->valid_stride_seq >= 0),
                "va_paged_decode: valid_len and valid_stride_seq must be non-negative");
-  const int64_t strides[] = {a->q_stride_seq,        a->q_stride_head,        a->out_stride_seq,
-                             a->out_stride_head,     a->pool.stride_block,    a->pool.stride_slot,
-                             a->pool.stride_head,    a->new_k_stride_seq,     a->new_k_stride_head,
-                             a->new_v_stride_seq,    a->new_v_stride_head};
+  const int64_t strides[] = {a->q_stride_seq,      a->q_stride_head,     a->out_stride_seq,
+                             a->out_stride_head,   a->new_k_stride_seq,  a->new_k_stride_head,
+                             a->new_v_stride_seq,  a->new_v_stride_head};
   for (int64_t s : strides)
     VA_CHECK_ARG((s * eb) % 16 == 0, "va_paged_decode: strides must be 16-byte multiples");
+  const int64_t pstrides[] = {a->pool.stride_block, a->pool.stride_slot, a->pool.stride_head};
+  for (int64_t s : pstrides)
+    VA_CHECK_ARG((s * kv_eb) % 16 == 0, "va_paged_decode: pool strides must be 16-byte multiples");
   const uintptr_t ptrs[] = {(uintptr_t)a->q, (uintptr_t)a->out, (uintptr_t)a->pool.k,
                             (uintptr_t)a->pool.v, (uintptr_t)a->new_k, (uintptr_t)a->new_v};
   for (uintptr_t p : ptrs)
@@ -322,9 +333,9 @@ int va::paged_decode_impl(const va_decode_args* a, void* stream) {
   p.o_sh = a->out_stride_head * eb;
   p.kp = (char*)a->pool.k;
   p.vp = (char*)a->pool.v;
-  p.s_blk = a->pool.stride_block * eb;
-  p.s_slot = a->pool.stride_slot * eb;
-  p.s_head = a->pool.stride_head * eb;
+  p.s_blk = a->pool.stride_block * kv_eb;
+  p.s_slot = a->pool.stride_slot * kv_eb;
+  p.s_head = a->pool.stride_head * kv_eb;
   p.block_size = a->pool.block_size;
   p.num_blocks = a->pool.num_blocks;
   p.block_is_chunk_aligned = a->pool.block_size % kChunk == 0;
@@ -337,7 +348,7 @@ int va::paged_decode_impl(const va_decode_args* a, void* stream) {
                              a->pool.stride_block +
                          (int64_t)(a->pool.block_size - 1) * a->pool.stride_slot +
                          (int64_t)(a->num_kv_heads - 1) * a->pool.stride_head + a->head_dim;
-    p.pool_off32 = last * eb < ((int64_t)1 << 32) && a->pool.stride_block >= 0 &&
+    p.pool_off32 = last * kv_eb < ((int64_t)1 << 32) && a->pool.stride_block >= 0 &&
                    a->pool.stride_slot >= 0 && a->pool.stride_head >= 0;
   }
   p.table = a->block_tables;
@@ -366,7 +377,13 @@ int va::paged_decode_impl(const va_decode_args* a, void* stream) {
   p.split_tokens = pl.split_tokens;
   p.max_parts = pl.max_parts;
   p.dyn_split = pl.dyn_split;
-  p.scale_log2 = a->scale * 1.4426950408889634f;
+  // An FP8 pool's key scale multiplies every logit; its value scale the
+  // output (applied after the weighted sum).
+  p.scale_log2 = a->scale * (f8 ? a->pool.k_scale : 1.0f) * 1.4426950408889634f;
+  p.kv_fp8 = f8;
+  p.v_scale = f8 ? a->pool.v_scale : 1.0f;
+  p.inv_k = f8 ? 1.0f / a->pool.k_scale : 1.0f;
+  p.inv_v = f8 ? 1.0f / a->pool.v_scale : 1.0f;
   p.has_pro = a->prologue != nullptr;
   p.pro = PrologueParams{};
   if (a->prologue != nullptr) {
@@ -400,7 +417,17 @@ int va::paged_decode_impl(const va_decode_args* a, void* stream) {
   const dim3 grid(a->num_seqs, a->num_kv_heads, pl.max_parts);
   const hipStream_t s = (hipStream_t)stream;
   bool ok = false;
-  if (use_mfma_decode(a)) {
+  if (f8 && !use_mfma_decode(a)) {
+    set_error("va_paged_decode: an FP8 pool needs bf16/f16 q, a block size that is a multiple "
+              "of 16, head_dim 64|128|256 and group 1|2|4|8 (got dtype %d, block %d, head_dim %d, "
+              "group %d)",
+              a->dtype, a->pool.block_size, a->head_dim, G);
+    return VA_ERR_UNSUPPORTED;
+  }
+  if (f8) {
+    ok = a->dtype == VA_BF16 ? launch_paged_decode_mfma_f8<BF16>(a->head_dim, G, p, grid, s)
+                             : launch_paged_decode_mfma_f8<F16>(a->head_dim, G, p, grid, s);
+  } else if (use_mfma_decode(a)) {
     ok = a->dtype == VA_BF16 ? launch_paged_decode_mfma<BF16>(a->head_dim, G, p, grid, s)
                              : launch_paged_decode_mfma<F16>(a->head_dim, G, p, grid, s);
   } else {

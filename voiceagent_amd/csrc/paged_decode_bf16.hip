@@ -12,7 +12,7 @@ bool launch_paged_decode<BF16>(int D, int G, const DecodeParams& p, dim3 grid, h
 template <>
 bool launch_paged_decode_mfma<BF16>(int D, int G, const DecodeParams& p, dim3 grid,
                                     hipStream_t s) {
-  return dispatch_mfma_d<BF16>(D, G, p, grid, s);
+  return dispatch_mfma_d<BF16, false>(D, G, p, grid, s);
 }
 
 }  // namespace va

@@ -12,7 +12,7 @@ bool launch_paged_decode<F16>(int D, int G, const DecodeParams& p, dim3 grid, hi
 template <>
 bool launch_paged_decode_mfma<F16>(int D, int G, const DecodeParams& p, dim3 grid,
                                     hipStream_t s) {
-  return dispatch_mfma_d<F16>(D, G, p, grid, s);
+  return dispatch_mfma_d<F16, false>(D, G, p, grid, s);
 }
 
 }  // namespace va

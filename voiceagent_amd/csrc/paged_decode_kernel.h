@@ -78,6 +78,9 @@ struct DecodeParams {
   float* part_o;
   int32_t has_pro;  // apply the Qwen3 q/k prologue to q and the current row
   PrologueParams pro;
+  int32_t kv_fp8;        // the pool holds e4m3 codes (matrix-core kernel only)
+  float v_scale;         // output factor: v_scale of an FP8 pool, else 1
+  float inv_k, inv_v;    // FP8 pool: 1 / k_scale, 1 / v_scale (current-row quantisation)
 };
 
 constexpr int kChunk = 16;
@@ -134,6 +137,24 @@ __device__ inline void store_detached_row(const DecodeParams& p, int h, int64_t 
       sb * p.s_blk + (slot - sb * p.block_size) * p.s_slot + (int64_t)h * p.s_head + col16;
   st16(p.kp + dst, kr);
   st16(p.vp + dst, vr);
+}
+
+// The same for an FP8 pool: this lane's 8 codes (at byte column col8).
+__device__ inline void store_detached_row_f8(const DecodeParams& p, int h, int64_t table_row,
+                                             int L, int col_new, int64_t new_slot, int col8,
+                                             uint2 kr, uint2 vr) {
+  int64_t slot = new_slot;
+  if (p.new_slots == nullptr) {
+    const int64_t blk =
+        col_new < p.table_width_full ? load_index(p.table, table_row + col_new, p.table_i64) : 0;
+    slot = (blk >= 0 && blk < p.num_blocks) ? blk * p.block_size + (L - 1) % p.block_size : -1;
+  }
+  if (slot < 0 || slot >= (int64_t)p.num_blocks * p.block_size) return;
+  const int64_t sb = slot / p.block_size;
+  const int64_t dst =
+      sb * p.s_blk + (slot - sb * p.block_size) * p.s_slot + (int64_t)h * p.s_head + col8;
+  *reinterpret_cast<uint2*>(p.kp + dst) = kr;
+  *reinterpret_cast<uint2*>(p.vp + dst) = vr;
 }
 
 __device__ inline int partition_tokens(const DecodeParams& p, int L) {
@@ -610,7 +631,9 @@ constexpr int kMaxParts = 256;
 // 2^(m_q - M) reach the o sums through readlane (q is wave-uniform).  Loads
 // use clamped indices and are masked afterwards, so no load sits behind a
 // branch.
-template <typename ET, int D, int G>
+// kTag only separates the instantiations of the translation units that
+// launch the kernel (native and FP8 pools), which then never share a name.
+template <typename ET, int D, int G, int kTag = 0>
 __global__ __launch_bounds__(256) void paged_decode_merge_kernel(DecodeParams p) {
   constexpr int E = ET::kPerVec;
   constexpr int kPerLane = kMaxParts / 64;

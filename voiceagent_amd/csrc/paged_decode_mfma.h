@@ -128,15 +128,29 @@ constexpr float kDecLazy = 8.0f;
 
 
 // kMask: the launch has a key_valid_mask (a separate instantiation, so the
-// kernel without one carries none of its loads or branches).
-template <typename ET, int D, int G, bool kProlog, bool kMask>
+// kernel without one carries none of its loads or branches).  kF8: the pool
+// holds OCP e4m3 codes; a staged tile of codes is converted, exactly, into a
+// 16-bit tile in the wave's conversion area, which the matrix-core reads
+// below use as they use a staged 16-bit tile.  k_scale is folded into the
+// softmax scale and v_scale into the output.
+template <typename ET, int D, int G, bool kProlog, bool kMask, bool kF8>
 __global__ __launch_bounds__(MfmaDecodeShape<D>::W * 64, 1) void paged_decode_mfma_kernel(
     DecodeParams p) {
   using Sh = MfmaDecodeShape<D>;
   using M = DecodeMma<ET>;
-  constexpr int W = Sh::W, S = Sh::S, NI = Sh::NI, ROWB = Sh::ROWB, CPR = Sh::CPR;
-  constexpr int RPI = Sh::RPI, TILE_B = Sh::TILE_B, DS = Sh::DS, DT = Sh::DT;
+  constexpr int W = Sh::W, S = Sh::S, ROWB = Sh::ROWB;
+  constexpr int TILE_B = Sh::TILE_B, DS = Sh::DS, DT = Sh::DT;
   constexpr int LPR = Sh::LPR, RPL = Sh::RPL, E = 8;
+  // A tile as the DMA stages it: 16-bit rows, or rows of D e4m3 codes.
+  constexpr int PROWB = kF8 ? D : ROWB;     // staged bytes per row
+  constexpr int CPR = PROWB / 16;           // 16-byte chunks per staged row
+  constexpr int RPI = 64 / CPR;             // rows per DMA instruction (1 KiB)
+  constexpr int NI = kChunk / RPI;          // DMA instructions per tile, K or V
+  constexpr int PTILE = kChunk * PROWB;     // staged bytes of one K (or V) tile
+  constexpr int STAGE_B = 2 * PTILE;
+  constexpr int CONV_B = kF8 ? 2 * TILE_B : 0;
+  constexpr int WAVE_B = S * STAGE_B + CONV_B;  // LDS bytes per wave
+  static_assert(WAVE_B <= Sh::WAVE_B, "FP8 stages and conversion area fit the 16-bit ring");
   constexpr int NT = W * 64;
   constexpr int QROWS = (G + RPL - 1) / RPL;  // query rows per lane in the row layout
   static_assert(G <= 16, "at most 16 query heads per kv head");
@@ -274,18 +288,20 @@ __global__ __launch_bounds__(MfmaDecodeShape<D>::W * 64, 1) void paged_decode_mf
                                  col * E);
   }
 
-  char* const s_wave = s_buf + wave * Sh::WAVE_B;
+  char* const s_wave = s_buf + wave * WAVE_B;
   const uint32_t lds_wave = __builtin_amdgcn_readfirstlane(
       (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)s_wave);
 
   // ---- tile DMA: instruction i of a tile moves rows RPI i .. RPI i + RPI - 1;
   // lane l writes row RPI i + l / CPR at chunk position l % CPR, i.e. reads
   // logical chunk (l % CPR) ^ swz(row) of that row ----
+  // (Codes are staged unswizzled: the conversion reads them in order.)
   uint32_t loff[NI];
 #pragma unroll
   for (int i = 0; i < NI; ++i) {
     const int row = RPI * i + lane / CPR;
-    loff[i] = (uint32_t)(row * p.s_slot) + (uint32_t)(((lane % CPR) ^ dec_swz<D>(row)) << 4);
+    const int pos = kF8 ? lane % CPR : (lane % CPR) ^ dec_swz<D>(row);
+    loff[i] = (uint32_t)(row * p.s_slot) + (uint32_t)(pos << 4);
   }
   const char* zero_row = reinterpret_cast<const char*>(&kDecZeroRow);
   const int64_t head_off = (int64_t)h * p.s_head;
@@ -304,7 +320,7 @@ __global__ __launch_bounds__(MfmaDecodeShape<D>::W * 64, 1) void paged_decode_mf
     }
     const int tb = start + (wave + W * k) * kChunk;
     const int32_t blk = __builtin_amdgcn_readlane(tab, k & 63);
-    const uint32_t dst = lds_wave + (uint32_t)((k % S) * 2 * TILE_B);
+    const uint32_t dst = lds_wave + (uint32_t)((k % S) * STAGE_B);
     if (blk >= 0 && blk < p.num_blocks) {
       const int64_t off = (int64_t)blk * p.s_blk + (int64_t)fast_mod((uint32_t)tb, p.bs_div) * p.s_slot +
                           head_off;
@@ -313,7 +329,7 @@ __global__ __launch_bounds__(MfmaDecodeShape<D>::W * 64, 1) void paged_decode_mf
 #pragma unroll
       for (int i = 0; i < NI; ++i) dma16_nt(loff[i], kb, dst + i * 1024);
 #pragma unroll
-      for (int i = 0; i < NI; ++i) dma16_nt(loff[i], vb, dst + TILE_B + i * 1024);
+      for (int i = 0; i < NI; ++i) dma16_nt(loff[i], vb, dst + PTILE + i * 1024);
     } else {
 #pragma unroll
       for (int i = 0; i < 2 * NI; ++i) dma16(zero_row, dst + i * 1024);
@@ -427,10 +443,25 @@ __global__ __launch_bounds__(MfmaDecodeShape<D>::W * 64, 1) void paged_decode_mf
                       : make_uint4(0, 0, 0, 0);
   }
 
+  // FP8 pool: the current row is stored as codes and attended as their
+  // values, as a later step reads it back.
+  uint2 kq = make_uint2(0u, 0u), vq = make_uint2(0u, 0u);
+  if constexpr (kF8) {
+    if (p.new_k != nullptr) {
+      kq = f8_quant8<ET>(kcur, p.inv_k);
+      vq = f8_quant8<ET>(vcur, p.inv_v);
+      kcur = f8_dequant8<ET>(kq);
+      vcur = f8_dequant8<ET>(vq);
+    }
+  }
   // The current row is not attended in place: wave 0 of the first partition
   // writes it.
-  if (detached && part == 0 && wave == 0 && rg == 0)
-    store_detached_row(p, h, table_row, Lr, col_new, new_slot, col * 16, kcur, vcur);
+  if (detached && part == 0 && wave == 0 && rg == 0) {
+    if constexpr (kF8)
+      store_detached_row_f8(p, h, table_row, Lr, col_new, new_slot, col * 8, kq, vq);
+    else
+      store_detached_row(p, h, table_row, Lr, col_new, new_slot, col * 16, kcur, vcur);
+  }
 
   if (!early) {
     for (int k = 0; k < S; ++k)
@@ -461,8 +492,33 @@ __global__ __launch_bounds__(MfmaDecodeShape<D>::W * 64, 1) void paged_decode_mf
       wait_vmcnt<2 * NI * (S - 1)>();  // tiles k + 1 .. k + S - 1 may stay in flight
     else
       wait_vmcnt<0>();
-    char* sK = s_wave + (k % S) * 2 * TILE_B;
-    char* sV = sK + TILE_B;
+    char* sK = s_wave + (k % S) * STAGE_B;
+    char* sV = sK + PTILE;
+    if constexpr (kF8) {
+      // Codes to 16-bit rows in the conversion area, each 16-byte chunk of
+      // the 16-bit tile at its swizzled position; then the stage is free
+      // and takes the wave's tile k + S right away.
+      char* cK = s_wave + S * STAGE_B;
+      char* cV = cK + TILE_B;
+      constexpr int NCH = PTILE / 16 / 64;  // code chunks per lane, K or V
+#pragma unroll
+      for (int i = 0; i < NCH; ++i) {
+        const int e = lane + 64 * i;
+        const int row = e / CPR, c8 = e % CPR;
+        const int p0 = ((2 * c8) ^ dec_swz<D>(row)) << 4;
+        const int p1 = ((2 * c8 + 1) ^ dec_swz<D>(row)) << 4;
+        const uint4 ck = *reinterpret_cast<const uint4*>(sK + e * 16);
+        const uint4 cv = *reinterpret_cast<const uint4*>(sV + e * 16);
+        *reinterpret_cast<uint4*>(cK + row * ROWB + p0) = f8_dequant8<ET>(make_uint2(ck.x, ck.y));
+        *reinterpret_cast<uint4*>(cK + row * ROWB + p1) = f8_dequant8<ET>(make_uint2(ck.z, ck.w));
+        *reinterpret_cast<uint4*>(cV + row * ROWB + p0) = f8_dequant8<ET>(make_uint2(cv.x, cv.y));
+        *reinterpret_cast<uint4*>(cV + row * ROWB + p1) = f8_dequant8<ET>(make_uint2(cv.z, cv.w));
+      }
+      wait_lgkmcnt0();
+      if (k + S < ntw) issue(k + S);
+      sK = cK;
+      sV = cV;
+    }
     const int c = wave + W * k;  // partition chunk of this tile
     const int tb = start + c * kChunk;
     if (k > 0 && (k & 63) == 0) {
@@ -486,7 +542,8 @@ __global__ __launch_bounds__(MfmaDecodeShape<D>::W * 64, 1) void paged_decode_mf
         *reinterpret_cast<uint4*>(sV + r * ROWB + pos16) = vcur;
         const int64_t sb = p.slot_small ? (int64_t)fast_div((uint32_t)slot, p.bs_div)
                                         : slot / p.block_size;
-        cur_dst = sb * p.s_blk + (slot - sb * p.block_size) * p.s_slot + head_off + col * 16;
+        cur_dst = sb * p.s_blk + (slot - sb * p.block_size) * p.s_slot + head_off +
+                  col * (kF8 ? 8 : 16);
       }
     }
 
@@ -549,9 +606,12 @@ __global__ __launch_bounds__(MfmaDecodeShape<D>::W * 64, 1) void paged_decode_mf
       au.y &= keep1;
       o[dt] = M::pv(__builtin_bit_cast(mf_s16x4, au), pb, o[dt]);
     }
-    // The stage is free once its LDS reads have returned.
-    wait_lgkmcnt0();
-    if (k + S < ntw) issue(k + S);
+    // The stage is free once its LDS reads have returned (an FP8 stage was
+    // reissued after its conversion).
+    if constexpr (!kF8) {
+      wait_lgkmcnt0();
+      if (k + S < ntw) issue(k + S);
+    }
   }
 
   // ---- merge the waves through LDS ----
@@ -603,14 +663,14 @@ __global__ __launch_bounds__(MfmaDecodeShape<D>::W * 64, 1) void paged_decode_mf
       acc += f * *reinterpret_cast<const mf_f32x4*>(s_o + (w * G + g) * D + d);
     }
     if (nparts == 1) {
-      const float inv = Lt > 0.f ? 1.f / Lt : 0.f;
+      const float inv = Lt > 0.f ? p.v_scale / Lt : 0.f;
       uint2 u;
       u.x = M::pack2(acc[0] * inv, acc[1] * inv);
       u.y = M::pack2(acc[2] * inv, acc[3] * inv);
       *reinterpret_cast<uint2*>(p.out + b * p.o_sb + (int64_t)(h * G + g) * p.o_sh + d * 2) = u;
     } else {
       const int64_t slot = (pair * p.max_parts + part) * G + g;
-      *reinterpret_cast<mf_f32x4*>(p.part_o + slot * D + d) = acc;
+      *reinterpret_cast<mf_f32x4*>(p.part_o + slot * D + d) = acc * p.v_scale;
       if (d == 0) {
         p.part_ml[slot * 2] = Mx;
         p.part_ml[slot * 2 + 1] = Lt;
@@ -618,54 +678,66 @@ __global__ __launch_bounds__(MfmaDecodeShape<D>::W * 64, 1) void paged_decode_mf
     }
   }
   if (cur_dst >= 0) {
-    st16(p.kp + cur_dst, kcur);
-    st16(p.vp + cur_dst, vcur);
+    if constexpr (kF8) {
+      *reinterpret_cast<uint2*>(p.kp + cur_dst) = kq;
+      *reinterpret_cast<uint2*>(p.vp + cur_dst) = vq;
+    } else {
+      st16(p.kp + cur_dst, kcur);
+      st16(p.vp + cur_dst, vcur);
+    }
   }
 }
 
 // ------------------------------------------------------------- launching
-template <typename ET, int D, int G>
+template <typename ET, int D, int G, bool kF8>
 static void launch_decode_mfma(const DecodeParams& p, dim3 grid, hipStream_t s) {
   constexpr int NT = MfmaDecodeShape<D>::W * 64;
   const bool mask = p.valid != nullptr && p.valid_len > 0;
   if (p.has_pro && mask)
-    hipLaunchKernelGGL((paged_decode_mfma_kernel<ET, D, G, true, true>), grid, dim3(NT), 0, s, p);
-  else if (p.has_pro)
-    hipLaunchKernelGGL((paged_decode_mfma_kernel<ET, D, G, true, false>), grid, dim3(NT), 0, s, p);
-  else if (mask)
-    hipLaunchKernelGGL((paged_decode_mfma_kernel<ET, D, G, false, true>), grid, dim3(NT), 0, s, p);
-  else
-    hipLaunchKernelGGL((paged_decode_mfma_kernel<ET, D, G, false, false>), grid, dim3(NT), 0, s,
-                       p);
-  if (p.max_parts > 1)
-    hipLaunchKernelGGL((paged_decode_merge_kernel<ET, D, G>), dim3(grid.y, grid.x), dim3(256), 0,
+    hipLaunchKernelGGL((paged_decode_mfma_kernel<ET, D, G, true, true, kF8>), grid, dim3(NT), 0,
                        s, p);
+  else if (p.has_pro)
+    hipLaunchKernelGGL((paged_decode_mfma_kernel<ET, D, G, true, false, kF8>), grid, dim3(NT), 0,
+                       s, p);
+  else if (mask)
+    hipLaunchKernelGGL((paged_decode_mfma_kernel<ET, D, G, false, true, kF8>), grid, dim3(NT), 0,
+                       s, p);
+  else
+    hipLaunchKernelGGL((paged_decode_mfma_kernel<ET, D, G, false, false, kF8>), grid, dim3(NT), 0,
+                       s, p);
+  if (p.max_parts > 1)
+    hipLaunchKernelGGL((paged_decode_merge_kernel<ET, D, G, kF8 ? 1 : 0>), dim3(grid.y, grid.x),
+                       dim3(256), 0, s, p);
 }
 
-template <typename ET, int D>
+template <typename ET, int D, bool kF8>
 static bool dispatch_mfma_g(int G, const DecodeParams& p, dim3 grid, hipStream_t s) {
   switch (G) {
-    case 1: launch_decode_mfma<ET, D, 1>(p, grid, s); return true;
-    case 2: launch_decode_mfma<ET, D, 2>(p, grid, s); return true;
-    case 4: launch_decode_mfma<ET, D, 4>(p, grid, s); return true;
-    case 8: launch_decode_mfma<ET, D, 8>(p, grid, s); return true;
+    case 1: launch_decode_mfma<ET, D, 1, kF8>(p, grid, s); return true;
+    case 2: launch_decode_mfma<ET, D, 2, kF8>(p, grid, s); return true;
+    case 4: launch_decode_mfma<ET, D, 4, kF8>(p, grid, s); return true;
+    case 8: launch_decode_mfma<ET, D, 8, kF8>(p, grid, s); return true;
     default: return false;
   }
 }
 
-template <typename ET>
+template <typename ET, bool kF8>
 static bool dispatch_mfma_d(int D, int G, const DecodeParams& p, dim3 grid, hipStream_t s) {
   switch (D) {
-    case 64: return dispatch_mfma_g<ET, 64>(G, p, grid, s);
-    case 128: return dispatch_mfma_g<ET, 128>(G, p, grid, s);
-    case 256: return dispatch_mfma_g<ET, 256>(G, p, grid, s);
+    case 64: return dispatch_mfma_g<ET, 64, kF8>(G, p, grid, s);
+    case 128: return dispatch_mfma_g<ET, 128, kF8>(G, p, grid, s);
+    case 256: return dispatch_mfma_g<ET, 256, kF8>(G, p, grid, s);
     default: return false;
   }
 }
 
 // Launch the matrix-core decode (and, when partitioned, the merge) for one
-// 16-bit element type; false for an unsupported (head_dim, group) pair.
+// 16-bit element type over a 16-bit pool (launch_paged_decode_mfma) or an
+// FP8 pool (launch_paged_decode_mfma_f8, in its own translation units);
+// false for an unsupported (head_dim, group) pair.
 template <typename ET>
 bool launch_paged_decode_mfma(int D, int G, const DecodeParams& p, dim3 grid, hipStream_t s);
+template <typename ET>
+bool launch_paged_decode_mfma_f8(int D, int G, const DecodeParams& p, dim3 grid, hipStream_t s);
 
 }  // namespace va

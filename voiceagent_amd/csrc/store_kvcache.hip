@@ -12,6 +12,10 @@
 // bf16 row (2 KiB) is moved by 128 lanes with one dwordx4 load and one
 // dwordx4 store each; consecutive lanes touch consecutive 16-byte words, so
 // both sides are fully coalesced.
+//
+// An FP8 pool (VA_KV_FP8_E4M3) receives each 16-byte word of 8 16-bit
+// elements as 8 e4m3 codes, x * (1 / scale) saturated to +-448 and rounded
+// to nearest even (one 8-byte store per lane).
 #include "common.h"
 
 namespace va {
@@ -31,10 +35,13 @@ struct StoreParams {
   int32_t num_tokens;
   int32_t words_per_head;  // head_dim * elem_bytes / 16
   int32_t words_per_row;   // num_kv_heads * words_per_head
+  float inv_k, inv_v;      // FP8 pools: 1 / k_scale, 1 / v_scale
 };
 
 constexpr int kStoreThreads = 256;
 
+// kF8: the pool holds e4m3 codes of the 16-bit elements of ET.
+template <bool kF8, typename ET>
 __global__ __launch_bounds__(kStoreThreads) void store_kvcache_kernel(StoreParams p) {
   // Work items: (token, kv-tensor, word) flattened; each thread moves 16 B.
   const int64_t words_per_tok = 2 * (int64_t)p.words_per_row;
@@ -55,7 +62,11 @@ __global__ __launch_bounds__(kStoreThreads) void store_kvcache_kernel(StoreParam
                            : p.key + tok * p.key_stride_tok + head * p.key_stride_head;
     char* dst = (is_v ? p.v_pool : p.k_pool) + blk * p.stride_block + off * p.stride_slot +
                 head * p.stride_head;
-    st16(dst + word * 16, ld16(src + word * 16));
+    if constexpr (kF8)
+      *reinterpret_cast<uint2*>(dst + word * 8) =
+          f8_quant8<ET>(ld16(src + word * 16), is_v ? p.inv_v : p.inv_k);
+    else
+      st16(dst + word * 16, ld16(src + word * 16));
   }
 }
 
@@ -81,6 +92,13 @@ extern "C" int va_store_kvcache(const va_store_args* a, void* stream) {
                a->struct_size, sizeof(va_store_args));
   const int eb = elem_bytes(a->dtype);
   VA_CHECK_ARG(eb != 0, "va_store_kvcache: unknown dtype %d", a->dtype);
+  const bool f8 = a->pool.kv_format == VA_KV_FP8_E4M3;
+  VA_CHECK_ARG(a->pool.kv_format == VA_KV_NATIVE || f8, "va_store_kvcache: unknown kv_format %d",
+               a->pool.kv_format);
+  VA_CHECK_ARG(!f8 || a->dtype != VA_F32, "va_store_kvcache: an FP8 pool needs 16-bit key/value");
+  VA_CHECK_ARG(!f8 || (a->pool.k_scale > 0.f && a->pool.v_scale > 0.f),
+               "va_store_kvcache: FP8 pool scales must be positive");
+  const int pb = f8 ? 1 : eb;  // bytes per pool element
   VA_CHECK_ARG(a->num_tokens >= 0, "va_store_kvcache: num_tokens < 0");
   if (a->num_tokens == 0) return VA_OK;
   VA_CHECK_ARG(a->key && a->value && a->pool.k && a->pool.v && a->slot_mapping,
@@ -93,11 +111,14 @@ extern "C" int va_store_kvcache(const va_store_args* a, void* stream) {
   VA_CHECK_ARG(a->slot_dtype == VA_I32 || a->slot_dtype == VA_I64,
                "va_store_kvcache: slot_dtype must be VA_I32 or VA_I64");
   // 16-byte alignment of every row start the kernel touches.
-  const int64_t strides[] = {a->key_stride_tok,  a->key_stride_head,   a->value_stride_tok,
-                             a->value_stride_head, a->pool.stride_block, a->pool.stride_slot,
-                             a->pool.stride_head};
+  const int64_t strides[] = {a->key_stride_tok, a->key_stride_head, a->value_stride_tok,
+                             a->value_stride_head};
   for (int64_t s : strides)
     VA_CHECK_ARG((s * eb) % 16 == 0, "va_store_kvcache: strides must be 16-byte multiples");
+  const int64_t pstrides[] = {a->pool.stride_block, a->pool.stride_slot, a->pool.stride_head};
+  for (int64_t s : pstrides)
+    VA_CHECK_ARG((s * pb) % (f8 ? 8 : 16) == 0,
+                 "va_store_kvcache: pool strides must be 16-byte (FP8: 8-byte) multiples");
   const uintptr_t ptrs[] = {(uintptr_t)a->key, (uintptr_t)a->value, (uintptr_t)a->pool.k,
                             (uintptr_t)a->pool.v};
   for (uintptr_t p : ptrs) VA_CHECK_ARG(p % 16 == 0, "va_store_kvcache: pointers must be 16-byte aligned");
@@ -111,9 +132,11 @@ extern "C" int va_store_kvcache(const va_store_args* a, void* stream) {
   p.value_stride_head = a->value_stride_head * eb;
   p.k_pool = (char*)a->pool.k;
   p.v_pool = (char*)a->pool.v;
-  p.stride_block = a->pool.stride_block * eb;
-  p.stride_slot = a->pool.stride_slot * eb;
-  p.stride_head = a->pool.stride_head * eb;
+  p.stride_block = a->pool.stride_block * pb;
+  p.stride_slot = a->pool.stride_slot * pb;
+  p.stride_head = a->pool.stride_head * pb;
+  p.inv_k = f8 ? 1.0f / a->pool.k_scale : 1.0f;
+  p.inv_v = f8 ? 1.0f / a->pool.v_scale : 1.0f;
   p.capacity = (int64_t)a->pool.num_blocks * a->pool.block_size;
   p.block_size = a->pool.block_size;
   p.slots = a->slot_mapping;
@@ -125,7 +148,15 @@ extern "C" int va_store_kvcache(const va_store_args* a, void* stream) {
   const int64_t total = (int64_t)a->num_tokens * 2 * p.words_per_row;
   int64_t grid = (total + kStoreThreads - 1) / kStoreThreads;
   if (grid > 65536) grid = 65536;
-  hipLaunchKernelGGL(store_kvcache_kernel, dim3((unsigned)grid), dim3(kStoreThreads), 0,
-                     (hipStream_t)stream, p);
+  const hipStream_t s = (hipStream_t)stream;
+  if (!f8)
+    hipLaunchKernelGGL((store_kvcache_kernel<false, BF16>), dim3((unsigned)grid),
+                       dim3(kStoreThreads), 0, s, p);
+  else if (a->dtype == VA_BF16)
+    hipLaunchKernelGGL((store_kvcache_kernel<true, BF16>), dim3((unsigned)grid),
+                       dim3(kStoreThreads), 0, s, p);
+  else
+    hipLaunchKernelGGL((store_kvcache_kernel<true, F16>), dim3((unsigned)grid),
+                       dim3(kStoreThreads), 0, s, p);
   return check_launch("va_store_kvcache");
 }

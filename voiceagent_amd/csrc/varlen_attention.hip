@@ -755,7 +755,103 @@ static bool dispatch_varlen(int D, int G, const VarlenParams& p, bool causal,
   }
 }
 
+// ------------------------------------------------------- FP8 pool prefix
+// With an FP8 pool the attention kernel above reads the paged prefix from a
+// 16-bit copy: f8_prefix_gather_kernel dequantises, for every sequence s and
+// table column c < ceil(prefix_s / block_size) (prefix_s = k_len - q_len,
+// or k_len when every key comes from the pool), block table[s][c] into
+// workspace block s W + c, laid out [slot][kv head][d], and maps (s, c) to
+// it in a workspace table (-1 for an unmapped block or a column past the
+// prefix).  The copy holds code * scale rounded to the 16-bit type.  The
+// new rows are quantised into the FP8 pool by the store kernel after the
+// attention.
+struct F8GatherParams {
+  const char* kp;
+  const char* vp;
+  int64_t s_blk, s_slot, s_head;  // bytes of the FP8 pool
+  int32_t block_size, num_blocks, num_kv_heads, head_dim;
+  const void* table;
+  int64_t t_sb;
+  int32_t table_i64, table_width;
+  const int32_t* cu_q;
+  const int32_t* cu_k;
+  int32_t all_from_pool;  // k is NULL: every key comes from the pool
+  int32_t width;          // W, workspace columns per sequence
+  float k_scale, v_scale;
+  int32_t* out_table;     // [num_seqs, W]
+  char* out_k;            // [num_seqs W, block_size, num_kv_heads, head_dim]
+  char* out_v;
+};
+
+template <typename ET>
+__global__ __launch_bounds__(256) void f8_prefix_gather_kernel(F8GatherParams g) {
+  const int c = blockIdx.x;
+  const int s = blockIdx.y;
+  const int ql = g.cu_q[s + 1] - g.cu_q[s];
+  const int kl = g.cu_k[s + 1] - g.cu_k[s];
+  const int prefix = g.all_from_pool ? kl : kl - ql;
+  const int64_t entry = (c * (int64_t)g.block_size < prefix)
+                            ? (c < g.table_width ? load_index(g.table, s * g.t_sb + c, g.table_i64)
+                                                 : 0)
+                            : -1;
+  const bool ok = entry >= 0 && entry < g.num_blocks;
+  const int64_t dst_blk = (int64_t)s * g.width + c;
+  if (threadIdx.x == 0) g.out_table[dst_blk] = ok ? (int32_t)dst_blk : -1;
+  if (!ok) return;
+  const int cpr = g.head_dim / 16;  // 16-code chunks per row
+  const int per = g.block_size * g.num_kv_heads * cpr;
+  const int64_t row_elems = (int64_t)g.num_kv_heads * g.head_dim;
+  for (int e = threadIdx.x; e < 2 * per; e += blockDim.x) {
+    const int is_v = e >= per;
+    const int r = is_v ? e - per : e;
+    const int ch = r % cpr;
+    const int head = (r / cpr) % g.num_kv_heads;
+    const int slot = r / (cpr * g.num_kv_heads);
+    const uint4 codes = ld16((is_v ? g.vp : g.kp) + entry * g.s_blk + slot * g.s_slot +
+                             head * g.s_head + ch * 16);
+    const float sc = is_v ? g.v_scale : g.k_scale;
+    char* dst = (is_v ? g.out_v : g.out_k) +
+                ((dst_blk * g.block_size + slot) * row_elems + (int64_t)head * g.head_dim +
+                 ch * 16) * 2;
+    float f[8];
+    ET::unpack(f8_dequant8<ET>(make_uint2(codes.x, codes.y)), f);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) f[i] *= sc;
+    st16(dst, ET::pack(f));
+    ET::unpack(f8_dequant8<ET>(make_uint2(codes.z, codes.w)), f);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) f[i] *= sc;
+    st16(dst + 16, ET::pack(f));
+  }
+}
+
+struct F8Layout {
+  int64_t width;  // W
+  size_t table_bytes, block_bytes, total;
+};
+
+// Workspace of the FP8 prefix copy (zero when the call reads no FP8 pool).
+static F8Layout f8_layout(const va_varlen_args* a) {
+  F8Layout l{};
+  if (a->pool.k == nullptr || a->pool.kv_format != VA_KV_FP8_E4M3 || a->block_tables == nullptr ||
+      a->pool.block_size <= 0 || a->num_seqs <= 0 || a->max_seqlen_k <= 0)
+    return l;
+  l.width = (a->max_seqlen_k + a->pool.block_size - 1) / a->pool.block_size;
+  const size_t blocks = (size_t)a->num_seqs * (size_t)l.width;
+  l.table_bytes = (blocks * 4 + 255) / 256 * 256;
+  l.block_bytes = blocks * (size_t)a->pool.block_size * a->num_kv_heads * a->head_dim * 2;
+  l.total = l.table_bytes + 2 * l.block_bytes;
+  return l;
+}
+
+static int varlen_native(const va_varlen_args* a, void* stream);
+
 }  // namespace va
+
+extern "C" size_t va_varlen_workspace_bytes(const va_varlen_args* a) {
+  if (a == nullptr || a->struct_size != sizeof(va_varlen_args)) return 0;
+  return va::f8_layout(a).total;
+}
 
 extern "C" int va_varlen_attention(const va_varlen_args* a, void* stream) {
   using namespace va;
@@ -765,6 +861,114 @@ extern "C" int va_varlen_attention(const va_varlen_args* a, void* stream) {
                a->struct_size, sizeof(va_varlen_args));
   VA_CHECK_ARG(a->num_seqs >= 0, "va_varlen_attention: num_seqs < 0");
   if (a->num_seqs == 0 || a->total_q == 0) return VA_OK;
+  const bool has_pool = a->pool.k != nullptr;
+  VA_CHECK_ARG(!has_pool || a->pool.kv_format == VA_KV_NATIVE ||
+                   a->pool.kv_format == VA_KV_FP8_E4M3,
+               "va_varlen_attention: unknown kv_format %d", a->pool.kv_format);
+  if (!has_pool || a->pool.kv_format == VA_KV_NATIVE) return varlen_native(a, stream);
+
+  // ---- FP8 pool: dequantised prefix copy, attention over it, then the store ----
+  VA_CHECK_ARG(a->dtype == VA_BF16 || a->dtype == VA_F16,
+               "va_varlen_attention: dtype must be VA_BF16 or VA_F16 (MFMA path)");
+  VA_CHECK_ARG(a->pool.v && a->block_tables && a->pool.block_size > 0 && a->pool.num_blocks >= 0 &&
+                   a->table_width >= 0 && a->cu_seqlens_q && a->cu_seqlens_k,
+               "va_varlen_attention: incomplete pool description");
+  VA_CHECK_ARG(a->pool.k_scale > 0.f && a->pool.v_scale > 0.f,
+               "va_varlen_attention: FP8 pool scales must be positive");
+  VA_CHECK_ARG(a->head_dim % 16 == 0 && a->num_kv_heads > 0,
+               "va_varlen_attention: FP8 pool head_dim must be a multiple of 16");
+  VA_CHECK_ARG(a->max_seqlen_k > 0, "va_varlen_attention: an FP8 pool needs max_seqlen_k, the "
+                                    "bound of every k_len");
+  VA_CHECK_ARG(a->table_dtype == VA_I32 || a->table_dtype == VA_I64,
+               "va_varlen_attention: table_dtype");
+  const int64_t pstrides[] = {a->pool.stride_block, a->pool.stride_slot, a->pool.stride_head};
+  for (int64_t s : pstrides)
+    VA_CHECK_ARG(s % 16 == 0, "va_varlen_attention: FP8 pool strides must be 16-byte multiples");
+  VA_CHECK_ARG((uintptr_t)a->pool.k % 16 == 0 && (uintptr_t)a->pool.v % 16 == 0,
+               "va_varlen_attention: pointers must be 16-byte aligned");
+  const F8Layout lay = f8_layout(a);
+  VA_CHECK_ARG(lay.width <= 65535 && a->num_seqs <= 65535,
+               "va_varlen_attention: max_seqlen_k / block_size too large for the FP8 prefix copy");
+  if (a->workspace == nullptr || a->workspace_bytes < lay.total) {
+    set_error("va_varlen_attention: workspace of %zu bytes needed for the FP8 prefix copy, %zu "
+              "given",
+              lay.total, a->workspace_bytes);
+    return VA_ERR_WORKSPACE;
+  }
+  VA_CHECK_ARG((uintptr_t)a->workspace % 16 == 0, "va_varlen_attention: workspace alignment");
+  char* ws = (char*)a->workspace;
+  F8GatherParams g;
+  g.kp = (const char*)a->pool.k;
+  g.vp = (const char*)a->pool.v;
+  g.s_blk = a->pool.stride_block;
+  g.s_slot = a->pool.stride_slot;
+  g.s_head = a->pool.stride_head;
+  g.block_size = a->pool.block_size;
+  g.num_blocks = a->pool.num_blocks;
+  g.num_kv_heads = a->num_kv_heads;
+  g.head_dim = a->head_dim;
+  g.table = a->block_tables;
+  g.t_sb = a->table_stride_seq;
+  g.table_i64 = a->table_dtype == VA_I64;
+  g.table_width = a->table_width;
+  g.cu_q = a->cu_seqlens_q;
+  g.cu_k = a->cu_seqlens_k;
+  g.all_from_pool = a->k == nullptr;
+  g.width = (int32_t)lay.width;
+  g.k_scale = a->pool.k_scale;
+  g.v_scale = a->pool.v_scale;
+  g.out_table = (int32_t*)ws;
+  g.out_k = ws + lay.table_bytes;
+  g.out_v = ws + lay.table_bytes + lay.block_bytes;
+  const hipStream_t st = (hipStream_t)stream;
+  const dim3 grid((unsigned)lay.width, (unsigned)a->num_seqs);
+  if (a->dtype == VA_BF16)
+    hipLaunchKernelGGL(f8_prefix_gather_kernel<BF16>, grid, dim3(256), 0, st, g);
+  else
+    hipLaunchKernelGGL(f8_prefix_gather_kernel<F16>, grid, dim3(256), 0, st, g);
+  int rc = check_launch("va_varlen_attention (FP8 prefix copy)");
+  if (rc != VA_OK) return rc;
+
+  va_varlen_args b = *a;
+  b.pool.k = g.out_k;
+  b.pool.v = g.out_v;
+  b.pool.stride_block = (int64_t)a->pool.block_size * a->num_kv_heads * a->head_dim;
+  b.pool.stride_slot = (int64_t)a->num_kv_heads * a->head_dim;
+  b.pool.stride_head = a->head_dim;
+  b.pool.num_blocks = (int32_t)((int64_t)a->num_seqs * lay.width);
+  b.pool.kv_format = VA_KV_NATIVE;
+  b.block_tables = g.out_table;
+  b.table_dtype = VA_I32;
+  b.table_stride_seq = lay.width;
+  b.table_width = (int32_t)lay.width;
+  b.slot_mapping = nullptr;
+  b.workspace = nullptr;
+  b.workspace_bytes = 0;
+  VA_CHECK_ARG((int64_t)a->num_seqs * lay.width <= INT32_MAX,
+               "va_varlen_attention: FP8 prefix copy too large");
+  rc = varlen_native(&b, stream);
+  if (rc != VA_OK || a->slot_mapping == nullptr) return rc;
+
+  va_store_args sa{};
+  sa.struct_size = sizeof(va_store_args);
+  sa.dtype = a->dtype;
+  sa.key = a->k;
+  sa.value = a->v;
+  sa.key_stride_tok = a->k_stride_tok;
+  sa.key_stride_head = a->k_stride_head;
+  sa.value_stride_tok = a->v_stride_tok;
+  sa.value_stride_head = a->v_stride_head;
+  sa.pool = a->pool;
+  sa.slot_mapping = a->slot_mapping;
+  sa.slot_dtype = a->slot_dtype;
+  sa.num_tokens = a->total_q;
+  sa.num_kv_heads = a->num_kv_heads;
+  sa.head_dim = a->head_dim;
+  return va_store_kvcache(&sa, stream);
+}
+
+int va::varlen_native(const va_varlen_args* a, void* stream) {
+  using namespace va;
   VA_CHECK_ARG(a->dtype == VA_BF16 || a->dtype == VA_F16,
                "va_varlen_attention: dtype must be VA_BF16 or VA_F16 (MFMA path)");
   VA_CHECK_ARG(a->q && a->out && a->cu_seqlens_q && a->cu_seqlens_k,

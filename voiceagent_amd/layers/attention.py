@@ -36,6 +36,12 @@ Hkv, D]`` as model_runner.py:116-131 allocates it (the default), or
 is a contiguous 4 KiB run; decode reads it ~9% faster.  Every reader and
 writer of the pool is a kernel of this package, so an engine may allocate
 either layout and set ``PagedAttention.kv_layout`` to match.
+
+The pool may also be FP8 (``torch.float8_e4m3fn``, half the bytes of bf16):
+the layer's ``k_scale`` / ``v_scale`` (vLLM's per-tensor convention, 1.0 by
+default) give each code's value, every store quantises and every read
+dequantises.  The engine allocates the cache in that dtype
+(model_runner.py:119) and sets the scales on the layers.
 """
 
 from __future__ import annotations
@@ -72,6 +78,8 @@ def store_kvcache(
 class PagedAttention(nn.Module):
     fuse_store = True
     kv_layout = ops.LAYOUT_NHD
+    k_scale = 1.0  # FP8 pools: value of a key code = code * k_scale
+    v_scale = 1.0
 
     def __init__(self, num_heads: int, head_dim: int, scale: float, num_kv_heads: int):
         super().__init__()
@@ -119,6 +127,8 @@ class PagedAttention(nn.Module):
                 max_seq_len=context.max_seqlen_k,
                 scale=self.scale,
                 layout=self.kv_layout,
+                k_scale=self.k_scale,
+                v_scale=self.v_scale,
             )
         if self.fuse_store:
             return ops.varlen_attention(
@@ -136,6 +146,8 @@ class PagedAttention(nn.Module):
                 block_tables=context.block_tables,
                 slot_mapping=context.slot_mapping,
                 layout=self.kv_layout,
+                k_scale=self.k_scale,
+                v_scale=self.v_scale,
             )
         self._store(k, v, context.slot_mapping)
         return ops.varlen_attention(
@@ -152,6 +164,8 @@ class PagedAttention(nn.Module):
             v_cache=self.v_cache,
             block_tables=context.block_tables,
             layout=self.kv_layout,
+            k_scale=self.k_scale,
+            v_scale=self.v_scale,
         )
 
     def _decode_fused(self, q, k, v, context, prologue: ops.QKPrologue | None) -> torch.Tensor:
@@ -170,16 +184,18 @@ class PagedAttention(nn.Module):
             new_v=v,
             new_slots=context.slot_mapping,
             prologue=prologue,
+            k_scale=self.k_scale,
+            v_scale=self.v_scale,
         )
 
     def _store(self, k: torch.Tensor, v: torch.Tensor, slot_mapping: torch.Tensor) -> None:
         """Unfused store: the reference's store_kvcache (and its stride
         contract) for an NHD pool, the same scatter by layout otherwise."""
-        if self.kv_layout == ops.LAYOUT_NHD:
+        if self.kv_layout == ops.LAYOUT_NHD and self.k_cache.dtype != ops.FP8_KV_DTYPE:
             store_kvcache(k, v, self.k_cache, self.v_cache, slot_mapping)
         else:
             ops.store_kvcache(k, v, self.k_cache, self.v_cache, slot_mapping,
-                              layout=self.kv_layout)
+                              layout=self.kv_layout, k_scale=self.k_scale, v_scale=self.v_scale)
 
 
 class VarlenSelfAttention(nn.Module):

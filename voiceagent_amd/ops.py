@@ -18,6 +18,9 @@ from voiceagent_amd import _native as N
 
 LAYOUT_NHD = "nhd"  # [num_blocks, block_size, Hkv, D]  (engine, model_runner.py:116-131)
 LAYOUT_HND = "hnd"  # [pages, Hkv, page_size, D]        (TTS, qwen_tts_outer_paged_cache.py:116-119)
+# An FP8 KV pool holds OCP e4m3 codes (torch.float8_e4m3fn); an element's
+# value is code * k_scale (keys) or code * v_scale (values).
+FP8_KV_DTYPE = torch.float8_e4m3fn
 
 
 class AttentionArgumentError(ValueError):
@@ -55,8 +58,16 @@ def _rows(t: torch.Tensor, what: str) -> None:
     _require(t.stride(-1) == 1, f"{what}: the last dimension must be contiguous")
 
 
-def kv_pool(k_cache: torch.Tensor, v_cache: torch.Tensor, layout: str = LAYOUT_NHD) -> N.KvPool:
-    """Describe a paged K/V pool pair (4-D, NHD or HND) for the C ABI."""
+def _pool_matches(pool: torch.Tensor, dtype: torch.dtype) -> bool:
+    """A pool of `dtype` itself, or an FP8 pool for 16-bit data."""
+    return pool.dtype == dtype or (pool.dtype == FP8_KV_DTYPE and
+                                   dtype in (torch.bfloat16, torch.float16))
+
+
+def kv_pool(k_cache: torch.Tensor, v_cache: torch.Tensor, layout: str = LAYOUT_NHD,
+            k_scale: float = 1.0, v_scale: float = 1.0) -> N.KvPool:
+    """Describe a paged K/V pool pair (4-D, NHD or HND) for the C ABI; an
+    FP8 (float8_e4m3fn) pool carries its k_scale / v_scale."""
     _require(k_cache.dim() == 4, "KV pool must be 4-D")
     _require(
         v_cache.shape == k_cache.shape and v_cache.stride() == k_cache.stride(),
@@ -85,6 +96,14 @@ def kv_pool(k_cache: torch.Tensor, v_cache: torch.Tensor, layout: str = LAYOUT_N
         raise AttentionArgumentError(f"unknown pool layout {layout!r}")
     pool.block_size = int(bs)
     pool.num_blocks = int(nb)
+    if k_cache.dtype == FP8_KV_DTYPE:
+        _require(k_scale > 0 and v_scale > 0, "FP8 pool scales must be positive")
+        pool.kv_format = N.VA_KV_FP8_E4M3
+        pool.k_scale = float(k_scale)
+        pool.v_scale = float(v_scale)
+    else:
+        pool.kv_format = N.VA_KV_NATIVE
+        pool.k_scale = pool.v_scale = 1.0
     return pool
 
 
@@ -103,15 +122,19 @@ def store_kvcache(
     v_cache: torch.Tensor,
     slot_mapping: torch.Tensor,
     layout: str = LAYOUT_NHD,
+    k_scale: float = 1.0,
+    v_scale: float = 1.0,
 ) -> None:
-    """Write key[i] / value[i] ([N, Hkv, D]) to pool slot slot_mapping[i]; -1 skips."""
+    """Write key[i] / value[i] ([N, Hkv, D]) to pool slot slot_mapping[i]; -1 skips.
+    An FP8 pool receives e4m3 codes of key / k_scale and value / v_scale."""
     device = _check_gpu(key, value, k_cache, v_cache, slot_mapping)
     _require(key.dim() == 3 and value.shape == key.shape, "key/value must be [N, Hkv, D]")
     _rows(key, "key")
     _rows(value, "value")
     hkv, d = pool_heads(k_cache, layout)
     _require(key.shape[1] == hkv and key.shape[2] == d, "key/value heads must match the pool")
-    _require(key.dtype == value.dtype == k_cache.dtype, "key/value/pool dtypes must match")
+    _require(key.dtype == value.dtype and _pool_matches(k_cache, key.dtype),
+             "key/value/pool dtypes must match (or the pool be FP8 for 16-bit rows)")
     _require(slot_mapping.dim() == 1 and slot_mapping.numel() == key.shape[0],
              "slot_mapping must have one entry per token")
     args = N.new_args(N.StoreArgs)
@@ -120,7 +143,7 @@ def store_kvcache(
     args.value = value.data_ptr()
     args.key_stride_tok, args.key_stride_head = key.stride(0), key.stride(1)
     args.value_stride_tok, args.value_stride_head = value.stride(0), value.stride(1)
-    args.pool = kv_pool(k_cache, v_cache, layout)
+    args.pool = kv_pool(k_cache, v_cache, layout, k_scale, v_scale)
     args.slot_mapping = slot_mapping.data_ptr()
     args.slot_dtype = _index_code(slot_mapping, "slot_mapping")
     args.num_tokens = int(key.shape[0])
@@ -246,7 +269,8 @@ def decode_workspace_bound(device: torch.device, num_heads: int, num_kv_heads: i
 
 
 def decode_workspace(device: torch.device, nbytes: int, floor: int = 0,
-                     stream: torch.cuda.Stream | None = None) -> torch.Tensor | None:
+                     stream: torch.cuda.Stream | None = None, kind: str = "decode"
+                     ) -> torch.Tensor | None:
     """Partial-result workspace of the decode launches on `stream` (torch's
     current stream of `device` by default): no initialisation needed.  One
     per stream: launches on one stream are ordered, while decodes on two
@@ -259,6 +283,8 @@ def decode_workspace(device: torch.device, nbytes: int, floor: int = 0,
     if stream is None:
         stream = torch.cuda.current_stream(device)
     key = (_device_index(device), stream.cuda_stream)
+    if kind != "decode":
+        key = key + (kind,)
     ws = _WORKSPACES.get(key)
     if ws is None or ws.numel() < nbytes:
         size = max(nbytes, floor if ws is None else 2 * ws.numel())
@@ -301,6 +327,8 @@ def paged_decode(
     key_limit: int = 0,
     table_read_width: int = 0,
     no_alloc: bool = False,
+    k_scale: float = 1.0,
+    v_scale: float = 1.0,
 ) -> torch.Tensor:
     """One-token paged GQA attention.
 
@@ -316,6 +344,8 @@ def paged_decode(
     len - 1 either way.  ``no_alloc`` launches va_paged_decode_noalloc, which
     keeps the split partials in the library's own scratch buffer instead of a
     workspace; ``out`` must then be given, so that nothing is allocated.
+    An FP8 (float8_e4m3fn) pool is read as code * k_scale / v_scale, and the
+    current row is stored into it quantised.
     """
     device = _check_gpu(q, k_cache, v_cache, block_tables, lens, valid_mask, new_k, new_v,
                         new_slots, out)
@@ -329,7 +359,8 @@ def paged_decode(
     hkv, pd = pool_heads(k_cache, layout)
     _require(pd == d, f"head_dim mismatch: q {d}, pool {pd}")
     _require(hq % hkv == 0, "num_heads must be a multiple of num_kv_heads")
-    _require(q.dtype == k_cache.dtype, "q and the KV pool must share a dtype")
+    _require(_pool_matches(k_cache, q.dtype),
+             "q and the KV pool must share a dtype (or the pool be FP8 for 16-bit q)")
     _require(block_tables.dim() == 2 and block_tables.shape[0] >= B,
              "block_tables must be [num_seqs, width]")
     _require(block_tables.stride(-1) == 1, "block_tables rows must be contiguous")
@@ -346,7 +377,7 @@ def paged_decode(
     args.q_stride_seq, args.q_stride_head = q.stride(0), q.stride(1)
     args.out = out.data_ptr()
     args.out_stride_seq, args.out_stride_head = out.stride(0), out.stride(1)
-    args.pool = kv_pool(k_cache, v_cache, layout)
+    args.pool = kv_pool(k_cache, v_cache, layout, k_scale, v_scale)
     args.block_tables = block_tables.data_ptr()
     args.table_dtype = _index_code(block_tables, "block_tables")
     args.table_stride_seq = block_tables.stride(0)
@@ -423,6 +454,8 @@ def varlen_attention(
     slot_mapping: torch.Tensor | None = None,
     layout: str = LAYOUT_NHD,
     out: torch.Tensor | None = None,
+    k_scale: float = 1.0,
+    v_scale: float = 1.0,
 ) -> torch.Tensor:
     """Packed variable-length attention (flash_attn_varlen_func semantics).
 
@@ -432,7 +465,10 @@ def varlen_attention(
     ``k``/``v`` rows aligned with the queries (all from the pool if ``k`` is
     None).  ``slot_mapping`` fuses store_kvcache of k/v into the same launch.
     ``max_seqlen_q`` must be at least every q_len, as for flash-attn: it sizes
-    the launch, and query rows past it are not computed.
+    the launch, and query rows past it are not computed.  With an FP8 pool
+    (float8_e4m3fn codes, values code * k_scale / v_scale) ``max_seqlen_k``
+    must bound every k_len: the paged prefix is dequantised into a workspace
+    first.
     """
     device = _check_gpu(q, k, v, cu_seqlens_q, cu_seqlens_k, k_cache, v_cache, block_tables,
                         slot_mapping, out)
@@ -452,8 +488,9 @@ def varlen_attention(
                  "a KV pool needs v_cache and block_tables")
         hkv, pd = pool_heads(k_cache, layout)
         _require(pd == d, "pool head_dim must match q")
-        _require(k_cache.dtype == q.dtype, "pool dtype must match q")
-        args.pool = kv_pool(k_cache, v_cache, layout)
+        _require(_pool_matches(k_cache, q.dtype),
+                 "pool dtype must match q (or the pool be FP8 for 16-bit q)")
+        args.pool = kv_pool(k_cache, v_cache, layout, k_scale, v_scale)
         _require(block_tables.dim() == 2 and block_tables.shape[0] >= num_seqs and
                  block_tables.stride(-1) == 1, "block_tables must be [num_seqs, width]")
         args.block_tables = block_tables.data_ptr()
@@ -501,6 +538,11 @@ def varlen_attention(
     args.max_seqlen_k = int(max_seqlen_k)
     args.causal = 1 if causal else 0
     args.scale = float(scale)
+    nbytes = N.lib().va_varlen_workspace_bytes(ctypes.byref(args))
+    ws = decode_workspace(device, nbytes, kind="varlen")
+    if ws is not None:
+        args.workspace = ws.data_ptr()
+        args.workspace_bytes = ws.numel()
     N.call("va_varlen_attention", args, device)
     return out
 
