@@ -62,31 +62,62 @@ def decode_kernel_name() -> str:
     return "paged_decode_mfma_kernel<BF16,128,2,false,false>"
 
 
-def timed_graph(fn, steps: int, warmup: int, stream: torch.cuda.Stream):
-    """Capture fn() in a graph, replay warmup + steps times; return ms per replay.
+TIMINGS: dict[str, dict] = {}  # per timed graph: median / mean / min ms per replay
 
-    The replays and the timing events are issued on the same stream, so the
-    events bracket exactly the replayed kernels.
+
+def timed_graph(fn, steps: int, warmup: int, stream: torch.cuda.Stream, name: str = ""):
+    """Capture fn() in a graph, replay warmup + steps times; return the median
+    ms per replay.
+
+    Every timed replay is bracketed by its own pair of events on the replay
+    stream (so the events bracket exactly the replayed kernels); the median,
+    mean and minimum are kept in TIMINGS[name].
     """
     with torch.cuda.stream(stream):
-        fn()  # eager warm-up: workspace allocation happens outside the capture
+        fn()  # eager warm-up
     torch.cuda.synchronize()
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph, stream=stream):
         fn()
     torch.cuda.synchronize()
-    start = torch.cuda.Event(enable_timing=True)
-    end = torch.cuda.Event(enable_timing=True)
+    events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+              for _ in range(steps)]
     with torch.cuda.stream(stream):
         for _ in range(warmup):
             graph.replay()
         torch.cuda.synchronize()
-        start.record(stream)
-        for _ in range(steps):
+        for start, end in events:
+            start.record(stream)
             graph.replay()
-        end.record(stream)
+            end.record(stream)
     torch.cuda.synchronize()
-    return start.elapsed_time(end) / steps, graph
+    times = sorted(start.elapsed_time(end) for start, end in events)
+    median = times[len(times) // 2] if len(times) % 2 else 0.5 * (
+        times[len(times) // 2 - 1] + times[len(times) // 2])
+    if name:
+        TIMINGS[name] = {"median_ms": round(median, 5), "mean_ms": round(sum(times) / len(times), 5),
+                         "min_ms": round(times[0], 5), "replays": len(times)}
+    return median, graph
+
+
+def gpu_state() -> dict:
+    """Clock, performance-level, power and temperature readings of the GPU
+    from rocm-smi (best effort: empty when the tool is missing or fails)."""
+    import subprocess
+
+    try:
+        r = subprocess.run(["rocm-smi", "--showclocks", "--showperflevel", "--showpower",
+                            "--showtemp", "--json"], capture_output=True, text=True, timeout=20)
+        data = json.loads(r.stdout)
+    except Exception as exc:  # noqa: BLE001 - a diagnostic, never fatal
+        return {"error": str(exc)[:200]}
+    card = next(iter(data.values())) if isinstance(data, dict) and data else {}
+    keep = {}
+    for key, val in card.items():
+        low = key.lower()
+        if any(w in low for w in ("clk", "perf", "power", "temp", "throttl")):
+            keep[key] = val
+    return keep
 
 
 def copy_calibration(dev, nbytes: int = 256 << 20, reps: int = 3) -> None:
@@ -127,7 +158,7 @@ def bench_decode(args, dev, stream):
                              new_v=nvs[i], new_slots=batch.slot_mapping, out=outs[i],
                              split_tokens=args.split)
 
-    ms, _ = timed_graph(step, args.steps, args.warmup, stream)
+    ms, _ = timed_graph(step, args.steps, args.warmup, stream, name="decode_cfg2")
     per_layer_bytes = decode_launch_bytes(lens)
     us_layer = ms * 1000.0 / layers
     gbs = per_layer_bytes / (us_layer * 1e-6) / 1e9
@@ -137,10 +168,96 @@ def bench_decode(args, dev, stream):
                 batch=batch, qs=qs, nks=nks, nvs=nvs)
 
 
-def decode_launch_bytes(lens) -> int:
-    """Algorithmic bytes of one config-2 decode launch (attention + fused store)."""
+def decode_launch_bytes(lens, kv_elem: int = 2) -> int:
+    """Algorithmic bytes of one config-2 decode launch (attention + fused
+    store): K/V rows of every context token (kv_elem bytes per element: 2 for
+    bf16, 1 for FP8 codes), q in and out (bf16), the used block-table entries,
+    the lengths, the stored rows and their slots."""
     B = len(lens)
-    return workloads.decode_bytes(lens) + 2 * B * workloads.HKV * workloads.HEAD_DIM * 2 + 4 * B
+    h, d = workloads.HKV, workloads.HEAD_DIM
+    kv = sum(lens) * h * d * kv_elem * 2
+    qo = 2 * B * workloads.HQ * d * 2
+    tables = sum(math.ceil(n / workloads.BLOCK) for n in lens) * 4
+    return kv + qo + tables + 4 * B + 2 * B * h * d * kv_elem + 4 * B
+
+
+FP8_SCALE = 2.0 ** -4  # k_scale = v_scale of the FP8 rows (a power of two)
+
+
+def fp8_pools(k_pools, v_pools, scale: float = FP8_SCALE):
+    """FP8 (e4m3) copies of 16-bit NHD pools, every slot written by the
+    library's own quantising store."""
+    ks, vs = [], []
+    for kp, vp in zip(k_pools, v_pools):
+        nb, bs, hkv, d = kp.shape
+        kf = torch.empty(kp.shape, dtype=ops.FP8_KV_DTYPE, device=kp.device)
+        vf = torch.empty_like(kf)
+        slots = torch.arange(nb * bs, dtype=torch.int32, device=kp.device)
+        ops.store_kvcache(kp.view(nb * bs, hkv, d), vp.view(nb * bs, hkv, d), kf, vf, slots,
+                          k_scale=scale, v_scale=scale)
+        ks.append(kf)
+        vs.append(vf)
+    torch.cuda.synchronize()
+    return ks, vs
+
+
+def bench_decode_fp8(args, dev, stream, dec):
+    """Config 2's decode step over FP8 copies of the 28 layer pools (half the
+    K/V bytes); the current rows are stored quantised."""
+    batch, layers = dec["batch"], workloads.LAYERS
+    kf, vf = fp8_pools(batch.k_pools, batch.v_pools)
+    outs = torch.empty_like(dec["qs"])
+
+    def step():
+        for i in range(layers):
+            ops.paged_decode(dec["qs"][i], kf[i], vf[i], batch.block_tables, batch.cu_seqlens_k,
+                             lens_cumulative=True, max_seq_len=batch.max_seq_len,
+                             scale=batch.scale, new_k=dec["nks"][i], new_v=dec["nvs"][i],
+                             new_slots=batch.slot_mapping, out=outs[i], k_scale=FP8_SCALE,
+                             v_scale=FP8_SCALE)
+
+    ms, _ = timed_graph(step, args.steps, args.warmup, stream, name="decode_cfg2_fp8")
+    del kf, vf
+    us = ms * 1000.0 / layers
+    nbytes = decode_launch_bytes(dec["lens"], kv_elem=1)
+    gbs = nbytes / (us * 1e-6) / 1e9
+    log(f"[fp8] config 2 over FP8 pools: {us:.2f} us/layer, {gbs:.0f} GB/s of {nbytes / 1e6:.2f} "
+        f"MB (bf16 pools {dec['us_layer']:.2f} us/layer)")
+    return {"us_per_layer": round(us, 2), "gbs": round(gbs, 1),
+            "frac": round(gbs / HBM_PEAK_GBS, 4), "bytes_per_layer": nbytes,
+            "kv_format": "OCP e4m3 codes, k_scale = v_scale = 2^-4",
+            "speedup_vs_bf16_pool": round(dec["us_layer"] / us, 3)}
+
+
+def bench_host_overhead(dev, dec, pre):
+    """Host microseconds per ops.paged_decode and ops.varlen_attention call
+    (argument checks, the struct, the C call and the launch), from 300 eager
+    calls of config 2's layer 0 and config 3's layer 0 without waiting for the
+    GPU."""
+    batch = dec["batch"]
+    out = torch.empty_like(dec["qs"][0])
+
+    def decode_call():
+        ops.paged_decode(dec["qs"][0], batch.k_pools[0], batch.v_pools[0], batch.block_tables,
+                         batch.cu_seqlens_k, lens_cumulative=True, max_seq_len=batch.max_seq_len,
+                         scale=batch.scale, new_k=dec["nks"][0], new_v=dec["nvs"][0],
+                         new_slots=batch.slot_mapping, out=out)
+
+    res = {}
+    for name, call in (("paged_decode", decode_call), ("varlen_attention", pre["call0"])):
+        for _ in range(20):
+            call()
+        torch.cuda.synchronize()
+        n = 300
+        t0 = time.perf_counter()
+        for _ in range(n):
+            call()
+        t1 = time.perf_counter()
+        torch.cuda.synchronize()
+        res[name] = round((t1 - t0) / n * 1e6, 2)
+    log(f"[host] us per call: paged_decode {res['paged_decode']}, varlen_attention "
+        f"{res['varlen_attention']}")
+    return res
 
 
 PROBE_MODES = {"plain": 0, "nt": 1, "lds_dma": 2}  # include/voiceagent_bench.h
@@ -374,32 +491,48 @@ def bench_longform(args, dev, stream):
                            device=dev) * 0.5).to(torch.bfloat16)
         outs = torch.empty_like(qs)
 
-        def make_step(max_seq_len):
+        def make_step(max_seq_len, kps, vps, kv_scale=1.0):
             def step():
                 for i in range(layers):
-                    ops.paged_decode(qs[i], batch.k_pools[i], batch.v_pools[i],
+                    ops.paged_decode(qs[i], kps[i], vps[i],
                                      batch.block_tables, batch.cu_seqlens_k,
                                      lens_cumulative=True, max_seq_len=max_seq_len,
                                      scale=batch.scale, new_k=nks[i], new_v=nvs[i],
                                      new_slots=batch.slot_mapping, out=outs[i],
-                                     split_tokens=args.split)
+                                     split_tokens=args.split, k_scale=kv_scale,
+                                     v_scale=kv_scale)
             return step
 
-        nbytes = workloads.decode_bytes(lens) + 2 * B * workloads.HKV * workloads.HEAD_DIM * 2 \
-            + 4 * B
-        ms, _ = timed_graph(make_step(batch.max_seq_len), args.steps, args.warmup, stream)
+        nbytes = decode_launch_bytes(lens)
+        ms, _ = timed_graph(make_step(batch.max_seq_len, batch.k_pools, batch.v_pools),
+                            args.steps, args.warmup, stream, name=f"longform_{variant}")
         us = ms * 1000.0 / layers
         gbs = nbytes / (us * 1e-6) / 1e9
-        ms_g, _ = timed_graph(make_step(MAX_MODEL_LEN), args.steps, args.warmup, stream)
+        ms_g, _ = timed_graph(make_step(MAX_MODEL_LEN, batch.k_pools, batch.v_pools),
+                              args.steps, args.warmup, stream)
         us_g = ms_g * 1000.0 / layers
         log(f"[longform {variant}] B={B} ctx sum {sum(lens)}: {us:.2f} us/layer, {gbs:.0f} GB/s "
             f"({nbytes / 1e6:.1f} MB/layer, {gbs / HBM_PEAK_GBS:.3f} of HBM peak); "
             f"max_seq_len={MAX_MODEL_LEN}: {us_g:.2f} us/layer")
+        # The same step over FP8 copies of the pools.
+        kf, vf = fp8_pools(batch.k_pools, batch.v_pools)
+        del batch.k_pools[:], batch.v_pools[:]
+        torch.cuda.empty_cache()
+        ms8, _ = timed_graph(make_step(batch.max_seq_len, kf, vf, FP8_SCALE), args.steps,
+                             args.warmup, stream, name=f"longform_{variant}_fp8")
+        us8 = ms8 * 1000.0 / layers
+        nbytes8 = decode_launch_bytes(lens, kv_elem=1)
+        gbs8 = nbytes8 / (us8 * 1e-6) / 1e9
+        log(f"[longform {variant} fp8] {us8:.2f} us/layer, {gbs8:.0f} GB/s of "
+            f"{nbytes8 / 1e6:.1f} MB/layer ({gbs8 / HBM_PEAK_GBS:.3f} of HBM peak)")
         res[variant] = {"us_per_layer": round(us, 2), "gbs": round(gbs, 1),
                         "frac": round(gbs / HBM_PEAK_GBS, 4), "bytes_per_layer": nbytes,
                         "batch": B, "context_tokens": sum(lens),
-                        "us_per_layer_max_model_len": round(us_g, 2)}
-        del batch, qs, nks, nvs, outs
+                        "us_per_layer_max_model_len": round(us_g, 2),
+                        "fp8": {"us_per_layer": round(us8, 2), "gbs": round(gbs8, 1),
+                                "frac": round(gbs8 / HBM_PEAK_GBS, 4),
+                                "bytes_per_layer": nbytes8}}
+        del batch, qs, nks, nvs, outs, kf, vf
         torch.cuda.empty_cache()
     return res
 
@@ -456,15 +589,20 @@ def bench_prefill(args, dev, stream):
                                  causal=True, k_cache=kp[i], v_cache=vp[i], block_tables=table,
                                  slot_mapping=slots, out=out[i])
 
-    ms, _ = timed_graph(step, args.steps, args.warmup, stream)
+    ms, _ = timed_graph(step, args.steps, args.warmup, stream, name="prefill_cfg3")
     us = ms * 1000.0 / layers
     flops = workloads.causal_flops(lens)
     tflops = flops / (us * 1e-6) / 1e12
     nbytes = workloads.varlen_bytes(lens, 16, 8, 128) + total * 2 * 8 * 128 * 2
     log(f"[prefill] {us:.2f} us/layer, {tflops:.1f} TFLOP/s ({flops / 1e9:.2f} GFLOP), "
         f"{nbytes / (us * 1e-6) / 1e9:.0f} GB/s")
+    def call0():
+        ops.varlen_attention(q[0], k[0], v[0], cu, cu, max(lens), max(lens), scale=scale,
+                             causal=True, k_cache=kp[0], v_cache=vp[0], block_tables=table,
+                             slot_mapping=slots, out=out[0])
+
     return dict(us_layer=us, tflops=tflops, flops=flops, bytes=nbytes,
-                inputs=(q[0], k[0], v[0], cu, scale, True))
+                inputs=(q[0], k[0], v[0], cu, scale, True), call0=call0)
 
 
 def bench_encoder(args, dev, stream):
@@ -485,7 +623,7 @@ def bench_encoder(args, dev, stream):
             ops.varlen_attention(q[i], k[i], v[i], cu, cu, max(wins), max(wins), scale=0.125,
                                  causal=False, out=out[i])
 
-    ms, _ = timed_graph(step, args.steps, args.warmup, stream)
+    ms, _ = timed_graph(step, args.steps, args.warmup, stream, name="encoder_cfg4")
     us = ms * 1000.0 / layers
     flops = workloads.bidir_flops(wins)
     nbytes = workloads.varlen_bytes(wins, 14, 14, 64)
@@ -566,7 +704,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--split", type=int, default=0, help="decode split_tokens (0 = auto)")
     ap.add_argument("--only", choices=["decode", "prefill", "encoder", "store", "longform",
-                                       "prologue", "kvformat", "floor", "tts", "all"],
+                                       "prologue", "kvformat", "floor", "tts", "fp8", "all"],
                     default="all")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
@@ -606,7 +744,12 @@ def main():
     if args.only == "tts":
         print(json.dumps({"tts_decode": bench_tts(args, dev, stream)}))
         return
+    state_before = gpu_state()
     dec = bench_decode(args, dev, stream)
+    state_after = gpu_state()
+    if args.only == "fp8":
+        print(json.dumps({"fp8_decode": bench_decode_fp8(args, dev, stream, dec)}))
+        return
     if args.only == "store":
         print(json.dumps({"store": bench_store(args, dev, stream, dec)}))
         return
@@ -618,6 +761,7 @@ def main():
         return
     extra = {}
     if args.only == "all":
+        extra["fp8_decode"] = bench_decode_fp8(args, dev, stream, dec)
         extra["store"] = bench_store(args, dev, stream, dec)
         extra["qwen3_prologue"] = bench_prologue(args, dev, stream, dec)
         extra["kv_format_hnd"] = bench_kv_format(args, dev, stream, dec)
@@ -631,6 +775,7 @@ def main():
                             "hbm_gbs": round(pre["bytes"] / (pre["us_layer"] * 1e-6) / 1e9, 1),
                             "config": "cfg3: 32 prompts U[50,450], GQA 16/8, D128, fused store, "
                                       "28 rotating input sets (cold)"}
+        extra["host_us_per_call"] = bench_host_overhead(dev, dec, pre)
         extra["longform"] = bench_longform(args, dev, stream)
         extra["encoder"] = {"us_per_layer": round(enc["us_layer"], 2),
                             "tflops": round(enc["tflops"], 2),
@@ -656,6 +801,8 @@ def main():
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(dec["ms"], 4),
+        "timing": "median of the per-replay HIP-event times of the timed replays "
+                  "(TIMINGS below holds mean and minimum too)",
         "us_per_layer": round(dec["us_layer"], 3),
         "higher_is_better": True,
         "scaling": "weak",
@@ -675,6 +822,8 @@ def main():
         "cpu_baseline": cpu,
     }
     line.update(extra)
+    line["timings"] = TIMINGS
+    line["gpu_state"] = {"before": state_before, "after": state_after}
     if line["roofline"]["frac"] > 1.0:
         log("[bench] WARNING: achieved bandwidth above the HBM peak: measurement error")
     print(json.dumps(line))

@@ -253,6 +253,54 @@ def _device_index(device: torch.device) -> int:
     return device.index if device.index is not None else torch.cuda.current_device()
 
 
+def _raw_stream(index: int) -> int:
+    """Handle of torch's current stream on device `index`."""
+    return torch._C._cuda_getCurrentRawStream(index)
+
+
+class _current:
+    """Make device `index` current for the block (the library plans launches
+    for, and launches on, the current device); a no-op when it already is."""
+
+    __slots__ = ("index", "prev")
+
+    def __init__(self, index: int):
+        self.index = index
+        self.prev = -1
+
+    def __enter__(self):
+        cur = torch._C._cuda_getDevice()
+        if cur != self.index:
+            self.prev = cur
+            torch._C._cuda_setDevice(self.index)
+        return self
+
+    def __exit__(self, *exc):
+        if self.prev >= 0:
+            torch._C._cuda_setDevice(self.prev)
+        return False
+
+
+_DECODE_ARGS_SIZE = ctypes.sizeof(N.DecodeArgs)
+_VARLEN_ARGS_SIZE = ctypes.sizeof(N.VarlenArgs)
+_POOLS: dict[tuple, N.KvPool] = {}  # pool descriptions by tensor identity and geometry
+
+
+def _pool_struct(k_cache, v_cache, layout, k_scale, v_scale) -> N.KvPool:
+    """kv_pool(...), cached: engine pools live for the whole run, and the
+    description depends only on the key's fields."""
+    key = (k_cache.data_ptr(), v_cache.data_ptr(), k_cache.shape, k_cache.stride(),
+           v_cache.shape, v_cache.stride(), k_cache.dtype, v_cache.dtype, layout,
+           float(k_scale), float(v_scale))
+    pool = _POOLS.get(key)
+    if pool is None:
+        pool = kv_pool(k_cache, v_cache, layout, k_scale, v_scale)
+        if len(_POOLS) >= 1024:
+            _POOLS.clear()
+        _POOLS[key] = pool
+    return pool
+
+
 def decode_workspace_bound(device: torch.device, num_heads: int, num_kv_heads: int,
                            head_dim: int) -> int:
     """Bytes that covers every automatic split (split_tokens = 0) of a decode
@@ -349,90 +397,84 @@ def paged_decode(
     """
     device = _check_gpu(q, k_cache, v_cache, block_tables, lens, valid_mask, new_k, new_v,
                         new_slots, out)
-    _require(not no_alloc or out is not None, "no_alloc needs the output tensor (out=...)")
     if prologue is not None:
         _check_gpu(q, prologue.q_norm_weight, prologue.k_norm_weight, prologue.cos_sin_cache,
                    prologue.positions)
+    _require(not no_alloc or out is not None, "no_alloc needs the output tensor (out=...)")
     _require(q.dim() == 3, "q must be [num_seqs, num_heads, head_dim]")
-    _rows(q, "q")
-    B, hq, d = (int(x) for x in q.shape)
+    qs = q.stride()
+    _require(qs[2] == 1, "q: the last dimension must be contiguous")
+    B, hq, d = q.shape
     hkv, pd = pool_heads(k_cache, layout)
     _require(pd == d, f"head_dim mismatch: q {d}, pool {pd}")
     _require(hq % hkv == 0, "num_heads must be a multiple of num_kv_heads")
     _require(_pool_matches(k_cache, q.dtype),
              "q and the KV pool must share a dtype (or the pool be FP8 for 16-bit q)")
+    bts = block_tables.stride()
     _require(block_tables.dim() == 2 and block_tables.shape[0] >= B,
              "block_tables must be [num_seqs, width]")
-    _require(block_tables.stride(-1) == 1, "block_tables rows must be contiguous")
+    _require(bts[1] == 1, "block_tables rows must be contiguous")
     expect = B + 1 if lens_cumulative else B
     _require(lens.dim() == 1 and lens.numel() >= expect and lens.is_contiguous(),
              f"lens must be a contiguous vector of at least {expect} entries")
     if out is None:
         out = torch.empty_like(q)
+    os_ = out.stride()
     _require(out.shape == q.shape and out.dtype == q.dtype, "out must match q")
-    _rows(out, "out")
-    args = N.new_args(N.DecodeArgs)
-    args.dtype = _dtype_code(q)
-    args.q = q.data_ptr()
-    args.q_stride_seq, args.q_stride_head = q.stride(0), q.stride(1)
-    args.out = out.data_ptr()
-    args.out_stride_seq, args.out_stride_head = out.stride(0), out.stride(1)
-    args.pool = kv_pool(k_cache, v_cache, layout, k_scale, v_scale)
-    args.block_tables = block_tables.data_ptr()
-    args.table_dtype = _index_code(block_tables, "block_tables")
-    args.table_stride_seq = block_tables.stride(0)
-    args.table_width = int(block_tables.shape[1])
-    args.lens = lens.data_ptr()
-    args.lens_dtype = _index_code(lens, "lens")
-    args.lens_kind = N.VA_LENS_CUMULATIVE if lens_cumulative else N.VA_LENS_PER_SEQ
+    _require(os_[2] == 1, "out: the last dimension must be contiguous")
+    _require(key_limit >= 0 and table_read_width >= 0,
+             "key_limit and table_read_width must be non-negative")
+    fields = dict(
+        struct_size=_DECODE_ARGS_SIZE, dtype=_dtype_code(q), q=q.data_ptr(),
+        q_stride_seq=qs[0], q_stride_head=qs[1], out=out.data_ptr(), out_stride_seq=os_[0],
+        out_stride_head=os_[1], pool=_pool_struct(k_cache, v_cache, layout, k_scale, v_scale),
+        block_tables=block_tables.data_ptr(),
+        table_dtype=_index_code(block_tables, "block_tables"), table_stride_seq=bts[0],
+        table_width=block_tables.shape[1], lens=lens.data_ptr(),
+        lens_dtype=_index_code(lens, "lens"),
+        lens_kind=N.VA_LENS_CUMULATIVE if lens_cumulative else N.VA_LENS_PER_SEQ,
+        num_seqs=B, num_heads=hq, num_kv_heads=hkv, head_dim=d, max_seq_len=int(max_seq_len),
+        split_tokens=int(split_tokens), scale=float(scale), key_limit=int(key_limit),
+        table_read_width=int(table_read_width))
     if valid_mask is not None:
         _require(valid_mask.dim() == 2 and valid_mask.shape[0] >= B and
                  valid_mask.dtype == torch.bool and valid_mask.stride(-1) == 1,
                  "key_valid_mask must be a [num_seqs, max_seq] bool tensor")
-        args.valid_mask = valid_mask.data_ptr()
-        args.valid_stride_seq = valid_mask.stride(0)
-        args.valid_len = int(valid_mask.shape[1])
+        fields.update(valid_mask=valid_mask.data_ptr(), valid_stride_seq=valid_mask.stride(0),
+                      valid_len=valid_mask.shape[1])
     _require((new_k is None) == (new_v is None), "new_k and new_v must be given together")
     if new_k is not None:
+        nks, nvs = new_k.stride(), new_v.stride()
         _require(new_k.shape == (B, hkv, d) and new_v.shape == new_k.shape,
                  "new_k/new_v must be [num_seqs, num_kv_heads, head_dim]")
         _require(new_k.dtype == new_v.dtype == q.dtype, "new_k/new_v must match q's dtype")
-        _rows(new_k, "new_k")
-        _rows(new_v, "new_v")
-        args.new_k = new_k.data_ptr()
-        args.new_k_stride_seq, args.new_k_stride_head = new_k.stride(0), new_k.stride(1)
-        args.new_v = new_v.data_ptr()
-        args.new_v_stride_seq, args.new_v_stride_head = new_v.stride(0), new_v.stride(1)
+        _require(nks[2] == 1 and nvs[2] == 1, "new_k/new_v: the last dimension must be contiguous")
+        fields.update(new_k=new_k.data_ptr(), new_k_stride_seq=nks[0], new_k_stride_head=nks[1],
+                      new_v=new_v.data_ptr(), new_v_stride_seq=nvs[0], new_v_stride_head=nvs[1])
     if new_slots is not None:
         _require(new_k is not None, "new_slots requires new_k/new_v")
         _require(new_slots.dim() == 1 and new_slots.numel() >= B and new_slots.is_contiguous(),
                  "new_slots must be a contiguous [num_seqs] vector")
-        args.new_slots = new_slots.data_ptr()
-        args.new_slots_dtype = _index_code(new_slots, "new_slots")
-    args.num_seqs = B
-    args.num_heads = hq
-    args.num_kv_heads = hkv
-    args.head_dim = d
-    args.max_seq_len = int(max_seq_len)
-    args.split_tokens = int(split_tokens)
-    args.scale = float(scale)
-    _require(key_limit >= 0 and table_read_width >= 0,
-             "key_limit and table_read_width must be non-negative")
-    args.key_limit = int(key_limit)
-    args.table_read_width = int(table_read_width)
+        fields.update(new_slots=new_slots.data_ptr(),
+                      new_slots_dtype=_index_code(new_slots, "new_slots"))
+    pro_struct = None
     if prologue is not None:
         pro_struct = _prologue_struct(prologue, d, B)  # kept alive through the call
-        args.prologue = ctypes.pointer(pro_struct)
-    if no_alloc:
-        N.call("va_paged_decode_noalloc", args, device)
-        return out
-    with torch.cuda.device(device):  # the split plan depends on the device's CU count
-        nbytes = N.lib().va_paged_decode_workspace_bytes(ctypes.byref(args))
-    ws = decode_workspace(device, nbytes, floor=decode_workspace_bound(device, hq, hkv, d))
-    if ws is not None:
-        args.workspace = ws.data_ptr()
-        args.workspace_bytes = ws.numel()
-    N.call("va_paged_decode", args, device)
+        fields["prologue"] = ctypes.pointer(pro_struct)
+    args = N.DecodeArgs(**fields)
+    lib = N.lib()
+    index = _device_index(device)
+    with _current(index):  # the split plan depends on the device's CU count
+        if no_alloc:
+            N.check("va_paged_decode_noalloc",
+                    lib.va_paged_decode_noalloc(ctypes.byref(args), _raw_stream(index)))
+            return out
+        nbytes = lib.va_paged_decode_workspace_bytes(ctypes.byref(args))
+        if nbytes:
+            ws = decode_workspace(device, nbytes, floor=decode_workspace_bound(device, hq, hkv, d))
+            args.workspace = ws.data_ptr()
+            args.workspace_bytes = ws.numel()
+        N.check("va_paged_decode", lib.va_paged_decode(ctypes.byref(args), _raw_stream(index)))
     return out
 
 
@@ -473,16 +515,17 @@ def varlen_attention(
     device = _check_gpu(q, k, v, cu_seqlens_q, cu_seqlens_k, k_cache, v_cache, block_tables,
                         slot_mapping, out)
     _require(q.dim() == 3, "q must be [total_q, num_heads, head_dim]")
-    _rows(q, "q")
-    total_q, hq, d = (int(x) for x in q.shape)
+    qs = q.stride()
+    _require(qs[2] == 1, "q: the last dimension must be contiguous")
+    total_q, hq, d = q.shape
     _require(cu_seqlens_q.dtype == torch.int32 and cu_seqlens_k.dtype == torch.int32,
              "cu_seqlens must be int32")
     _require(cu_seqlens_q.dim() == 1 and cu_seqlens_q.numel() >= 2 and
              cu_seqlens_k.numel() == cu_seqlens_q.numel(), "cu_seqlens must be [num_seqs + 1]")
     _require(cu_seqlens_q.is_contiguous() and cu_seqlens_k.is_contiguous(),
              "cu_seqlens must be contiguous")
-    num_seqs = int(cu_seqlens_q.numel()) - 1
-    args = N.new_args(N.VarlenArgs)
+    num_seqs = cu_seqlens_q.numel() - 1
+    fields = {}
     if k_cache is not None:
         _require(v_cache is not None and block_tables is not None,
                  "a KV pool needs v_cache and block_tables")
@@ -490,60 +533,55 @@ def varlen_attention(
         _require(pd == d, "pool head_dim must match q")
         _require(_pool_matches(k_cache, q.dtype),
                  "pool dtype must match q (or the pool be FP8 for 16-bit q)")
-        args.pool = kv_pool(k_cache, v_cache, layout, k_scale, v_scale)
-        _require(block_tables.dim() == 2 and block_tables.shape[0] >= num_seqs and
-                 block_tables.stride(-1) == 1, "block_tables must be [num_seqs, width]")
-        args.block_tables = block_tables.data_ptr()
-        args.table_dtype = _index_code(block_tables, "block_tables")
-        args.table_stride_seq = block_tables.stride(0)
-        args.table_width = int(block_tables.shape[1])
+        bts = block_tables.stride()
+        _require(block_tables.dim() == 2 and block_tables.shape[0] >= num_seqs and bts[1] == 1,
+                 "block_tables must be [num_seqs, width]")
+        fields.update(pool=_pool_struct(k_cache, v_cache, layout, k_scale, v_scale),
+                      block_tables=block_tables.data_ptr(),
+                      table_dtype=_index_code(block_tables, "block_tables"),
+                      table_stride_seq=bts[0], table_width=block_tables.shape[1])
     else:
         _require(k is not None and v is not None, "k and v are required without a KV pool")
-        hkv = int(k.shape[1])
+        hkv = k.shape[1]
     if k is not None:
         _require(v is not None and k.dim() == 3 and v.shape == k.shape,
                  "k/v must be [tokens, num_kv_heads, head_dim]")
         _require(k.shape[1] == hkv and k.shape[2] == d, "k/v heads must match")
         _require(k.dtype == v.dtype == q.dtype, "q/k/v dtypes must match")
-        _rows(k, "k")
-        _rows(v, "v")
-        args.k = k.data_ptr()
-        args.k_stride_tok, args.k_stride_head = k.stride(0), k.stride(1)
-        args.v = v.data_ptr()
-        args.v_stride_tok, args.v_stride_head = v.stride(0), v.stride(1)
+        ks, vs = k.stride(), v.stride()
+        _require(ks[2] == 1 and vs[2] == 1, "k/v: the last dimension must be contiguous")
+        fields.update(k=k.data_ptr(), k_stride_tok=ks[0], k_stride_head=ks[1], v=v.data_ptr(),
+                      v_stride_tok=vs[0], v_stride_head=vs[1])
     _require(hq % hkv == 0, "num_heads must be a multiple of num_kv_heads")
     if slot_mapping is not None:
         _require(k_cache is not None and k is not None, "slot_mapping needs a pool and k/v")
         _require(slot_mapping.dim() == 1 and slot_mapping.numel() == total_q and
                  slot_mapping.is_contiguous(), "slot_mapping must have one entry per query")
-        args.slot_mapping = slot_mapping.data_ptr()
-        args.slot_dtype = _index_code(slot_mapping, "slot_mapping")
+        fields.update(slot_mapping=slot_mapping.data_ptr(),
+                      slot_dtype=_index_code(slot_mapping, "slot_mapping"))
     if out is None:
         out = torch.empty_like(q)
+    os_ = out.stride()
     _require(out.shape == q.shape and out.dtype == q.dtype, "out must match q")
-    _rows(out, "out")
-    args.dtype = _dtype_code(q)
-    args.q = q.data_ptr()
-    args.q_stride_tok, args.q_stride_head = q.stride(0), q.stride(1)
-    args.out = out.data_ptr()
-    args.out_stride_tok, args.out_stride_head = out.stride(0), out.stride(1)
-    args.cu_seqlens_q = cu_seqlens_q.data_ptr()
-    args.cu_seqlens_k = cu_seqlens_k.data_ptr()
-    args.num_seqs = num_seqs
-    args.total_q = total_q
-    args.num_heads = hq
-    args.num_kv_heads = hkv
-    args.head_dim = d
-    args.max_seqlen_q = int(max_seqlen_q)
-    args.max_seqlen_k = int(max_seqlen_k)
-    args.causal = 1 if causal else 0
-    args.scale = float(scale)
-    nbytes = N.lib().va_varlen_workspace_bytes(ctypes.byref(args))
-    ws = decode_workspace(device, nbytes, kind="varlen")
-    if ws is not None:
-        args.workspace = ws.data_ptr()
-        args.workspace_bytes = ws.numel()
-    N.call("va_varlen_attention", args, device)
+    _require(os_[2] == 1, "out: the last dimension must be contiguous")
+    args = N.VarlenArgs(
+        struct_size=_VARLEN_ARGS_SIZE, dtype=_dtype_code(q), q=q.data_ptr(), q_stride_tok=qs[0],
+        q_stride_head=qs[1], out=out.data_ptr(), out_stride_tok=os_[0], out_stride_head=os_[1],
+        cu_seqlens_q=cu_seqlens_q.data_ptr(), cu_seqlens_k=cu_seqlens_k.data_ptr(),
+        num_seqs=num_seqs, total_q=total_q, num_heads=hq, num_kv_heads=hkv, head_dim=d,
+        max_seqlen_q=int(max_seqlen_q), max_seqlen_k=int(max_seqlen_k),
+        causal=1 if causal else 0, scale=float(scale), **fields)
+    lib = N.lib()
+    index = _device_index(device)
+    with _current(index):
+        if k_cache is not None and k_cache.dtype == FP8_KV_DTYPE:
+            nbytes = lib.va_varlen_workspace_bytes(ctypes.byref(args))
+            ws = decode_workspace(device, nbytes, kind="varlen")
+            if ws is not None:
+                args.workspace = ws.data_ptr()
+                args.workspace_bytes = ws.numel()
+        N.check("va_varlen_attention",
+                lib.va_varlen_attention(ctypes.byref(args), _raw_stream(index)))
     return out
 
 
