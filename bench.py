@@ -729,7 +729,7 @@ def main():
     if args.only in ("prefill",):
         result["prefill"] = bench_prefill(args, dev, stream)
         print(json.dumps({"prefill": {k: v for k, v in result["prefill"].items()
-                                      if k != "inputs"}}))
+                                      if k not in ("inputs", "call0")}}))
         return
     if args.only in ("encoder",):
         enc = bench_encoder(args, dev, stream)

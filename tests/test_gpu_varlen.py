@@ -35,6 +35,44 @@ def test_cfg3_causal_packed(dev):
     assert _err(out, ref) <= TOL
 
 
+def test_cfg3_full_size_paged_with_fused_store(dev):
+    # The launch bench.py times for config 3: 32 prompts U[50, 450], GQA 16/8,
+    # head_dim 128, keys from k/v with the store fused into a block-16 pool
+    # (varlen_attention_kernel<bf16, 128, 2, causal, paged>), over shuffled
+    # block tables padded with -1.
+    lens = workloads.cfg3_lens(0)
+    b = workloads.make_varlen_batch(lens, 16, 8, 128, causal=True, seed=31)
+    bs = 16
+    need = [math.ceil(n / bs) for n in lens]
+    nb = sum(need) + 8
+    perm = torch.randperm(nb, generator=torch.Generator().manual_seed(32)).tolist()
+    rows, cur, slots = [], 0, []
+    for n, m in zip(lens, need):
+        rows.append(perm[cur:cur + m] + [-1] * (max(need) - m))
+        slots += [perm[cur + p // bs] * bs + p % bs for p in range(n)]
+        cur += m
+    table = torch.tensor(rows, dtype=torch.int32)
+    slots = torch.tensor(slots, dtype=torch.int32)
+    gen = torch.Generator().manual_seed(33)
+    kp = torch.randn(nb, bs, 8, 128, generator=gen).to(torch.bfloat16)
+    vp = torch.randn(nb, bs, 8, 128, generator=gen).to(torch.bfloat16)
+    kd, vd = kp.to(dev), vp.to(dev)
+    out = ops.varlen_attention(b.q.to(dev), b.k.to(dev), b.v.to(dev), b.cu_seqlens.to(dev),
+                               b.cu_seqlens.to(dev), b.max_seqlen, b.max_seqlen, scale=b.scale,
+                               causal=True, k_cache=kd, v_cache=vd, block_tables=table.to(dev),
+                               slot_mapping=slots.to(dev))
+    torch.cuda.synchronize()
+    ek, ev = oracle.store_kvcache(b.k, b.v, kp, vp, slots)
+    assert torch.equal(kd.cpu(), ek) and torch.equal(vd.cpu(), ev)
+    ref = oracle.varlen_attention(b.q, b.k, b.v, b.cu_seqlens, b.cu_seqlens, b.scale, True)
+    assert _err(out, ref) <= TOL
+    # With the keys read back from the pool (k = None) the result is the same.
+    out2 = ops.varlen_attention(b.q.to(dev), None, None, b.cu_seqlens.to(dev),
+                                b.cu_seqlens.to(dev), b.max_seqlen, b.max_seqlen, scale=b.scale,
+                                causal=True, k_cache=kd, v_cache=vd, block_tables=table.to(dev))
+    assert torch.equal(out2, out)
+
+
 def test_cfg4_encoder_block_diagonal(dev):
     wins = workloads.cfg4_windows(0)
     b = workloads.make_varlen_batch(wins, 14, 14, 64, causal=False, seed=1)

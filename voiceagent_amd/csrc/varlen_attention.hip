@@ -435,7 +435,7 @@ __global__ __launch_bounds__(kVarlenThreads, 2) void varlen_attention_kernel(Var
   if (cur.ntiles > 0)
     issue_tile(cur.h, cur.pool_prefix, cur.kend, cur.new_base, cur.table_row, 0, 0);
   load_q(cur);
-  uint2 st_slot = load_slot(cur), nxt_slot = make_uint2(~0u, ~0u);
+  uint2 st_slot = load_slot(cur);
   int stage = 0;  // stage holding the current item's next tile to reduce
 
   for (;;) {
@@ -483,14 +483,29 @@ __global__ __launch_bounds__(kVarlenThreads, 2) void varlen_attention_kernel(Var
           asm volatile("" ::"v"(qreg[tt][ds].x), "v"(qreg[tt][ds].y), "v"(qreg[tt][ds].z),
                        "v"(qreg[tt][ds].w));
       asm volatile("" ::"v"(st_slot.x), "v"(st_slot.y));
-      {
-        // One call site, fields picked one by one (uniform selects).
-        const bool same = t + 1 < cur.ntiles;
-        if (same || (has_next && nxt.ntiles > 0))
-          issue_tile(same ? cur.h : nxt.h, same ? cur.pool_prefix : nxt.pool_prefix,
-                     same ? cur.kend : nxt.kend, same ? cur.new_base : nxt.new_base,
-                     same ? cur.table_row : nxt.table_row, same ? kb + kKeyTile : 0, stage ^ 1);
+      // The next tile (this item's tile t + 1, or the next item's first)
+      // goes to the other stage.  A whole tile from k/v is issued in NI
+      // pairs spread over the S^T loop below: issued back to back, its DMAs
+      // stall the wave on the vector memory queue for as long as the
+      // MFMAs of half a tile take.  Other tiles are issued here.
+      const bool same = t + 1 < cur.ntiles;
+      const bool next_tile = same || (has_next && nxt.ntiles > 0);
+      const int n_h = same ? cur.h : nxt.h;
+      const int n_prefix = same ? cur.pool_prefix : nxt.pool_prefix;
+      const int n_kend = same ? cur.kend : nxt.kend;
+      const int64_t n_base = same ? cur.new_base : nxt.new_base;
+      const int n_kb = same ? kb + kKeyTile : 0;
+      const bool spread = next_tile && n_kb >= n_prefix && n_kb + kKeyTile <= n_kend;
+      const char* n_kbase = nullptr;
+      const char* n_vbase = nullptr;
+      if (spread) {
+        n_kbase = uniform_ptr(p.k + (n_base + n_kb) * p.k_st + n_h * p.k_sh);
+        n_vbase = uniform_ptr(p.v + (n_base + n_kb) * p.v_st + n_h * p.v_sh);
+      } else if (next_tile) {
+        issue_tile(n_h, n_prefix, n_kend, n_base, same ? cur.table_row : nxt.table_row, n_kb,
+                   stage ^ 1);
       }
+      const uint32_t n_dst = lds_base + (uint32_t)((stage ^ 1) * 2 * TILE_B + wave * NI * 1024);
       const char* s_k = s_kv + stage * 2 * TILE_B;
       const char* s_v = s_k + TILE_B;
 
@@ -522,23 +537,48 @@ __global__ __launch_bounds__(kVarlenThreads, 2) void varlen_attention_kernel(Var
       }
 
       // ---- S^T = K Q^T for both row tiles ----
+      // K rows of 16-key group kt + 1 are read before group kt's DMA pair:
+      // no LDS read moves across a DMA.
+      static_assert(KT % NI == 0 || NI % KT == 0, "DMA pairs spread evenly over the key groups");
+      constexpr int PAIRS = NI >= KT ? NI / KT : 1;  // DMA pairs after each chosen group
+      constexpr int EVERY = NI >= KT ? 1 : KT / NI;  // every EVERY-th group gets them
       f32x4_t sacc[2][KT];
+      uint4 ka[2][DS];
+#pragma unroll
+      for (int ds = 0; ds < DS; ++ds)
+        ka[0][ds] = lds_read16(s_k, r16 * ROWB + (((4 * ds + g4) ^ kswz) << 4));
 #pragma unroll
       for (int kt = 0; kt < KT; ++kt) {
+        if (kt + 1 < KT) {
+#pragma unroll
+          for (int ds = 0; ds < DS; ++ds)
+            ka[(kt + 1) & 1][ds] =
+                lds_read16(s_k, (16 * (kt + 1) + r16) * ROWB + (((4 * ds + g4) ^ kswz) << 4));
+        }
         sacc[0][kt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
         sacc[1][kt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int ds = 0; ds < DS; ++ds) {
-          const uint4 a = lds_read16(s_k, (16 * kt + r16) * ROWB + (((4 * ds + g4) ^ kswz) << 4));
-          sacc[0][kt] = M::mfma(a, qreg[0][ds], sacc[0][kt]);
-          sacc[1][kt] = M::mfma(a, qreg[1][ds], sacc[1][kt]);
+          sacc[0][kt] = M::mfma(ka[kt & 1][ds], qreg[0][ds], sacc[0][kt]);
+          sacc[1][kt] = M::mfma(ka[kt & 1][ds], qreg[1][ds], sacc[1][kt]);
+        }
+        if (spread && kt % EVERY == 0) {
+#pragma unroll
+          for (int j = 0; j < PAIRS; ++j) {
+            const int i = (kt / EVERY) * PAIRS + j;
+            dma16(koff[i], n_kbase, n_dst + i * 1024);
+            dma16(voff[i], n_vbase, n_dst + TILE_B + i * 1024);
+          }
         }
       }
       // The query rows are dead now: on the item's last tile, start the next
-      // item's loads.
+      // item's loads.  Its store slot goes straight into st_slot (this item's
+      // store steps ran at the top of this tile): a copy at the item's end
+      // would have to wait for the load, and with it for every store issued
+      // after it.
       if (t + 1 == cur.ntiles && has_next) {
         load_q(nxt);
-        nxt_slot = load_slot(nxt);
+        st_slot = load_slot(nxt);
       }
 
       // ---- online softmax (exp2 domain) and P^T packing ----
@@ -624,7 +664,7 @@ __global__ __launch_bounds__(kVarlenThreads, 2) void varlen_attention_kernel(Var
       if (nxt.ntiles > 0)
         issue_tile(nxt.h, nxt.pool_prefix, nxt.kend, nxt.new_base, nxt.table_row, 0, stage);
       load_q(nxt);
-      nxt_slot = load_slot(nxt);
+      st_slot = load_slot(nxt);
     }
 
     // ---- normalise and write: lane holds O[row r16][16 dt + 4 g4 + i] ----
@@ -684,7 +724,6 @@ __global__ __launch_bounds__(kVarlenThreads, 2) void varlen_attention_kernel(Var
     }
     if (!has_next) break;
     cur = nxt;
-    st_slot = nxt_slot;
   }
 }
 
