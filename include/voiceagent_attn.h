@@ -220,7 +220,11 @@ size_t va_paged_decode_workspace_bytes(const va_decode_args* args);
 /* One-token GQA attention over a paged pool: split-context partitions, then
  * (only when a context spans several) a merge pass.  Replaces the decode use of
  * flash_attn_varlen_func (qwen_asr_vllm/layers/attention.py:96-107) and
- * paged_attention_decode (qwen_tts_paged_attention.py:383-516). */
+ * paged_attention_decode (qwen_tts_paged_attention.py:383-516).  head_dim
+ * 64 / 128 / 256 with groups of 1 / 2 / 4 / 8 run the vector kernels (16-byte
+ * aligned strides and pointers); any other head_dim up to 1024 and any group
+ * run a scalar kernel that needs element alignment only and never splits
+ * (no prologue, no FP8 pool there). */
 int va_paged_decode(const va_decode_args* args, void* stream);
 
 /* Size of the scratch buffer of va_paged_decode_noalloc, per GPU. */

@@ -63,10 +63,19 @@ def test_decode_rejects_bad_geometry():
     assert lib.va_paged_decode(ctypes.byref(args), None) == -1
     assert "valid_stride_seq" in N.last_error()
     args.valid_mask = None
-    args.head_dim = 96  # unsupported head_dim reaches the dispatcher only after host checks
     args.q_stride_seq = 1  # not a 16-byte multiple
     assert lib.va_paged_decode(ctypes.byref(args), None) == -1
     assert "16-byte" in N.last_error()
+    # Other head dims take the small-head kernel, which needs element
+    # alignment only; the checks still run before any launch.
+    args.head_dim, args.dtype = 4, 2  # fp32
+    args.q_stride_seq = 1  # 4 bytes: fine for fp32 elements
+    args.q = 18  # not 4-byte aligned
+    assert lib.va_paged_decode(ctypes.byref(args), None) == -1
+    assert "4-byte aligned" in N.last_error()
+    args.head_dim = 2000
+    assert lib.va_paged_decode(ctypes.byref(args), None) == -1
+    assert "head_dim 2000 outside" in N.last_error()
 
 
 def test_decode_workspace_sizing():

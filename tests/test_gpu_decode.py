@@ -4,6 +4,7 @@ Tolerances (max-abs): 1e-5 for fp32 inputs, 2e-2 for bf16/fp16 inputs, both
 against the oracle evaluated in fp32 on the same inputs.
 """
 
+import math
 import os
 
 import numpy as np
@@ -301,12 +302,93 @@ def test_tts_known_answer_integer_values(dev):
     assert torch.all(out[0] == 1.0) and torch.all(out[1] == 9.0)
 
 
-def test_tts_unsupported_head_dim_raises(dev):
+def test_tts_reference_fixture_on_the_small_head_kernel(dev):
+    # The reference's own fixture (tests/test_qwen_tts_paged_attention_kernel.py:16-57,
+    # and the fused write of :144-177): HND pool of 2-token pages, head_dim 4, fp32,
+    # GQA 2, a left-padded row.  Expected values: the committed float64 brute force
+    # (tests/golden/brute.py); the fused pools bit-exact.
     g = np.load(os.path.join(GOLDEN, "tts_seed17.npz"))
-    args = [torch.from_numpy(g[k]).to(dev) for k in ("q", "k_pool", "v_pool", "page_table",
-                                                      "seq_lens", "valid")]
-    with pytest.raises(_native.NativeError, match="head_dim"):
-        paged_attention_decode(*args)
+    t = {k: torch.from_numpy(g[k]) for k in g.files}
+    kd, vd = t["k_pool"].to(dev), t["v_pool"].to(dev)
+    out = paged_attention_decode(t["q"].to(dev), kd, vd, t["page_table"].to(dev),
+                                 t["seq_lens"].to(dev), t["valid"].to(dev))
+    torch.cuda.synchronize()
+    assert out.shape == (2, 4, 1, 4)
+    assert (out[:, :, 0].double().cpu() - t["expected"]).abs().max().item() <= 1e-5
+    assert torch.equal(kd.cpu(), t["k_pool"]) and torch.equal(vd.cpu(), t["v_pool"])
+    kd, vd = t["k_pool"].to(dev), t["v_pool"].to(dev)
+    out = paged_attention_decode(t["q"].to(dev), kd, vd, t["page_table"].to(dev),
+                                 t["seq_lens"].to(dev), t["valid"].to(dev),
+                                 new_key=t["new_key"].to(dev), new_value=t["new_value"].to(dev))
+    torch.cuda.synchronize()
+    assert torch.equal(kd.cpu(), t["k_pool_fused"]) and torch.equal(vd.cpu(), t["v_pool_fused"])
+    assert (out[:, :, 0].double().cpu() - t["expected_fused"]).abs().max().item() <= 1e-5
+
+
+@pytest.mark.parametrize(
+    "dtype,d,hq,hkv,bs,layout,fused,bound",
+    [
+        (torch.float32, 1, 4, 2, 2, ops.LAYOUT_HND, False, "exact"),
+        (torch.float32, 4, 6, 2, 1, ops.LAYOUT_NHD, True, "exact"),     # group 3, 1-token blocks
+        (torch.bfloat16, 32, 8, 8, 5, ops.LAYOUT_HND, True, "limit"),   # current row detached
+        (torch.float16, 96, 12, 4, 16, ops.LAYOUT_NHD, False, "exact"),  # head_dim 96, group 3
+        (torch.bfloat16, 128, 6, 2, 16, ops.LAYOUT_NHD, True, "exact"),  # head_dim 128, group 3
+        (torch.float32, 160, 4, 1, 3, ops.LAYOUT_HND, False, "limit"),   # group 4, odd blocks
+    ],
+)
+def test_small_head_kernel_matches_oracle(dev, dtype, d, hq, hkv, bs, layout, fused, bound):
+    # Shapes the vector kernels do not take run on the small-head kernel: any
+    # head_dim, any group, any block size, contexts past its 1024-key chunk,
+    # a key mask, invalid block ids, the fused current row (in place, or
+    # detached past key_limit), and the TTS read bounds.
+    gen = torch.Generator().manual_seed(d * 131 + hq)
+    lens = [1, 3, 17, 1030, 2500, 700]
+    B = len(lens)
+    need = [math.ceil(n / bs) for n in lens]
+    nb = sum(need) + 6
+    perm = torch.randperm(nb, generator=gen).tolist()
+    width = max(need) + 1
+    rows, cur = [], 0
+    for n in need:
+        rows.append(perm[cur:cur + n] + [-1] * (width - n))
+        cur += n
+    table = torch.tensor(rows, dtype=torch.int32)
+    table[4, 3] = nb + 7  # an invalid block id inside a context: those tokens are masked
+    shape = (nb, bs, hkv, d) if layout == ops.LAYOUT_NHD else (nb, hkv, bs, d)
+    kp = (torch.randn(shape, generator=gen) * 0.5).to(dtype)
+    vp = torch.randn(shape, generator=gen).to(dtype)
+    q = torch.randn(B, hq, d, generator=gen).to(dtype)
+    valid = torch.rand(B, 2600, generator=gen) < 0.85
+    valid[:, 0] = True
+    nk = (torch.randn(B, hkv, d, generator=gen) * 0.5).to(dtype) if fused else None
+    nv = torch.randn(B, hkv, d, generator=gen).to(dtype) if fused else None
+    lens_t = torch.tensor(lens, dtype=torch.int64)
+    key_limit = 1600 if bound == "limit" else 0
+    read_width = (1500 // bs) if bound == "limit" else 0
+    kd, vd = kp.to(dev), vp.to(dev)
+    scale = d ** -0.5
+    print(f"small head {dtype} d={d} hq={hq} hkv={hkv} bs={bs} {layout} fused={fused} {bound}",
+          flush=True)
+    out = ops.paged_decode(q.to(dev), kd, vd, table.to(dev), lens_t.to(dev),
+                           max_seq_len=max(lens), scale=scale, layout=layout,
+                           valid_mask=valid.to(dev),
+                           new_k=None if nk is None else nk.to(dev),
+                           new_v=None if nv is None else nv.to(dev),
+                           key_limit=key_limit, table_read_width=read_width)
+    torch.cuda.synchronize()
+    k0, v0 = kp, vp
+    if fused:
+        k0, v0 = oracle.write_current_kv(kp, vp, table, lens_t, nk, nv, layout=layout)
+    assert torch.equal(kd.cpu(), k0) and torch.equal(vd.cpu(), v0)
+    # The oracle sees the invalid block as a valid one whose tokens are masked.
+    table_o, valid_o = table.clone(), valid.clone()
+    table_o[4, 3] = 0
+    valid_o[4, 3 * bs:4 * bs] = False
+    ref = oracle.paged_decode(q, k0, v0, table_o, lens_t, scale, layout=layout,
+                              valid_mask=valid_o, key_limit=key_limit or None,
+                              table_read_width=read_width or None)
+    tol = 1e-5 if dtype == torch.float32 else 2e-2
+    assert (out.float().cpu() - ref).abs().max().item() <= tol
 
 
 def test_constant_values_property_at_cfg2_scale(dev):

@@ -16,6 +16,7 @@ import torch
 from oracle import attention as oracle
 from voiceagent_amd import ops, workloads
 from voiceagent_amd.layers.attention import PagedAttention
+from voiceagent_amd.layers.attention import store_kvcache as layer_store_kvcache
 from voiceagent_amd.layers.context import AttentionContext, attention_context
 
 pytestmark = pytest.mark.gpu
@@ -54,6 +55,12 @@ def test_store_quantises_bit_exactly(dev, dtype, scale):
     ek, ev = oracle.store_kvcache(key, value, kp, vp, slots, k_scale=scale, v_scale=scale * 2)
     assert torch.equal(_codes(kd.cpu()), _codes(ek))
     assert torch.equal(_codes(vd.cpu()), _codes(ev))
+    # The reference-signature layer function passes the scales through.
+    kl, vl = kp.to(dev), vp.to(dev)
+    layer_store_kvcache(key.to(dev), value.to(dev), kl, vl, slots.to(dev), k_scale=scale,
+                        v_scale=scale * 2)
+    torch.cuda.synchronize()
+    assert torch.equal(_codes(kl.cpu()), _codes(ek)) and torch.equal(_codes(vl.cpu()), _codes(ev))
 
 
 def _fp8_batch(lens, dev, seed, dtype=torch.bfloat16, hq=16, hkv=8, d=128, bs=16,

@@ -40,6 +40,14 @@ static bool general_kernel_forced() {
   return forced != 0;
 }
 
+// Shapes neither the matrix-core nor the general kernel takes run on the
+// small-head kernel (see launch_paged_decode_small).
+static bool small_head_decode(const va_decode_args* a) {
+  const bool d_ok = a->head_dim == 64 || a->head_dim == 128 || a->head_dim == 256;
+  const int G = a->num_kv_heads > 0 ? a->num_heads / a->num_kv_heads : 0;
+  return !d_ok || !(G == 1 || G == 2 || G == 4 || G == 8);
+}
+
 static bool use_mfma_decode(const va_decode_args* a) {
   if (a->dtype != VA_BF16 && a->dtype != VA_F16) return false;
   const int64_t kv_eb = a->pool.kv_format == VA_KV_FP8_E4M3 ? 1 : 2;
@@ -80,6 +88,11 @@ static int nosplit_tokens_for(const va_decode_args* a) {
 
 static DecodePlan plan_decode(const va_decode_args* a) {
   DecodePlan pl{};
+  if (small_head_decode(a)) {  // one workgroup per (sequence, query head), no split
+    pl.max_parts = 1;
+    pl.split_tokens = a->max_seq_len > 0 ? a->max_seq_len : 1;
+    return pl;
+  }
   const int G = a->num_kv_heads > 0 ? a->num_heads / a->num_kv_heads : 1;
   int unit = use_mfma_decode(a) ? mfma_unit_for(a->head_dim)
                                 : decode_unit_for(a->dtype, a->head_dim, G);
@@ -300,18 +313,35 @@ int va::paged_decode_impl(const va_decode_args* a, void* stream) {
                "va_paged_decode: key_limit and table_read_width must be non-negative");
   VA_CHECK_ARG(a->valid_mask == nullptr || (a->valid_len >= 0 && a->valid_stride_seq >= 0),
                "va_paged_decode: valid_len and valid_stride_seq must be non-negative");
+  // The vector kernels move 16-byte pieces; the small-head kernel moves
+  // single elements.
+  const bool small = small_head_decode(a);
+  const int64_t align = small ? eb : 16, palign = small ? kv_eb : 16;
+  VA_CHECK_ARG(!small || (a->head_dim >= 1 && a->head_dim <= kSmallMaxHeadDim),
+               "va_paged_decode: head_dim %d outside [1, %d]", a->head_dim, kSmallMaxHeadDim);
+  VA_CHECK_ARG(!small || (a->prologue == nullptr && !f8),
+               "va_paged_decode: the q/k prologue and FP8 pools need head_dim 64|128|256 and "
+               "group 1|2|4|8 (got head_dim %d, group %d)",
+               a->head_dim, G);
   const int64_t strides[] = {a->q_stride_seq,      a->q_stride_head,     a->out_stride_seq,
                              a->out_stride_head,   a->new_k_stride_seq,  a->new_k_stride_head,
                              a->new_v_stride_seq,  a->new_v_stride_head};
   for (int64_t s : strides)
-    VA_CHECK_ARG((s * eb) % 16 == 0, "va_paged_decode: strides must be 16-byte multiples");
+    VA_CHECK_ARG((s * eb) % align == 0, "va_paged_decode: strides must be %lld-byte multiples",
+                 (long long)align);
   const int64_t pstrides[] = {a->pool.stride_block, a->pool.stride_slot, a->pool.stride_head};
   for (int64_t s : pstrides)
-    VA_CHECK_ARG((s * kv_eb) % 16 == 0, "va_paged_decode: pool strides must be 16-byte multiples");
-  const uintptr_t ptrs[] = {(uintptr_t)a->q, (uintptr_t)a->out, (uintptr_t)a->pool.k,
-                            (uintptr_t)a->pool.v, (uintptr_t)a->new_k, (uintptr_t)a->new_v};
+    VA_CHECK_ARG((s * kv_eb) % palign == 0,
+                 "va_paged_decode: pool strides must be %lld-byte multiples", (long long)palign);
+  const uintptr_t ptrs[] = {(uintptr_t)a->q, (uintptr_t)a->out, (uintptr_t)a->new_k,
+                            (uintptr_t)a->new_v};
   for (uintptr_t p : ptrs)
-    VA_CHECK_ARG(p % 16 == 0, "va_paged_decode: pointers must be 16-byte aligned");
+    VA_CHECK_ARG(p % align == 0, "va_paged_decode: pointers must be %lld-byte aligned",
+                 (long long)align);
+  const uintptr_t pptrs[] = {(uintptr_t)a->pool.k, (uintptr_t)a->pool.v};
+  for (uintptr_t p : pptrs)
+    VA_CHECK_ARG(p % palign == 0, "va_paged_decode: pool pointers must be %lld-byte aligned",
+                 (long long)palign);
 
   const DecodePlan pl = plan_decode(a);
   if (pl.total_bytes > 0) {
@@ -417,6 +447,15 @@ int va::paged_decode_impl(const va_decode_args* a, void* stream) {
   const dim3 grid(a->num_seqs, a->num_kv_heads, pl.max_parts);
   const hipStream_t s = (hipStream_t)stream;
   bool ok = false;
+  if (small) {
+    ok = launch_paged_decode_small(a->dtype, a->head_dim, G, p, dim3(a->num_seqs, a->num_heads),
+                                   s);
+    if (!ok) {
+      set_error("va_paged_decode: unsupported dtype %d / head_dim %d", a->dtype, a->head_dim);
+      return VA_ERR_UNSUPPORTED;
+    }
+    return check_launch("va_paged_decode");
+  }
   if (f8 && !use_mfma_decode(a)) {
     set_error("va_paged_decode: an FP8 pool needs bf16/f16 q, a block size that is a multiple "
               "of 16, head_dim 64|128|256 and group 1|2|4|8 (got dtype %d, block %d, head_dim %d, "

@@ -774,5 +774,13 @@ static bool dispatch_d(int D, int G, const DecodeParams& p, dim3 grid, hipStream
 template <typename ET>
 bool launch_paged_decode(int D, int G, const DecodeParams& p, dim3 grid, hipStream_t s);
 
+// Shapes the two kernels above do not take (head_dim other than 64 / 128 /
+// 256, or a group other than 1 / 2 / 4 / 8) go to the small-head kernel
+// (paged_decode_small.hip): grid (num_seqs, num_heads), no context split.
+// False for a head_dim outside [1, kSmallMaxHeadDim] or an unknown dtype.
+constexpr int kSmallMaxHeadDim = 1024;
+bool launch_paged_decode_small(int dtype, int D, int G, const DecodeParams& p, dim3 grid,
+                               hipStream_t s);
+
 }  // namespace va
 

@@ -59,12 +59,17 @@ def store_kvcache(
     k_cache: torch.Tensor,
     v_cache: torch.Tensor,
     slot_mapping: torch.Tensor,
+    *,
+    k_scale: float = 1.0,
+    v_scale: float = 1.0,
 ) -> None:
     """Scatter key/value rows [N, Hkv, D] into an NHD pool [nb, bs, Hkv, D].
 
     Mirrors qwen_asr_vllm/layers/attention.py:52-67, including its stride
     contract (assertions :61-64): rows may be strided (the engine's ``v`` is a
-    view of the fused qkv output) but each row's heads are contiguous.
+    view of the fused qkv output) but each row's heads are contiguous.  An FP8
+    (float8_e4m3fn) pool receives the codes of key / k_scale and
+    value / v_scale; the scales are ignored for a 16-bit or fp32 pool.
     """
     num_tokens, num_heads, head_dim = key.shape
     hidden = num_heads * head_dim
@@ -72,7 +77,8 @@ def store_kvcache(
     assert key.stride(1) == head_dim and value.stride(1) == head_dim
     assert k_cache.stride(1) == hidden and v_cache.stride(1) == hidden
     assert slot_mapping.numel() == num_tokens
-    ops.store_kvcache(key, value, k_cache, v_cache, slot_mapping, layout=ops.LAYOUT_NHD)
+    ops.store_kvcache(key, value, k_cache, v_cache, slot_mapping, layout=ops.LAYOUT_NHD,
+                      k_scale=k_scale, v_scale=v_scale)
 
 
 class PagedAttention(nn.Module):
