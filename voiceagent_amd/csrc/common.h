@@ -256,20 +256,37 @@ __device__ inline float strided_max(float x) {
 
 __device__ inline float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
-// The value of lane (lane ^ 16) / (lane ^ 32) through gfx950's
-// v_permlane16_swap / v_permlane32_swap (VALU, no LDS round trip).
-// permlane32_swap(a, a) leaves lanes 32..63 of its first result and lanes
-// 0..31 of its second holding the other half's values; permlane16_swap does
-// the same for the odd / even 16-lane rows of each half.
-__device__ inline float lane_xor32(float x) {
+// Maximum / sum of x over lanes l and l ^ 32 (or l ^ 16) through gfx950's
+// v_permlane32_swap / v_permlane16_swap (VALU, no LDS round trip).
+// permlane32_swap(a, a) swaps lanes 32..63 of its first operand with lanes
+// 0..31 of its second, so in every lane its two results hold x[l] and
+// x[l ^ 32], in one order or the other: the reduction of the two needs no
+// lane test.  permlane16_swap does the same for the odd / even 16-lane rows
+// of each half.  The maximum is a plain v_max_f32: fmaxf would canonicalise
+// both swapped values first (two more instructions per step).
+__device__ inline float max_xor32(float x) {
   const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
                                                   false);
-  return __uint_as_float((threadIdx.x & 32) ? r[0] : r[1]);
+  float m;
+  asm("v_max_f32 %0, %1, %2" : "=v"(m) : "v"(r[0]), "v"(r[1]));
+  return m;
 }
-__device__ inline float lane_xor16(float x) {
+__device__ inline float max_xor16(float x) {
   const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false,
                                                   false);
-  return __uint_as_float((threadIdx.x & 16) ? r[0] : r[1]);
+  float m;
+  asm("v_max_f32 %0, %1, %2" : "=v"(m) : "v"(r[0]), "v"(r[1]));
+  return m;
+}
+__device__ inline float sum_xor32(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ inline float sum_xor16(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
 // ------------------------------------------------------- global -> LDS DMA

@@ -575,8 +575,8 @@ __global__ __launch_bounds__(MfmaDecodeShape<D>::W * 64, 1) void paged_decode_mf
     const uint32_t keep0 = ((live & 1u) ? 0xffffu : 0u) | ((live & 2u) ? 0xffff0000u : 0u);
     const uint32_t keep1 = ((live & 4u) ? 0xffffu : 0u) | ((live & 8u) ? 0xffff0000u : 0u);
     float mx = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
-    mx = fmaxf(mx, lane_xor16(mx));
-    mx = fmaxf(mx, lane_xor32(mx));
+    mx = max_xor16(mx);
+    mx = max_xor32(mx);
     const float mxs = mx * p.scale_log2;
     if (__builtin_amdgcn_ballot_w64(mxs > m + kDecLazy) != 0) {
       const float mnew = fmaxf(m, mxs);
@@ -618,8 +618,8 @@ __global__ __launch_bounds__(MfmaDecodeShape<D>::W * 64, 1) void paged_decode_mf
   // A wave with fewer tiles than the early issue fetched still has them in
   // flight: they land before the merge reuses the LDS.
   wait_vmcnt<0>();
-  l += lane_xor16(l);
-  l += lane_xor32(l);
+  l = sum_xor16(l);
+  l = sum_xor32(l);
   if constexpr (!kOwnMerge) __syncthreads();  // every wave is done with its stages
   float* s_o = reinterpret_cast<float*>(kOwnMerge ? s_mrg : s_buf);  // [W][G][D]
   float* s_m = s_o + W * G * D;                                       // [G][W]

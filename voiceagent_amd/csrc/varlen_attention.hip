@@ -610,8 +610,8 @@ __global__ __launch_bounds__(kVarlenThreads, 2) void varlen_attention_kernel(Var
         for (int kt = 0; kt < KT; ++kt)
 #pragma unroll
           for (int i = 0; i < 4; ++i) mx = fmaxf(mx, sv[kt][i]);
-        mx = fmaxf(mx, lane_xor16(mx));
-        mx = fmaxf(mx, lane_xor32(mx));
+        mx = max_xor16(mx);
+        mx = max_xor32(mx);
         const float mxs = mx * p.scale_log2;
         if (__builtin_amdgcn_ballot_w64(mxs > m[tt] + kLazy) != 0) {
           const float mnew = fmaxf(m[tt], mxs);
@@ -682,8 +682,8 @@ __global__ __launch_bounds__(kVarlenThreads, 2) void varlen_attention_kernel(Var
 #pragma unroll
       for (int tt = 0; tt < 2; ++tt) {
         float lt = l[tt];
-        lt += lane_xor16(lt);
-        lt += lane_xor32(lt);
+        lt = sum_xor16(lt);
+        lt = sum_xor32(lt);
         const float inv = lt > 0.f ? 1.f / lt : 0.f;
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) {
