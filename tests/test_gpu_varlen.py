@@ -98,6 +98,24 @@ def test_ragged_lengths_and_geometries(dev, dtype, causal, hq, hkv, d):
     assert _err(out, ref) <= TOL
 
 
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("hq,hkv,d", [(14, 14, 64), (16, 8, 128), (16, 4, 64), (32, 4, 128)])
+def test_one_query_block_per_sequence(dev, dtype, hq, hkv, d):
+    # Non-causal launches whose sequences all fit one query block (128 rows /
+    # group) take the instantiation that streams K/V non-temporally; ragged
+    # lengths up to the block, one empty sequence.
+    bq = 128 // (hq // hkv)
+    lens = [n for n in (1, 3, bq // 2 - 1, bq // 2, bq // 2 + 1, bq - 1, bq, 7) if n > 0] + [0, bq]
+    b = workloads.make_varlen_batch(lens, hq, hkv, d, causal=False, dtype=dtype, seed=hq + d)
+    out = ops.varlen_attention(b.q.to(dev), b.k.to(dev), b.v.to(dev), b.cu_seqlens.to(dev),
+                               b.cu_seqlens.to(dev), b.max_seqlen, b.max_seqlen, scale=b.scale,
+                               causal=False)
+    ref = oracle.varlen_attention(b.q, b.k, b.v, b.cu_seqlens, b.cu_seqlens, b.scale, False)
+    assert b.max_seqlen <= bq
+    assert _err(out, ref) <= TOL
+
+
 def test_persistent_rounds_long_prompts(dev):
     # 8 prompts of ~2000 tokens, 8 kv heads: each XCD lists 8 pairs x 32 blocks,
     # so every workgroup takes several items in snake order and the level walk
