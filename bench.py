@@ -277,6 +277,9 @@ def bench_lib():
         lib.va_bench_hbm_read.restype = ctypes.c_int
         lib.va_bench_hbm_read.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int,
                                           ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
+        lib.va_bench_hbm_copy.restype = ctypes.c_int
+        lib.va_bench_hbm_copy.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p,
+                                          ctypes.c_size_t, ctypes.c_int, ctypes.c_void_p]
         lib.va_bench_last_error.restype = ctypes.c_char_p
         lib.va_bench_last_error.argtypes = []
         _BENCH_LIB = lib
@@ -295,6 +298,47 @@ def hbm_read(buf: torch.Tensor, workgroups: int, mode: str, sink: torch.Tensor) 
                                        sink.data_ptr(), torch.cuda.current_stream().cuda_stream)
     if rc != 0:
         raise ValueError(bench_lib().va_bench_last_error().decode())
+
+
+def hbm_copy(src: torch.Tensor, dst: torch.Tensor, workgroups: int) -> None:
+    """Read all of `src` and write all of `dst` (contiguous GPU tensors) in one
+    launch of `workgroups` workgroups (va_bench_hbm_copy)."""
+    if not (src.is_cuda and dst.is_cuda and src.is_contiguous() and dst.is_contiguous()):
+        raise ValueError("hbm_copy needs contiguous GPU tensors")
+    rc = bench_lib().va_bench_hbm_copy(src.data_ptr(), src.numel() * src.element_size(),
+                                       dst.data_ptr(), dst.numel() * dst.element_size(),
+                                       int(workgroups), torch.cuda.current_stream().cuda_stream)
+    if rc != 0:
+        raise ValueError(bench_lib().va_bench_last_error().decode())
+
+
+def copy_floor(name: str, read_bytes: int, write_bytes: int, launches: int, args, dev,
+               stream) -> dict:
+    """Mixed read/write floor: `read_bytes` read and `write_bytes` written in
+    one launch (va_bench_hbm_copy), `launches` launches per graph replay on
+    distinct windows (cold), at several grid sizes; the fastest is reported."""
+    rb, wb = read_bytes // 16 * 16, write_bytes // 16 * 16
+    rs, ws = (rb + 65535) // 65536 * 65536, (wb + 65535) // 65536 * 65536
+    src = torch.ones(rs * launches, dtype=torch.uint8, device=dev)
+    dst = torch.zeros(ws * launches, dtype=torch.uint8, device=dev)
+    pairs = [(src[i * rs:i * rs + rb], dst[i * ws:i * ws + wb]) for i in range(launches)]
+    table = {}
+    for wgs in (256, 512, 1024, 2048):
+        def step(wgs=wgs):
+            for a, b in pairs:
+                hbm_copy(a, b, wgs)
+
+        ms, _ = timed_graph(step, args.steps, args.warmup, stream)
+        table[wgs] = ms * 1000.0 / launches
+    wgs, us = min(table.items(), key=lambda kv: kv[1])
+    gbs = (rb + wb) / (us * 1e-6) / 1e9
+    log(f"[copy floor] {name}: read {rb / 1e6:.2f} MB + write {wb / 1e6:.2f} MB: "
+        + ", ".join(f"{w}: {t:.2f}" for w, t in table.items())
+        + f" us/launch; best {us:.2f} us at {wgs} workgroups, {gbs:.0f} GB/s")
+    del src, dst, pairs
+    return {"us_per_launch": round(us, 2), "gbs": round(gbs, 1), "workgroups": wgs,
+            "read_bytes": rb, "write_bytes": wb,
+            "us_by_grid": {str(w): round(t, 2) for w, t in table.items()}}
 
 
 def bench_floor(args, dev, stream):
@@ -325,7 +369,20 @@ def bench_floor(args, dev, stream):
     gbs = nbytes / (us * 1e-6) / 1e9
     log(f"[floor] best: {mode} at {wgs} workgroups, {us:.2f} us/launch for "
         f"{nbytes / 1e6:.2f} MB, {gbs:.0f} GB/s ({gbs / HBM_PEAK_GBS:.3f} of peak)")
-    return {"us_per_launch": round(us, 2), "gbs": round(gbs, 1),
+    del buf, views
+    # Mixed floors of the varlen launches: their algorithmic reads (q, k, v)
+    # and writes (output, and for prefill the stored K/V rows).
+    pre_lens, wins = workloads.cfg3_lens(0), workloads.cfg4_windows(0)
+    # varlen_bytes counts q, k, v and out; at GQA 16/8 out is a third of it and
+    # the stored K/V rows are as large as k + v.
+    pre_r = workloads.varlen_bytes(pre_lens, workloads.HQ, workloads.HKV,
+                                   workloads.HEAD_DIM) * 2 // 3  # q + k + v
+    pre_w = pre_r  # output + stored K/V rows
+    enc_all = workloads.varlen_bytes(wins, 14, 14, 64)
+    copies = {"prefill_cfg3": copy_floor("prefill cfg3", pre_r, pre_w, layers, args, dev, stream),
+              "encoder_cfg4": copy_floor("encoder cfg4", enc_all * 3 // 4, enc_all // 4, 18,
+                                         args, dev, stream)}
+    return {"us_per_launch": round(us, 2), "gbs": round(gbs, 1), "copy": copies,
             "frac": round(gbs / HBM_PEAK_GBS, 4), "bytes": nbytes, "mode": mode,
             "workgroups": wgs,
             "us_by_mode_grid": {f"{m}/{w}": round(t, 2) for (m, w), t in table.items()},

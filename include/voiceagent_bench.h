@@ -3,7 +3,8 @@
  *
  * Not part of the drop-in ABI (include/voiceagent_attn.h) and with no
  * counterpart in the reference: bench.py uses it to measure the HBM read
- * floor that the decode kernel's bandwidth is read against.
+ * floor that the decode kernel's bandwidth is read against, and the mixed
+ * read/write floor of the varlen launches.
  */
 #ifndef VOICEAGENT_BENCH_H
 #define VOICEAGENT_BENCH_H
@@ -27,6 +28,15 @@ extern "C" {
  * message is in va_bench_last_error()). */
 int va_bench_hbm_read(const void* src, size_t bytes, int workgroups, int mode, void* sink,
                       void* stream);
+
+/* Mixed stream in one launch of `workgroups` 512-lane workgroups: reads
+ * `read_bytes` at `src` and writes `write_bytes` at `dst` (16-byte aligned,
+ * non-overlapping), both contiguous, with non-temporal loads and stores; each
+ * workgroup takes one contiguous slice of max(read_bytes, write_bytes).  The
+ * floor that a launch reading and writing those byte counts is read against.
+ * Returns 0, or -1 on a bad argument (va_bench_last_error()). */
+int va_bench_hbm_copy(const void* src, size_t read_bytes, void* dst, size_t write_bytes,
+                      int workgroups, void* stream);
 
 const char* va_bench_last_error(void);
 

@@ -17,6 +17,10 @@
 // Register loads are XOR-folded and the fold is written to sink[w] only when
 // it equals a fixed value, so the loads cannot be removed and, in practice,
 // nothing is written; the DMA path writes only LDS.
+//
+// va_bench_hbm_copy is the mixed floor for the varlen launches: it reads and
+// writes given byte counts in one launch (for prefill, its q, k, v reads and
+// its output and stored-row writes).
 #include <stdarg.h>
 #include <stdio.h>
 
@@ -90,8 +94,58 @@ __global__ __launch_bounds__(kProbeThreads) void hbm_read_probe_dma_kernel(const
   wait_vmcnt<0>();
 }
 
+// Mixed read/write stream: workgroup w covers the slice [w per_wg, (w + 1)
+// per_wg) of max(nr, nw) 16-byte words; word j is read from src when j < nr
+// and written to dst when j < nw (the word read, so that no load can be
+// dropped).  Eight non-temporal loads per lane are in flight before their
+// non-temporal stores, as an attention epilogue stores rows it has no further
+// use for.
+template <int kUnroll>
+__global__ __launch_bounds__(kProbeThreads) void hbm_copy_probe_kernel(
+    const uint4* __restrict__ src, int64_t nr, uint4* __restrict__ dst, int64_t nw,
+    int64_t per_wg) {
+  const int64_t n = nr > nw ? nr : nw;
+  const int64_t beg = (int64_t)blockIdx.x * per_wg;
+  const int64_t end = beg + per_wg < n ? beg + per_wg : n;
+  for (int64_t i = beg + threadIdx.x; i < end; i += kUnroll * kProbeThreads) {
+    uint4 w[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const int64_t j = i + (int64_t)u * kProbeThreads;
+      w[u] = (j < end && j < nr) ? ld16_nt(src + j) : make_uint4((uint32_t)j, 0u, 0u, 0u);
+    }
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const int64_t j = i + (int64_t)u * kProbeThreads;
+      if (j < end && j < nw) st16_nt(dst + j, w[u]);
+    }
+  }
+}
+
 }  // namespace
 }  // namespace va
+
+extern "C" int va_bench_hbm_copy(const void* src, size_t read_bytes, void* dst,
+                                 size_t write_bytes, int workgroups, void* stream) {
+  using namespace va;
+  if ((read_bytes > 0 && src == nullptr) || (write_bytes > 0 && dst == nullptr))
+    return bench_fail("va_bench_hbm_copy: null pointer");
+  if ((uintptr_t)src % 16 != 0 || (uintptr_t)dst % 16 != 0 || read_bytes % 16 != 0 ||
+      write_bytes % 16 != 0)
+    return bench_fail("va_bench_hbm_copy: pointers and sizes must be 16-byte aligned");
+  if (workgroups < 1 || workgroups > 65536)
+    return bench_fail("va_bench_hbm_copy: workgroups must be in [1, 65536]");
+  const int64_t nr = (int64_t)(read_bytes / 16), nw = (int64_t)(write_bytes / 16);
+  const int64_t n = nr > nw ? nr : nw;
+  if (n == 0) return 0;
+  const int64_t per_wg = (n + workgroups - 1) / workgroups;
+  hipLaunchKernelGGL((hbm_copy_probe_kernel<8>), dim3((unsigned)workgroups), dim3(kProbeThreads),
+                     0, (hipStream_t)stream, reinterpret_cast<const uint4*>(src), nr,
+                     reinterpret_cast<uint4*>(dst), nw, per_wg);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return bench_fail("va_bench_hbm_copy: launch failed: %s", hipGetErrorString(e));
+  return 0;
+}
 
 extern "C" int va_bench_hbm_read(const void* src, size_t bytes, int workgroups, int mode,
                                  void* sink, void* stream) {
