@@ -250,3 +250,41 @@ def test_paged_attention_layer_prefill_then_decode_on_fp8_pool(dev):
         ref = oracle.paged_decode(qd, ek, ev, table, torch.tensor(lens), d ** -0.5,
                                   k_scale=0.03, v_scale=0.06)
         assert _err(out, ref) <= 2e-2, step
+
+
+@pytest.mark.parametrize("B", [8, 40])
+def test_fused_prologue_over_fp8_pool(dev, B):
+    # The Qwen3 q/k prologue fused into a decode over an FP8 pool: q and the
+    # current key are normalised and rotated inside the launch, the current
+    # row is stored as codes and attended as their values.  B=8 splits the
+    # contexts into partitions, B=40 does not.  The fused launch equals the
+    # two-launch path (va_qk_norm_rope, then the FP8 decode) bit for bit,
+    # output and pool, and the oracle on the dequantised pool within 2e-2.
+    lens = torch.randint(20, 300, (B,), generator=torch.Generator().manual_seed(B)).tolist()
+    ks, vs = 0.05, 0.08
+    table, kp, vp, q, nk, nv = _fp8_batch(lens, dev, seed=B + 3, k_scale=ks, v_scale=vs)
+    g = torch.Generator().manual_seed(B + 4)
+    wq = (torch.rand(128, generator=g) + 0.5).to(torch.bfloat16)
+    wk = (torch.rand(128, generator=g) + 0.5).to(torch.bfloat16)
+    cs = oracle.rope_cache(128, 1024, 1_000_000.0)
+    pos = torch.tensor(lens) - 1
+    lens_t = torch.tensor(lens, dtype=torch.int32)
+    print(f"fp8 decode with the fused prologue B={B}", flush=True)
+    pro = ops.QKPrologue(wq.to(dev), wk.to(dev), 1e-6, cs.to(dev), pos.to(dev))
+    common = dict(max_seq_len=max(lens), scale=128 ** -0.5, new_v=nv.to(dev), k_scale=ks,
+                  v_scale=vs)
+    kd1, vd1 = kp.to(dev), vp.to(dev)
+    kd2, vd2 = kd1.clone(), vd1.clone()
+    td, ld = table.to(dev), lens_t.to(dev)
+    out1 = ops.paged_decode(q.to(dev), kd1, vd1, td, ld, new_k=nk.to(dev), prologue=pro,
+                            **common)
+    qn, kn = ops.qk_norm_rope(q.to(dev), nk.to(dev), pro)
+    out2 = ops.paged_decode(qn, kd2, vd2, td, ld, new_k=kn, **common)
+    torch.cuda.synchronize()
+    assert torch.equal(out1, out2)
+    assert torch.equal(_codes(kd1), _codes(kd2)) and torch.equal(_codes(vd1), _codes(vd2))
+    rq, rk = oracle.qk_norm_rope(q, nk, pos, wq, wk, 1e-6, cs)
+    ek, ev = oracle.write_current_kv(kp, vp, table, lens_t, rk, nv, layout=ops.LAYOUT_NHD,
+                                     k_scale=ks, v_scale=vs)
+    ref = oracle.paged_decode(rq, ek, ev, table, lens_t, 128 ** -0.5, k_scale=ks, v_scale=vs)
+    assert _err(out1, ref) <= 2e-2
