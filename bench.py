@@ -801,9 +801,12 @@ def main():
     if args.only == "tts":
         print(json.dumps({"tts_decode": bench_tts(args, dev, stream)}))
         return
-    state_before = gpu_state()
+    # rocm-smi runs only in the default run: under a profiler its child
+    # process would start with the profiler's library loaded.
+    full = args.only == "all"
+    state_before = gpu_state() if full else {}
     dec = bench_decode(args, dev, stream)
-    state_after = gpu_state()
+    state_after = gpu_state() if full else {}
     if args.only == "fp8":
         print(json.dumps({"fp8_decode": bench_decode_fp8(args, dev, stream, dec)}))
         return
