@@ -169,3 +169,20 @@ def test_bench_library_is_apart_from_the_drop_in_library():
     assert rc == -1 and b"aligned" in blib.va_bench_last_error()
     rc = blib.va_bench_hbm_read(16, 16, 1, 7, 16, None)
     assert rc == -1 and b"mode" in blib.va_bench_last_error()
+
+
+def test_host_fast_path_module_loads_and_declines_cpu_tensors():
+    # csrc/host/fast_calls.cpp: built beside the library, handed its entry
+    # points, and it takes no call whose tensors are not on the named GPU.
+    fast = ops._fast_calls()
+    assert fast is not None
+    assert fast.NOT_TAKEN == ops._FAST_NOT_TAKEN
+    q = torch.zeros(2, 16, 128, dtype=torch.bfloat16)
+    pool = torch.zeros(4, 16, 8, 128, dtype=torch.bfloat16)
+    tables = torch.zeros(2, 1, dtype=torch.int32)
+    lens = torch.ones(2, dtype=torch.int32)
+    assert fast.paged_decode(q, pool, pool, tables, lens, q, None, None, None, None, False, False,
+                             16, 0.1, 0, 0, 0, 1.0, 1.0, 0, 0) == ops._FAST_NOT_TAKEN
+    cu = torch.tensor([0, 1, 2], dtype=torch.int32)
+    assert fast.varlen_attention(q, q, q, cu, cu, 1, 1, 0.1, True, None, None, None, None, q,
+                                 False, 0, 0) == ops._FAST_NOT_TAKEN

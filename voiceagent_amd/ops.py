@@ -283,6 +283,43 @@ class _current:
 
 _DECODE_ARGS_SIZE = ctypes.sizeof(N.DecodeArgs)
 _VARLEN_ARGS_SIZE = ctypes.sizeof(N.VarlenArgs)
+
+# Host fast path (csrc/host/fast_calls.cpp, the ``_fast_calls`` module next
+# to the library): the same checks and the same C-ABI call in C++, for the
+# common paged_decode / varlen_attention calls.  It launches nothing for a
+# call it does not take, and the Python path below then runs (and raises the
+# error for a bad argument), so results and errors are the same either way.
+_FAST_NOT_TAKEN = -1000
+_FAST = None
+_FAST_LOADED = False
+
+
+def _fast_calls():
+    """The fast-path module with the library's entry points handed to it, or
+    None when it is not built or does not load."""
+    global _FAST, _FAST_LOADED
+    if not _FAST_LOADED:
+        _FAST_LOADED = True
+        from voiceagent_amd.build import FAST_MODULE, FAST_PATH
+
+        if FAST_PATH.exists():
+            import importlib.util
+
+            try:
+                spec = importlib.util.spec_from_file_location(FAST_MODULE, FAST_PATH)
+                mod = importlib.util.module_from_spec(spec)
+                spec.loader.exec_module(mod)
+            except ImportError:
+                return None
+            lib = N.lib()
+
+            def addr(fn):
+                return ctypes.cast(fn, ctypes.c_void_p).value
+
+            mod.set_entries(addr(lib.va_paged_decode), addr(lib.va_paged_decode_workspace_bytes),
+                            addr(lib.va_varlen_attention))
+            _FAST = mod
+    return _FAST
 _POOLS: dict[tuple, N.KvPool] = {}  # pool descriptions by tensor identity and geometry
 
 
@@ -395,6 +432,24 @@ def paged_decode(
     An FP8 (float8_e4m3fn) pool is read as code * k_scale / v_scale, and the
     current row is stored into it quantised.
     """
+    fast = _FAST if _FAST_LOADED else _fast_calls()
+    if (fast is not None and valid_mask is None and prologue is None and not no_alloc and
+            layout in (LAYOUT_NHD, LAYOUT_HND)):
+        index = q.get_device()
+        if index >= 0 and index == torch.cuda.current_device():
+            if out is None:
+                out = torch.empty_like(q)
+            stream = _raw_stream(index)
+            rc = fast.paged_decode(
+                q, k_cache, v_cache, block_tables, lens, out, new_k, new_v, new_slots,
+                _WORKSPACES.get((index, stream)), lens_cumulative, layout == LAYOUT_HND,
+                int(max_seq_len), float(scale), int(split_tokens), int(key_limit),
+                int(table_read_width), float(k_scale), float(v_scale), index, stream)
+            if rc == 0:
+                return out
+            if _FAST_NOT_TAKEN < rc < 0:
+                N.check("va_paged_decode", rc)
+            # Not taken, or a workspace is needed first: the path below.
     device = _check_gpu(q, k_cache, v_cache, block_tables, lens, valid_mask, new_k, new_v,
                         new_slots, out)
     if prologue is not None:
@@ -512,6 +567,21 @@ def varlen_attention(
     must bound every k_len: the paged prefix is dequantised into a workspace
     first.
     """
+    fast = _FAST if _FAST_LOADED else _fast_calls()
+    if (fast is not None and layout in (LAYOUT_NHD, LAYOUT_HND) and
+            (k_cache is None or k_cache.dtype != FP8_KV_DTYPE)):
+        index = q.get_device()
+        if index >= 0 and index == torch.cuda.current_device():
+            if out is None:
+                out = torch.empty_like(q)
+            rc = fast.varlen_attention(
+                q, k, v, cu_seqlens_q, cu_seqlens_k, int(max_seqlen_q), int(max_seqlen_k),
+                float(scale), bool(causal), k_cache, v_cache, block_tables, slot_mapping, out,
+                layout == LAYOUT_HND, index, _raw_stream(index))
+            if rc == 0:
+                return out
+            if _FAST_NOT_TAKEN < rc < 0:
+                N.check("va_varlen_attention", rc)
     device = _check_gpu(q, k, v, cu_seqlens_q, cu_seqlens_k, k_cache, v_cache, block_tables,
                         slot_mapping, out)
     _require(q.dim() == 3, "q must be [total_q, num_heads, head_dim]")
