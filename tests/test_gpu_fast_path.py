@@ -2,8 +2,8 @@
 
 ops.paged_decode and ops.varlen_attention hand common calls to the C++
 module, which makes the wrappers' checks and the same C-ABI call; anything it
-does not take (a mask, a prologue, an FP8 prefill pool, a bad argument) runs
-the Python path.  Both paths launch the same kernels with the same
+does not take (a prologue, no_alloc, an FP8 prefill pool, a bad argument)
+runs the Python path.  Both paths launch the same kernels with the same
 arguments, so their outputs and pools agree bit for bit; the oracle check of
 every other GPU test runs through the fast path.
 """
@@ -32,10 +32,12 @@ def test_fast_module_is_loaded(dev):
     assert fast.NOT_TAKEN == ops._FAST_NOT_TAKEN
 
 
-@pytest.mark.parametrize("fused,cumulative,layout", [
-    (True, True, ops.LAYOUT_NHD), (False, False, ops.LAYOUT_NHD), (True, False, ops.LAYOUT_HND)])
+@pytest.mark.parametrize("fused,cumulative,layout,masked", [
+    (True, True, ops.LAYOUT_NHD, False), (False, False, ops.LAYOUT_NHD, True),
+    (True, False, ops.LAYOUT_HND, True)])
 @pytest.mark.parametrize("B", [4, 40])
-def test_decode_fast_and_python_paths_agree(dev, python_path, fused, cumulative, layout, B):
+def test_decode_fast_and_python_paths_agree(dev, python_path, fused, cumulative, layout, masked,
+                                            B):
     # B=4 splits the contexts (the workspace is allocated by the Python path
     # on the first call, then reused by the fast path); B=40 does not.
     lens = torch.randint(1, 700, (B,), generator=torch.Generator().manual_seed(B)).tolist()
@@ -47,6 +49,7 @@ def test_decode_fast_and_python_paths_agree(dev, python_path, fused, cumulative,
     nk = torch.randn(B, 8, 128, device=dev, generator=g).to(torch.bfloat16)
     nv = torch.randn(B, 8, 128, device=dev, generator=g).to(torch.bfloat16)
     lens_arg = b.cu_seqlens_k if cumulative else b.context_lens
+    valid = (torch.rand(B, max(lens) + 5, device=dev, generator=g) < 0.8) if masked else None
     pools = [(kp.clone(), vp.clone()) for _ in range(3)]
     outs = []
     for i, (k, v) in enumerate(pools):
@@ -54,7 +57,7 @@ def test_decode_fast_and_python_paths_agree(dev, python_path, fused, cumulative,
             python_path()
         outs.append(ops.paged_decode(b.q, k, v, b.block_tables, lens_arg,
                                      lens_cumulative=cumulative, max_seq_len=b.max_seq_len,
-                                     scale=b.scale, layout=layout,
+                                     scale=b.scale, layout=layout, valid_mask=valid,
                                      new_k=nk if fused else None, new_v=nv if fused else None))
     torch.cuda.synchronize()
     assert torch.equal(outs[0], outs[1]) and torch.equal(outs[0], outs[2])
@@ -62,7 +65,8 @@ def test_decode_fast_and_python_paths_agree(dev, python_path, fused, cumulative,
         assert torch.equal(k, pools[0][0]) and torch.equal(v, pools[0][1])
     if not fused:
         ref = oracle.paged_decode(b.q.cpu(), kp.cpu(), vp.cpu(), b.block_tables.cpu(),
-                                  b.context_lens.cpu(), b.scale, layout=layout)
+                                  b.context_lens.cpu(), b.scale, layout=layout,
+                                  valid_mask=None if valid is None else valid.cpu())
         assert (outs[0].float().cpu() - ref.float()).abs().max().item() <= 2e-2
 
 
@@ -93,5 +97,5 @@ def test_bad_arguments_raise_the_python_paths_errors(dev):
     cpu_q = b.q.cpu()
     # A tensor on another device than the one named: not taken, nothing launched.
     assert fast.paged_decode(cpu_q, b.k_pools[0], b.v_pools[0], b.block_tables,
-                             b.context_lens, b.q, None, None, None, None, False, False, 16, 0.1,
-                             0, 0, 0, 1.0, 1.0, b.q.get_device(), 0) == ops._FAST_NOT_TAKEN
+                             b.context_lens, b.q, None, None, None, None, None, False, False, 16,
+                             0.1, 0, 0, 0, 1.0, 1.0, b.q.get_device(), 0) == ops._FAST_NOT_TAKEN

@@ -102,14 +102,15 @@ void set_entries(int64_t decode, int64_t decode_ws, int64_t varlen) {
   g_varlen = reinterpret_cast<VarlenFn>(static_cast<intptr_t>(varlen));
 }
 
-// ops.paged_decode without key mask, prologue or no_alloc (layout_hnd picks
-// the pool layout).  0: launched; > 0: workspace bytes needed, nothing
+// ops.paged_decode without prologue or no_alloc (layout_hnd picks the pool
+// layout).  0: launched; > 0: workspace bytes needed, nothing
 // launched; VA_ERR_*: the library's status; kNotTaken: nothing done.
 int64_t paged_decode(const at::Tensor& q, const at::Tensor& kc, const at::Tensor& vc,
                      const at::Tensor& tables, const at::Tensor& lens, const at::Tensor& out,
                      const c10::optional<at::Tensor>& new_k,
                      const c10::optional<at::Tensor>& new_v,
                      const c10::optional<at::Tensor>& new_slots,
+                     const c10::optional<at::Tensor>& valid_mask,
                      const c10::optional<at::Tensor>& workspace, bool cumulative, bool layout_hnd,
                      int64_t max_seq_len, double scale, int64_t split_tokens, int64_t key_limit,
                      int64_t table_read_width, double k_scale, double v_scale, int64_t device,
@@ -176,6 +177,15 @@ int64_t paged_decode(const at::Tensor& q, const at::Tensor& kc, const at::Tensor
     if (!new_k.has_value() || !on(ns, device) || !index_vector(ns, B)) return kNotTaken;
     a.new_slots = ns.data_ptr();
     a.new_slots_dtype = index_code(ns.scalar_type());
+  }
+  if (valid_mask.has_value()) {
+    const at::Tensor& vm = *valid_mask;
+    if (!on(vm, device) || vm.dim() != 2 || vm.size(0) < B || vm.scalar_type() != at::kBool ||
+        vm.stride(1) != 1 || !fits_i32(vm.size(1)))
+      return kNotTaken;
+    a.valid_mask = static_cast<const uint8_t*>(vm.data_ptr());
+    a.valid_stride_seq = vm.stride(0);
+    a.valid_len = (int32_t)vm.size(1);
   }
   a.num_seqs = (int32_t)B;
   a.num_heads = (int32_t)hq;

@@ -433,7 +433,7 @@ def paged_decode(
     current row is stored into it quantised.
     """
     fast = _FAST if _FAST_LOADED else _fast_calls()
-    if (fast is not None and valid_mask is None and prologue is None and not no_alloc and
+    if (fast is not None and prologue is None and not no_alloc and
             layout in (LAYOUT_NHD, LAYOUT_HND)):
         index = q.get_device()
         if index >= 0 and index == torch.cuda.current_device():
@@ -442,7 +442,8 @@ def paged_decode(
             stream = _raw_stream(index)
             rc = fast.paged_decode(
                 q, k_cache, v_cache, block_tables, lens, out, new_k, new_v, new_slots,
-                _WORKSPACES.get((index, stream)), lens_cumulative, layout == LAYOUT_HND,
+                valid_mask, _WORKSPACES.get((index, stream)), lens_cumulative,
+                layout == LAYOUT_HND,
                 int(max_seq_len), float(scale), int(split_tokens), int(key_limit),
                 int(table_read_width), float(k_scale), float(v_scale), index, stream)
             if rc == 0:
