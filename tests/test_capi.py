@@ -181,8 +181,9 @@ def test_host_fast_path_module_loads_and_declines_cpu_tensors():
     pool = torch.zeros(4, 16, 8, 128, dtype=torch.bfloat16)
     tables = torch.zeros(2, 1, dtype=torch.int32)
     lens = torch.ones(2, dtype=torch.int32)
-    assert fast.paged_decode(q, pool, pool, tables, lens, q, None, None, None, None, None, False,
-                             False, 16, 0.1, 0, 0, 0, 1.0, 1.0, 0, 0) == ops._FAST_NOT_TAKEN
+    assert fast.paged_decode(q, pool, pool, tables, lens, q, None, None, None, None, None, None,
+                             0.0, None, None, None, False, False, 16, 0.1, 0, 0, 0, 1.0, 1.0, 0,
+                             0) == ops._FAST_NOT_TAKEN
     cu = torch.tensor([0, 1, 2], dtype=torch.int32)
     assert fast.varlen_attention(q, q, q, cu, cu, 1, 1, 0.1, True, None, None, None, None, q,
                                  False, 0, 0) == ops._FAST_NOT_TAKEN

@@ -2,8 +2,8 @@
 
 ops.paged_decode and ops.varlen_attention hand common calls to the C++
 module, which makes the wrappers' checks and the same C-ABI call; anything it
-does not take (a prologue, no_alloc, an FP8 prefill pool, a bad argument)
-runs the Python path.  Both paths launch the same kernels with the same
+does not take (no_alloc, an FP8 prefill pool, a bad argument) runs the
+Python path.  Both paths launch the same kernels with the same
 arguments, so their outputs and pools agree bit for bit; the oracle check of
 every other GPU test runs through the fast path.
 """
@@ -97,5 +97,39 @@ def test_bad_arguments_raise_the_python_paths_errors(dev):
     cpu_q = b.q.cpu()
     # A tensor on another device than the one named: not taken, nothing launched.
     assert fast.paged_decode(cpu_q, b.k_pools[0], b.v_pools[0], b.block_tables,
-                             b.context_lens, b.q, None, None, None, None, None, False, False, 16,
-                             0.1, 0, 0, 0, 1.0, 1.0, b.q.get_device(), 0) == ops._FAST_NOT_TAKEN
+                             b.context_lens, b.q, None, None, None, None, None, None, 0.0, None,
+                             None, None, False, False, 16, 0.1, 0, 0, 0, 1.0, 1.0,
+                             b.q.get_device(), 0) == ops._FAST_NOT_TAKEN
+
+
+def test_store_rope_and_prologue_decode_agree_on_both_paths(dev, python_path):
+    g = torch.Generator(device=dev).manual_seed(9)
+    n, hkv, d = 300, 8, 128
+    key = torch.randn(n, hkv, d, device=dev, generator=g).to(torch.bfloat16)
+    value = torch.randn(n, 2 * hkv, d, device=dev, generator=g).to(torch.bfloat16)[:, :hkv]
+    slots = torch.randperm(64 * 16, device=dev, generator=g)[:n].to(torch.int32)
+    slots[::7] = -1
+    q = torch.randn(n, 16, d, device=dev, generator=g).to(torch.bfloat16)
+    wq = (torch.rand(d, device=dev, generator=g) + 0.5).to(torch.bfloat16)
+    wk = (torch.rand(d, device=dev, generator=g) + 0.5).to(torch.bfloat16)
+    cs = oracle.rope_cache(d, 4096, 1_000_000.0).to(dev)
+    pos = torch.randint(0, 4096, (n,), device=dev, generator=g)
+    pro = ops.QKPrologue(wq, wk, 1e-6, cs, pos)
+    # decode with the fused prologue: 8 sequences over the stored pool
+    lens = torch.tensor([1, 30, 77, 100, 160, 200, 250, 299], dtype=torch.int32, device=dev)
+    table = torch.arange(8 * 19, dtype=torch.int32, device=dev).view(8, 19)
+    dpro = ops.QKPrologue(wq, wk, 1e-6, cs, (lens - 1).long())
+    res = []
+    for i in range(2):
+        if i == 1:
+            python_path()
+        kp = torch.zeros(256, 16, hkv, d, dtype=torch.bfloat16, device=dev)
+        vp = torch.zeros_like(kp)
+        ops.store_kvcache(key, value, kp, vp, slots)
+        qo, ko = ops.qk_norm_rope(q, key, pro)
+        out = ops.paged_decode(q[:8], kp, vp, table, lens, max_seq_len=300, scale=d ** -0.5,
+                               new_k=key[:8], new_v=value[:8], prologue=dpro)
+        res.append((kp, vp, qo, ko, out))
+    torch.cuda.synchronize()
+    for a, b in zip(*res):
+        assert torch.equal(a, b)

@@ -1,11 +1,12 @@
-// Host fast path of ops.paged_decode and ops.varlen_attention.
+// Host fast path of ops.paged_decode, ops.varlen_attention, ops.store_kvcache
+// and ops.qk_norm_rope.
 //
 // The Python wrappers validate every argument and fill a ctypes struct on
 // each call, about 10 us of host time, which an eager engine step pays once
 // per layer.  This module takes the same tensors through pybind11, makes the
-// same checks on them, fills the same va_decode_args / va_varlen_args and
-// calls the same entry points of libvoiceagent_attn.so (their addresses come
-// from ops.py, so nothing here links the library or any GPU runtime).
+// same checks on them, fills the same argument structs and calls the same
+// entry points of libvoiceagent_attn.so (their addresses come from ops.py,
+// so nothing here links the library or any GPU runtime).
 //
 // Only the common calls are taken, and only with arguments that pass every
 // check the Python wrapper makes.  Anything else returns kNotTaken without
@@ -25,10 +26,14 @@ namespace {
 using DecodeFn = int (*)(const va_decode_args*, void*);
 using DecodeWsFn = size_t (*)(const va_decode_args*);
 using VarlenFn = int (*)(const va_varlen_args*, void*);
+using StoreFn = int (*)(const va_store_args*, void*);
+using RopeFn = int (*)(const va_qk_norm_rope_args*, void*);
 
 DecodeFn g_decode = nullptr;
 DecodeWsFn g_decode_ws = nullptr;
 VarlenFn g_varlen = nullptr;
+StoreFn g_store = nullptr;
+RopeFn g_rope = nullptr;
 
 constexpr int64_t kNotTaken = -1000;
 
@@ -96,14 +101,44 @@ bool index_vector(const at::Tensor& t, int64_t n) {
   return t.dim() == 1 && t.numel() >= n && t.is_contiguous() && index_code(t.scalar_type()) >= 0;
 }
 
-void set_entries(int64_t decode, int64_t decode_ws, int64_t varlen) {
+void set_entries(int64_t decode, int64_t decode_ws, int64_t varlen, int64_t store,
+                 int64_t rope) {
   g_decode = reinterpret_cast<DecodeFn>(static_cast<intptr_t>(decode));
   g_decode_ws = reinterpret_cast<DecodeWsFn>(static_cast<intptr_t>(decode_ws));
   g_varlen = reinterpret_cast<VarlenFn>(static_cast<intptr_t>(varlen));
+  g_store = reinterpret_cast<StoreFn>(static_cast<intptr_t>(store));
+  g_rope = reinterpret_cast<RopeFn>(static_cast<intptr_t>(rope));
 }
 
-// ops.paged_decode without prologue or no_alloc (layout_hnd picks the pool
-// layout).  0: launched; > 0: workspace bytes needed, nothing
+// The prologue description of _prologue_struct(): [head_dim] weights of one
+// dtype, contiguous; an fp32 [max_position, (1,) head_dim] cos | sin table
+// with contiguous rows; at least n contiguous positions.
+bool fill_prologue(const at::Tensor& qw, const at::Tensor& kw, double eps, const at::Tensor& cs,
+                   const at::Tensor& pos, int64_t d, int64_t n, int64_t device,
+                   va_qk_prologue* pro) {
+  if (!on(qw, device) || !on(kw, device) || !on(cs, device) || !on(pos, device)) return false;
+  for (const at::Tensor* w : {&qw, &kw})
+    if (w->dim() != 1 || w->numel() != d || !w->is_contiguous()) return false;
+  if (qw.scalar_type() != kw.scalar_type() || dtype_code(qw.scalar_type()) < 0) return false;
+  if (cs.dim() == 3 && cs.size(1) != 1) return false;
+  if ((cs.dim() != 2 && cs.dim() != 3) || cs.size(cs.dim() - 1) != d ||
+      cs.scalar_type() != at::kFloat || cs.stride(cs.dim() - 1) != 1 || !fits_i32(cs.size(0)))
+    return false;
+  if (!index_vector(pos, n)) return false;
+  pro->q_norm_weight = qw.data_ptr();
+  pro->k_norm_weight = kw.data_ptr();
+  pro->weight_dtype = dtype_code(qw.scalar_type());
+  pro->eps = (float)eps;
+  pro->cos_sin_cache = static_cast<const float*>(cs.data_ptr());
+  pro->cos_sin_stride = cs.stride(0);
+  pro->max_position = (int32_t)cs.size(0);
+  pro->positions_dtype = index_code(pos.scalar_type());
+  pro->positions = pos.data_ptr();
+  return true;
+}
+
+// ops.paged_decode without no_alloc (layout_hnd picks the pool layout; the
+// prologue is given by its four tensors and eps, all or none).  0: launched; > 0: workspace bytes needed, nothing
 // launched; VA_ERR_*: the library's status; kNotTaken: nothing done.
 int64_t paged_decode(const at::Tensor& q, const at::Tensor& kc, const at::Tensor& vc,
                      const at::Tensor& tables, const at::Tensor& lens, const at::Tensor& out,
@@ -111,6 +146,10 @@ int64_t paged_decode(const at::Tensor& q, const at::Tensor& kc, const at::Tensor
                      const c10::optional<at::Tensor>& new_v,
                      const c10::optional<at::Tensor>& new_slots,
                      const c10::optional<at::Tensor>& valid_mask,
+                     const c10::optional<at::Tensor>& pro_q_w,
+                     const c10::optional<at::Tensor>& pro_k_w, double pro_eps,
+                     const c10::optional<at::Tensor>& pro_cos_sin,
+                     const c10::optional<at::Tensor>& pro_positions,
                      const c10::optional<at::Tensor>& workspace, bool cumulative, bool layout_hnd,
                      int64_t max_seq_len, double scale, int64_t split_tokens, int64_t key_limit,
                      int64_t table_read_width, double k_scale, double v_scale, int64_t device,
@@ -186,6 +225,14 @@ int64_t paged_decode(const at::Tensor& q, const at::Tensor& kc, const at::Tensor
     a.valid_mask = static_cast<const uint8_t*>(vm.data_ptr());
     a.valid_stride_seq = vm.stride(0);
     a.valid_len = (int32_t)vm.size(1);
+  }
+  va_qk_prologue pro{};
+  if (pro_q_w.has_value()) {
+    if (!pro_k_w.has_value() || !pro_cos_sin.has_value() || !pro_positions.has_value() ||
+        !fill_prologue(*pro_q_w, *pro_k_w, pro_eps, *pro_cos_sin, *pro_positions, d, B, device,
+                       &pro))
+      return kNotTaken;
+    a.prologue = &pro;
   }
   a.num_seqs = (int32_t)B;
   a.num_heads = (int32_t)hq;
@@ -309,12 +356,95 @@ int64_t varlen_attention(const at::Tensor& q, const c10::optional<at::Tensor>& k
   return g_varlen(&a, reinterpret_cast<void*>(static_cast<intptr_t>(stream)));
 }
 
+// ops.store_kvcache.  0: launched; VA_ERR_*: the library's status;
+// kNotTaken: nothing done.
+int64_t store_kvcache(const at::Tensor& key, const at::Tensor& value, const at::Tensor& kc,
+                      const at::Tensor& vc, const at::Tensor& slots, bool layout_hnd,
+                      double k_scale, double v_scale, int64_t device, int64_t stream) {
+  if (g_store == nullptr) return kNotTaken;
+  if (!on(key, device) || !on(value, device) || !on(kc, device) || !on(vc, device) ||
+      !on(slots, device))
+    return kNotTaken;
+  if (key.dim() != 3 || value.sizes() != key.sizes() || key.stride(2) != 1 ||
+      value.stride(2) != 1 || kc.dim() != 4)
+    return kNotTaken;
+  const int64_t hkv = layout_hnd ? kc.size(1) : kc.size(2);
+  if (key.size(1) != hkv || key.size(2) != kc.size(3)) return kNotTaken;
+  if (key.scalar_type() != value.scalar_type() || !pool_matches(kc, key.scalar_type()) ||
+      dtype_code(key.scalar_type()) < 0)
+    return kNotTaken;
+  if (slots.dim() != 1 || slots.numel() != key.size(0) || !slots.is_contiguous() ||
+      index_code(slots.scalar_type()) < 0 ||
+      !fits_i32(key.size(0)) || !fits_i32(hkv) || !fits_i32(key.size(2)))
+    return kNotTaken;
+  va_store_args a{};
+  a.struct_size = sizeof(a);
+  if (!fill_pool(kc, vc, layout_hnd, k_scale, v_scale, &a.pool)) return kNotTaken;
+  a.dtype = dtype_code(key.scalar_type());
+  a.key = key.data_ptr();
+  a.value = value.data_ptr();
+  a.key_stride_tok = key.stride(0);
+  a.key_stride_head = key.stride(1);
+  a.value_stride_tok = value.stride(0);
+  a.value_stride_head = value.stride(1);
+  a.slot_mapping = slots.data_ptr();
+  a.slot_dtype = index_code(slots.scalar_type());
+  a.num_tokens = (int32_t)key.size(0);
+  a.num_kv_heads = (int32_t)hkv;
+  a.head_dim = (int32_t)key.size(2);
+  return g_store(&a, reinterpret_cast<void*>(static_cast<intptr_t>(stream)));
+}
+
+// ops.qk_norm_rope with both outputs given.  0: launched; VA_ERR_*: the
+// library's status; kNotTaken: nothing done.
+int64_t qk_norm_rope(const at::Tensor& q, const at::Tensor& k, const at::Tensor& q_out,
+                     const at::Tensor& k_out, const at::Tensor& q_w, const at::Tensor& k_w,
+                     double eps, const at::Tensor& cos_sin, const at::Tensor& positions,
+                     int64_t device, int64_t stream) {
+  if (g_rope == nullptr) return kNotTaken;
+  if (!on(q, device) || !on(k, device) || !on(q_out, device) || !on(k_out, device))
+    return kNotTaken;
+  if (q.dim() != 3 || k.dim() != 3 || q.size(0) != k.size(0) || q.size(2) != k.size(2) ||
+      q.scalar_type() != k.scalar_type() || q.stride(2) != 1 || k.stride(2) != 1)
+    return kNotTaken;
+  if (q_out.sizes() != q.sizes() || q_out.scalar_type() != q.scalar_type() ||
+      k_out.sizes() != k.sizes() || k_out.scalar_type() != k.scalar_type() ||
+      q_out.stride(2) != 1 || k_out.stride(2) != 1 || dtype_code(q.scalar_type()) < 0)
+    return kNotTaken;
+  const int64_t T = q.size(0), hq = q.size(1), hkv = k.size(1), d = q.size(2);
+  if (!fits_i32(T) || !fits_i32(hq) || !fits_i32(hkv) || !fits_i32(d)) return kNotTaken;
+  va_qk_norm_rope_args a{};
+  a.struct_size = sizeof(a);
+  if (!fill_prologue(q_w, k_w, eps, cos_sin, positions, d, T, device, &a.prologue))
+    return kNotTaken;
+  a.dtype = dtype_code(q.scalar_type());
+  a.q = q.data_ptr();
+  a.q_stride_tok = q.stride(0);
+  a.q_stride_head = q.stride(1);
+  a.k = k.data_ptr();
+  a.k_stride_tok = k.stride(0);
+  a.k_stride_head = k.stride(1);
+  a.q_out = q_out.data_ptr();
+  a.q_out_stride_tok = q_out.stride(0);
+  a.q_out_stride_head = q_out.stride(1);
+  a.k_out = k_out.data_ptr();
+  a.k_out_stride_tok = k_out.stride(0);
+  a.k_out_stride_head = k_out.stride(1);
+  a.num_tokens = (int32_t)T;
+  a.num_heads = (int32_t)hq;
+  a.num_kv_heads = (int32_t)hkv;
+  a.head_dim = (int32_t)d;
+  return g_rope(&a, reinterpret_cast<void*>(static_cast<intptr_t>(stream)));
+}
+
 }  // namespace
 
 PYBIND11_MODULE(_fast_calls, m) {
-  m.doc() = "Host fast path of ops.paged_decode and ops.varlen_attention";
+  m.doc() = "Host fast path of the ops wrappers";
   m.attr("NOT_TAKEN") = kNotTaken;
   m.def("set_entries", &set_entries);
   m.def("paged_decode", &paged_decode);
   m.def("varlen_attention", &varlen_attention);
+  m.def("store_kvcache", &store_kvcache);
+  m.def("qk_norm_rope", &qk_norm_rope);
 }

@@ -127,6 +127,17 @@ def store_kvcache(
 ) -> None:
     """Write key[i] / value[i] ([N, Hkv, D]) to pool slot slot_mapping[i]; -1 skips.
     An FP8 pool receives e4m3 codes of key / k_scale and value / v_scale."""
+    fast = _FAST if _FAST_LOADED else _fast_calls()
+    if fast is not None and layout in (LAYOUT_NHD, LAYOUT_HND):
+        index = key.get_device()
+        if index >= 0 and index == torch.cuda.current_device():
+            rc = fast.store_kvcache(key, value, k_cache, v_cache, slot_mapping,
+                                    layout == LAYOUT_HND, float(k_scale), float(v_scale), index,
+                                    _raw_stream(index))
+            if rc == 0:
+                return
+            if _FAST_NOT_TAKEN < rc < 0:
+                N.check("va_store_kvcache", rc)
     device = _check_gpu(key, value, k_cache, v_cache, slot_mapping)
     _require(key.dim() == 3 and value.shape == key.shape, "key/value must be [N, Hkv, D]")
     _rows(key, "key")
@@ -137,6 +148,7 @@ def store_kvcache(
              "key/value/pool dtypes must match (or the pool be FP8 for 16-bit rows)")
     _require(slot_mapping.dim() == 1 and slot_mapping.numel() == key.shape[0],
              "slot_mapping must have one entry per token")
+    _require(slot_mapping.is_contiguous(), "slot_mapping must be contiguous")
     args = N.new_args(N.StoreArgs)
     args.dtype = _dtype_code(key)
     args.key = key.data_ptr()
@@ -208,6 +220,22 @@ def qk_norm_rope(
     """Apply the Qwen3 q/k prologue to q [T, Hq, D] and k [T, Hkv, D] (one
     position per token).  Outputs are allocated contiguous when not given and
     may be q / k themselves (in place)."""
+    fast = _FAST if _FAST_LOADED else _fast_calls()
+    if fast is not None:
+        index = q.get_device()
+        if index >= 0 and index == torch.cuda.current_device():
+            if q_out is None:
+                q_out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+            if k_out is None:
+                k_out = torch.empty(k.shape, dtype=k.dtype, device=k.device)
+            rc = fast.qk_norm_rope(q, k, q_out, k_out, prologue.q_norm_weight,
+                                   prologue.k_norm_weight, float(prologue.eps),
+                                   prologue.cos_sin_cache, prologue.positions, index,
+                                   _raw_stream(index))
+            if rc == 0:
+                return q_out, k_out
+            if _FAST_NOT_TAKEN < rc < 0:
+                N.check("va_qk_norm_rope", rc)
     device = _check_gpu(q, k, q_out, k_out, prologue.q_norm_weight, prologue.k_norm_weight,
                         prologue.cos_sin_cache, prologue.positions)
     _require(q.dim() == 3 and k.dim() == 3 and q.shape[0] == k.shape[0] and
@@ -286,7 +314,7 @@ _VARLEN_ARGS_SIZE = ctypes.sizeof(N.VarlenArgs)
 
 # Host fast path (csrc/host/fast_calls.cpp, the ``_fast_calls`` module next
 # to the library): the same checks and the same C-ABI call in C++, for the
-# common paged_decode / varlen_attention calls.  It launches nothing for a
+# common paged_decode / varlen_attention / store_kvcache / qk_norm_rope calls.  It launches nothing for a
 # call it does not take, and the Python path below then runs (and raises the
 # error for a bad argument), so results and errors are the same either way.
 _FAST_NOT_TAKEN = -1000
@@ -317,7 +345,8 @@ def _fast_calls():
                 return ctypes.cast(fn, ctypes.c_void_p).value
 
             mod.set_entries(addr(lib.va_paged_decode), addr(lib.va_paged_decode_workspace_bytes),
-                            addr(lib.va_varlen_attention))
+                            addr(lib.va_varlen_attention), addr(lib.va_store_kvcache),
+                            addr(lib.va_qk_norm_rope))
             _FAST = mod
     return _FAST
 _POOLS: dict[tuple, N.KvPool] = {}  # pool descriptions by tensor identity and geometry
@@ -433,17 +462,21 @@ def paged_decode(
     current row is stored into it quantised.
     """
     fast = _FAST if _FAST_LOADED else _fast_calls()
-    if (fast is not None and prologue is None and not no_alloc and
-            layout in (LAYOUT_NHD, LAYOUT_HND)):
+    if fast is not None and not no_alloc and layout in (LAYOUT_NHD, LAYOUT_HND):
         index = q.get_device()
         if index >= 0 and index == torch.cuda.current_device():
             if out is None:
                 out = torch.empty_like(q)
             stream = _raw_stream(index)
+            pro = prologue
             rc = fast.paged_decode(
                 q, k_cache, v_cache, block_tables, lens, out, new_k, new_v, new_slots,
-                valid_mask, _WORKSPACES.get((index, stream)), lens_cumulative,
-                layout == LAYOUT_HND,
+                valid_mask, None if pro is None else pro.q_norm_weight,
+                None if pro is None else pro.k_norm_weight,
+                0.0 if pro is None else float(pro.eps),
+                None if pro is None else pro.cos_sin_cache,
+                None if pro is None else pro.positions, _WORKSPACES.get((index, stream)),
+                lens_cumulative, layout == LAYOUT_HND,
                 int(max_seq_len), float(scale), int(split_tokens), int(key_limit),
                 int(table_read_width), float(k_scale), float(v_scale), index, stream)
             if rc == 0:
