@@ -58,8 +58,10 @@ bool fits_i32(int64_t x) {
   return x >= std::numeric_limits<int32_t>::min() && x <= std::numeric_limits<int32_t>::max();
 }
 
-// A GPU tensor on `device`.
-bool on(const at::Tensor& t, int64_t device) { return t.is_cuda() && t.get_device() == device; }
+// A dense GPU tensor on `device`.
+bool on(const at::Tensor& t, int64_t device) {
+  return t.defined() && t.layout() == at::kStrided && t.is_cuda() && t.get_device() == device;
+}
 
 // The pool description of kv_pool(): 4-D NHD [blocks, block_size, Hkv, D] or
 // HND [blocks, Hkv, block_size, D], k and v alike, rows contiguous; an FP8
