@@ -140,8 +140,9 @@ bool fill_prologue(const at::Tensor& qw, const at::Tensor& kw, double eps, const
 }
 
 // ops.paged_decode without no_alloc (layout_hnd picks the pool layout; the
-// prologue is given by its four tensors and eps, all or none).  0: launched; > 0: workspace bytes needed, nothing
-// launched; VA_ERR_*: the library's status; kNotTaken: nothing done.
+// prologue is given by its four tensors and eps, all or none).  0: launched;
+// > 0: workspace bytes needed, nothing launched; VA_ERR_*: the library's
+// status; kNotTaken: nothing done.
 int64_t paged_decode(const at::Tensor& q, const at::Tensor& kc, const at::Tensor& vc,
                      const at::Tensor& tables, const at::Tensor& lens, const at::Tensor& out,
                      const c10::optional<at::Tensor>& new_k,
