@@ -3,9 +3,10 @@
 // with its key_valid_mask.  The general kernel in paged_decode_kernel.h
 // covers the rest.
 //
-// Same semantics, grid and partial/merge protocol as paged_decode_kernel:
-// the grid is (sequence, kv head, partition); a workgroup owns P consecutive
-// tokens of one (sequence, kv head) pair and all G query heads of its group.
+// Same semantics and partial/merge protocol as paged_decode_kernel; the grid
+// is (kv head, sequence, partition) here (see `h` below).  A workgroup owns P
+// consecutive tokens of one (sequence, kv head) pair and all G query heads
+// of its group.
 //
 // Work decomposition.  A workgroup is W wave64s (8, two per SIMD, for head
 // dims up to 128; 4 for 256).  The partition's 16-token tiles go round robin
@@ -169,8 +170,13 @@ __global__ __launch_bounds__(MfmaDecodeShape<D>::W * 64, 1) void paged_decode_mf
   __shared__ __align__(16) char s_q[Q_B];
   __shared__ __align__(16) char s_mrg[kOwnMerge ? MERGE_B : 16];
 
-  const int b = blockIdx.x;
-  const int h = blockIdx.y;
+  // Grid (kv head, sequence, partition), kv head fastest: workgroup i runs
+  // on XCD i % 8, so each XCD takes the same kv heads of every sequence and
+  // reads an equal share of the step's bytes however the lengths vary
+  // (sequence-major, an XCD held all heads of a few sequences: config 2
+  // 13.33-13.42 us against 12.95-12.99).
+  const int b = blockIdx.y;
+  const int h = blockIdx.x;
   const int part = blockIdx.z;
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
@@ -692,18 +698,19 @@ __global__ __launch_bounds__(MfmaDecodeShape<D>::W * 64, 1) void paged_decode_mf
 template <typename ET, int D, int G, bool kF8>
 static void launch_decode_mfma(const DecodeParams& p, dim3 grid, hipStream_t s) {
   constexpr int NT = MfmaDecodeShape<D>::W * 64;
+  const dim3 hgrid(grid.y, grid.x, grid.z);  // (kv head, sequence, partition)
   const bool mask = p.valid != nullptr && p.valid_len > 0;
   if (p.has_pro && mask)
-    hipLaunchKernelGGL((paged_decode_mfma_kernel<ET, D, G, true, true, kF8>), grid, dim3(NT), 0,
+    hipLaunchKernelGGL((paged_decode_mfma_kernel<ET, D, G, true, true, kF8>), hgrid, dim3(NT), 0,
                        s, p);
   else if (p.has_pro)
-    hipLaunchKernelGGL((paged_decode_mfma_kernel<ET, D, G, true, false, kF8>), grid, dim3(NT), 0,
+    hipLaunchKernelGGL((paged_decode_mfma_kernel<ET, D, G, true, false, kF8>), hgrid, dim3(NT), 0,
                        s, p);
   else if (mask)
-    hipLaunchKernelGGL((paged_decode_mfma_kernel<ET, D, G, false, true, kF8>), grid, dim3(NT), 0,
+    hipLaunchKernelGGL((paged_decode_mfma_kernel<ET, D, G, false, true, kF8>), hgrid, dim3(NT), 0,
                        s, p);
   else
-    hipLaunchKernelGGL((paged_decode_mfma_kernel<ET, D, G, false, false, kF8>), grid, dim3(NT), 0,
+    hipLaunchKernelGGL((paged_decode_mfma_kernel<ET, D, G, false, false, kF8>), hgrid, dim3(NT), 0,
                        s, p);
   if (p.max_parts > 1)
     hipLaunchKernelGGL((paged_decode_merge_kernel<ET, D, G, kF8 ? 1 : 0>), dim3(grid.y, grid.x),
