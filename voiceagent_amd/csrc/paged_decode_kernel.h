@@ -204,8 +204,10 @@ __global__ __launch_bounds__((DecodeShape<ET, D, G>::NW * 64),
   // Partition-major grid: every sequence's first partition is dispatched
   // before any second one, so workgroups past the end of short contexts
   // (which exit after reading the length) queue behind the live ones.
-  const int b = blockIdx.x;
-  const int h = blockIdx.y;
+  // Grid (kv head, sequence, partition), as the matrix-core kernel's: each
+  // XCD takes the same kv heads of every sequence.
+  const int b = blockIdx.y;
+  const int h = blockIdx.x;
   const int part = blockIdx.z;
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
@@ -728,11 +730,12 @@ __global__ __launch_bounds__(256) void paged_decode_merge_kernel(DecodeParams p)
 // ------------------------------------------------------------- launching
 template <typename ET, int D, int G, bool kProlog>
 static void launch_decode_kernel(const DecodeParams& p, dim3 grid, hipStream_t s) {
+  const dim3 hgrid(grid.y, grid.x, grid.z);  // (kv head, sequence, partition)
   if (p.block_is_chunk_aligned)
-    hipLaunchKernelGGL((paged_decode_kernel<ET, D, G, true, kProlog>), grid,
+    hipLaunchKernelGGL((paged_decode_kernel<ET, D, G, true, kProlog>), hgrid,
                        dim3(DecodeShape<ET, D, G>::NW * 64), 0, s, p);
   else
-    hipLaunchKernelGGL((paged_decode_kernel<ET, D, G, false, kProlog>), grid,
+    hipLaunchKernelGGL((paged_decode_kernel<ET, D, G, false, kProlog>), hgrid,
                        dim3(DecodeShape<ET, D, G>::NW * 64), 0, s, p);
 }
 
