@@ -280,6 +280,8 @@ def bench_lib():
         lib.va_bench_hbm_copy.restype = ctypes.c_int
         lib.va_bench_hbm_copy.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p,
                                           ctypes.c_size_t, ctypes.c_int, ctypes.c_void_p]
+        lib.va_bench_empty.restype = ctypes.c_int
+        lib.va_bench_empty.argtypes = [ctypes.c_int, ctypes.c_void_p]
         lib.va_bench_last_error.restype = ctypes.c_char_p
         lib.va_bench_last_error.argtypes = []
         _BENCH_LIB = lib
@@ -310,6 +312,31 @@ def hbm_copy(src: torch.Tensor, dst: torch.Tensor, workgroups: int) -> None:
                                        int(workgroups), torch.cuda.current_stream().cuda_stream)
     if rc != 0:
         raise ValueError(bench_lib().va_bench_last_error().decode())
+
+
+def empty_launch(workgroups: int) -> None:
+    """One launch of a kernel that does nothing over `workgroups` 512-lane
+    workgroups (va_bench_empty)."""
+    rc = bench_lib().va_bench_empty(int(workgroups), torch.cuda.current_stream().cuda_stream)
+    if rc != 0:
+        raise ValueError(bench_lib().va_bench_last_error().decode())
+
+
+def launch_floor(args, stream) -> dict:
+    """Fixed cost of a launch: 28 launches of an empty kernel per graph
+    replay, as the attention legs replay 28 layers, at the decode's grid
+    (256 workgroups) and at 2048."""
+    table = {}
+    for wgs in (256, 2048):
+        def step(wgs=wgs):
+            for _ in range(workloads.LAYERS):
+                empty_launch(wgs)
+
+        ms, _ = timed_graph(step, args.steps, args.warmup, stream)
+        table[wgs] = ms * 1000.0 / workloads.LAYERS
+    log("[launch floor] empty kernel, 28 launches per graph replay: "
+        + ", ".join(f"{w} workgroups {t:.2f}" for w, t in table.items()) + " us/launch")
+    return {str(w): round(t, 2) for w, t in table.items()}
 
 
 def copy_floor(name: str, read_bytes: int, write_bytes: int, launches: int, args, dev,
@@ -347,7 +374,8 @@ def bench_floor(args, dev, stream):
     graph replay on distinct windows of a 1.3 GB buffer (cold, past the 256 MB
     MALL), through three load paths (plain loads, non-temporal loads, the
     decode's non-temporal LDS DMA) at several grid sizes; the fastest
-    (path, grid) is reported."""
+    (path, grid) is reported.  Also the varlen launches' read + write floors
+    and the fixed cost of an empty launch."""
     nbytes = decode_launch_bytes(workloads.cfg2_lens(0)) // 16 * 16
     layers = workloads.LAYERS
     stride = (nbytes + 65535) // 65536 * 65536
@@ -382,7 +410,9 @@ def bench_floor(args, dev, stream):
     copies = {"prefill_cfg3": copy_floor("prefill cfg3", pre_r, pre_w, layers, args, dev, stream),
               "encoder_cfg4": copy_floor("encoder cfg4", enc_all * 3 // 4, enc_all // 4, 18,
                                          args, dev, stream)}
+    empty = launch_floor(args, stream)
     return {"us_per_launch": round(us, 2), "gbs": round(gbs, 1), "copy": copies,
+            "empty_launch_us": empty,
             "frac": round(gbs / HBM_PEAK_GBS, 4), "bytes": nbytes, "mode": mode,
             "workgroups": wgs,
             "us_by_mode_grid": {f"{m}/{w}": round(t, 2) for (m, w), t in table.items()},

@@ -38,6 +38,13 @@ int va_bench_hbm_read(const void* src, size_t bytes, int workgroups, int mode, v
 int va_bench_hbm_copy(const void* src, size_t read_bytes, void* dst, size_t write_bytes,
                       int workgroups, void* stream);
 
+/* One launch of `workgroups` 512-lane workgroups whose kernel does nothing:
+ * the fixed cost of a launch of that grid (dispatch, completion and the
+ * caches' hand-over to the next kernel), which every attention launch pays
+ * before it moves a byte.  Returns 0, or -1 on a bad argument
+ * (va_bench_last_error()). */
+int va_bench_empty(int workgroups, void* stream);
+
 const char* va_bench_last_error(void);
 
 #ifdef __cplusplus

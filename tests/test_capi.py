@@ -169,6 +169,8 @@ def test_bench_library_is_apart_from_the_drop_in_library():
     assert rc == -1 and b"aligned" in blib.va_bench_last_error()
     rc = blib.va_bench_hbm_read(16, 16, 1, 7, 16, None)
     assert rc == -1 and b"mode" in blib.va_bench_last_error()
+    rc = blib.va_bench_empty(0, None)  # no workgroups: rejected before any launch
+    assert rc == -1 and b"workgroups" in blib.va_bench_last_error()
 
 
 def test_host_fast_path_module_loads_and_declines_cpu_tensors():

@@ -20,7 +20,8 @@
 //
 // va_bench_hbm_copy is the mixed floor for the varlen launches: it reads and
 // writes given byte counts in one launch (for prefill, its q, k, v reads and
-// its output and stored-row writes).
+// its output and stored-row writes).  va_bench_empty launches a kernel that
+// does nothing: the fixed cost of a launch of a given grid.
 #include <stdarg.h>
 #include <stdio.h>
 
@@ -122,6 +123,9 @@ __global__ __launch_bounds__(kProbeThreads) void hbm_copy_probe_kernel(
   }
 }
 
+// Does nothing: the fixed cost of a launch of its grid.
+__global__ __launch_bounds__(kProbeThreads) void empty_probe_kernel() {}
+
 }  // namespace
 }  // namespace va
 
@@ -173,6 +177,17 @@ extern "C" int va_bench_hbm_read(const void* src, size_t bytes, int workgroups, 
                        reinterpret_cast<const char*>(src), nvec, per_wg);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return bench_fail("va_bench_hbm_read: launch failed: %s", hipGetErrorString(e));
+  return 0;
+}
+
+extern "C" int va_bench_empty(int workgroups, void* stream) {
+  using namespace va;
+  if (workgroups < 1 || workgroups > 65536)
+    return bench_fail("va_bench_empty: workgroups must be in [1, 65536]");
+  hipLaunchKernelGGL(empty_probe_kernel, dim3((unsigned)workgroups), dim3(kProbeThreads), 0,
+                     (hipStream_t)stream);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return bench_fail("va_bench_empty: launch failed: %s", hipGetErrorString(e));
   return 0;
 }
 
