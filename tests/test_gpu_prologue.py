@@ -47,11 +47,16 @@ def _prologue_inputs(T, hq, hkv, d, dtype, seed, max_pos=4096):
     return q, k, wq, wk, pos, cs
 
 
-@pytest.mark.parametrize("dtype,hq,hkv,d", [
-    (torch.bfloat16, 16, 8, 128), (torch.float16, 16, 8, 128), (torch.float32, 16, 8, 128),
-    (torch.bfloat16, 14, 14, 64), (torch.bfloat16, 4, 1, 256)])
-def test_qk_norm_rope_matches_oracle(dev, dtype, hq, hkv, d):
-    T = 257
+# T = 257 spreads each token's rows over several waves; T = 4096 takes one
+# wave per token, with 72 rows in three chunks of loads (Hq 64) or a row group
+# holding both query and key rows (Hq 6).
+@pytest.mark.parametrize("dtype,hq,hkv,d,T", [
+    (torch.bfloat16, 16, 8, 128, 257), (torch.float16, 16, 8, 128, 257),
+    (torch.float32, 16, 8, 128, 257), (torch.bfloat16, 14, 14, 64, 257),
+    (torch.bfloat16, 4, 1, 256, 257), (torch.bfloat16, 16, 8, 128, 4096),
+    (torch.bfloat16, 64, 8, 128, 4096), (torch.bfloat16, 6, 2, 128, 4096),
+    (torch.float32, 6, 2, 64, 4096)])
+def test_qk_norm_rope_matches_oracle(dev, dtype, hq, hkv, d, T):
     q, k, wq, wk, pos, cs = _prologue_inputs(T, hq, hkv, d, dtype, seed=d + hq)
     print(f"qk_norm_rope {dtype} T={T} Hq={hq} Hkv={hkv} D={d}", flush=True)
     pro = ops.QKPrologue(wq.to(dev), wk.to(dev), 1e-6, cs.to(dev), pos.to(dev))

@@ -319,7 +319,7 @@ __global__ __launch_bounds__((DecodeShape<ET, D, G>::NW * 64),
       float w[E], x[E];
       convert_weights<E>(pro_wk, p.pro.w_dtype, w);
       ET::unpack(kw, x);
-      qk_prologue<ET, LPR, E>(x, w, p.pro.eps, D, pro_c, pro_s, col < LPR / 2);
+      qk_prologue<ET, LPR, E>(x, w, p.pro.eps, D, pro_c, pro_s);
       kw = ET::pack(x);
     }
     if (rg == 0) store_detached_row(p, h, table_row, Lr, col_new, new_slot, col * 16, kw, vcur);
@@ -451,21 +451,20 @@ __global__ __launch_bounds__((DecodeShape<ET, D, G>::NW * 64),
   // trip overlaps that of the K/V rows.
   auto prepare_query = [&]() {
     if constexpr (kProlog) {
-      const bool first_half = col < LPR / 2;
-      float w[E];
+        float w[E];
       convert_weights<E>(pro_wq, p.pro.w_dtype, w);
 #pragma unroll
       for (int g = 0; g < G; ++g) {
         float x[E];
         ET::unpack(qv[g], x);
-        qk_prologue<ET, LPR, E>(x, w, p.pro.eps, D, pro_c, pro_s, first_half);
+        qk_prologue<ET, LPR, E>(x, w, p.pro.eps, D, pro_c, pro_s);
         qv[g] = ET::pack(x);
       }
       if (new_tok >= 0) {
         convert_weights<E>(pro_wk, p.pro.w_dtype, w);
         float x[E];
         ET::unpack(kcur, x);
-        qk_prologue<ET, LPR, E>(x, w, p.pro.eps, D, pro_c, pro_s, first_half);
+        qk_prologue<ET, LPR, E>(x, w, p.pro.eps, D, pro_c, pro_s);
         kcur = ET::pack(x);
       }
     }

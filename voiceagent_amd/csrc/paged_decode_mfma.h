@@ -420,21 +420,20 @@ __global__ __launch_bounds__(MfmaDecodeShape<D>::W * 64, 1) void paged_decode_mf
   // ---- prologue (Qwen3 q/k RMSNorm + RoPE) in the row layout, then the
   // query rows go through LDS into the B-operand layout ----
   if constexpr (kProlog) {
-    const bool first_half = col < LPR / 2;
     float w[E];
     convert_weights<E>(pro_wq, p.pro.w_dtype, w);
 #pragma unroll
     for (int k = 0; k < QROWS; ++k) {
       float x[E];
       ET::unpack(qrow[k], x);
-      qk_prologue<ET, LPR, E>(x, w, p.pro.eps, D, pro_c, pro_s, first_half);
+      qk_prologue<ET, LPR, E>(x, w, p.pro.eps, D, pro_c, pro_s);
       qrow[k] = ET::pack(x);
     }
     if (new_tok >= 0 || (detached && part == 0 && wave == 0)) {
       convert_weights<E>(pro_wk, p.pro.w_dtype, w);
       float x[E];
       ET::unpack(kcur, x);
-      qk_prologue<ET, LPR, E>(x, w, p.pro.eps, D, pro_c, pro_s, first_half);
+      qk_prologue<ET, LPR, E>(x, w, p.pro.eps, D, pro_c, pro_s);
       kcur = ET::pack(x);
     }
 #pragma unroll

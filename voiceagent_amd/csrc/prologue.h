@@ -8,7 +8,8 @@
 // lanes; the rotary partner of element i (i +- D/2) sits in lane c ^ (LPR/2)
 // at the same slot.  Every rounding the reference performs in the element
 // type is reproduced (to_dtype after the normalisation, after the weight,
-// after the rotation), and products and sums are rounded separately.
+// and, by the caller's pack, after the rotation), and the rotation's products
+// are rounded before their sum.
 #pragma once
 
 #include <type_traits>
@@ -29,16 +30,30 @@ struct PrologueParams {
   const void* pos;
 };
 
-// x rounded to the element type (nearest even) and widened back to float.
-// bf16 uses gfx950's v_cvt_pk_bf16_f32.
-template <typename ET>
-__device__ inline float round_to(float x) {
-  if constexpr (ET::kBytes == 4) {
-    return x;
-  } else if constexpr (ET::kIsBF16) {
-    return (float)(__bf16)x;
-  } else {
-    return (float)(_Float16)x;
+// Every element of x rounded to the element type (nearest even) and widened
+// back to float, two at a time (one packed conversion per pair; bf16 through
+// gfx950's v_cvt_pk_bf16_f32).
+template <typename ET, int E>
+__device__ inline void round_to(float (&x)[E]) {
+  static_assert(E % 2 == 0, "pairs");
+  if constexpr (ET::kBytes == 2) {
+#pragma unroll
+    for (int i = 0; i < E / 2; ++i) {
+      if constexpr (ET::kIsBF16) {
+        bf16x2_t v;
+        v.x = (__bf16)x[2 * i];
+        v.y = (__bf16)x[2 * i + 1];
+        const uint32_t u = __builtin_bit_cast(uint32_t, v);
+        x[2 * i] = __uint_as_float(u << 16);
+        x[2 * i + 1] = __uint_as_float(u & 0xffff0000u);
+      } else {
+        f16x2_t v;
+        v.x = (_Float16)x[2 * i];
+        v.y = (_Float16)x[2 * i + 1];
+        x[2 * i] = (float)v.x;
+        x[2 * i + 1] = (float)v.y;
+      }
+    }
   }
 }
 
@@ -48,8 +63,10 @@ __device__ inline float round_to(float x) {
 template <int LPR>
 __device__ inline float rotary_partner(float x) {
   if constexpr (LPR == 16) {
-    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x128 /* row_ror:8 */,
-                                                      0xF, 0xF, false));
+    // Every lane of the row has a source, so no fallback value is needed
+    // (update_dpp would first move one into the destination).
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x128 /* row_ror:8 */, 0xF,
+                                                   0xF, false));
   } else {
     return __shfl_xor(x, LPR / 2, 64);
   }
@@ -105,37 +122,51 @@ __device__ inline void convert_weights(const WeightRaw<E>& r, int dtype, float (
 }
 
 // The cos / sin factors of this lane's slice at `pos` (col = lane's index in
-// its row of LPR lanes).
+// its row of LPR lanes).  The sin factors of the row's first half come
+// negated: element i < D/2 rotates to x_i cos - x_(i+D/2) sin, and
+// x cos + p (-sin) rounds exactly as x cos - p sin does.
 template <int E, int LPR>
 __device__ inline void load_rotary(const PrologueParams& pp, int64_t pos, int col, int D,
                                    float (&c)[E], float (&s)[E]) {
   const float* row = pp.cs + pos * pp.cs_stride;
   const int i0 = (col % (LPR / 2)) * E;
+  const bool first_half = col < LPR / 2;
 #pragma unroll
   for (int e = 0; e < E; ++e) {
     c[e] = row[i0 + e];
-    s[e] = row[D / 2 + i0 + e];
+    const float sv = row[D / 2 + i0 + e];
+    s[e] = first_half ? -sv : sv;
   }
 }
 
-// In place on the lane's E floats of one row: normalise, weight, rotate.
+// In place on the lane's E floats of one row: normalise, weight, rotate, with
+// s from load_rotary.  The result is left unrounded: every caller packs it
+// to the element type, which is the reference's last rounding.
 template <typename ET, int LPR, int E>
 __device__ inline void qk_prologue(float (&x)[E], const float (&w)[E], float eps, int D,
-                                   const float (&c)[E], const float (&s)[E], bool first_half) {
+                                   const float (&c)[E], const float (&s)[E]) {
+  // The sum of squares is reduced in another order than the reference's
+  // mean, so it is not bit-exact either way; it takes fused multiply-adds.
   float ss = 0.f;
 #pragma unroll
-  for (int e = 0; e < E; ++e) ss = __fadd_rn(ss, __fmul_rn(x[e], x[e]));
+  for (int e = 0; e < E; ++e) ss = fmaf(x[e], x[e], ss);
   ss = group_sum<LPR>(ss);
   const float r = 1.0f / sqrtf(__fadd_rn(ss / (float)D, eps));
 #pragma unroll
-  for (int e = 0; e < E; ++e) x[e] = round_to<ET>(__fmul_rn(round_to<ET>(__fmul_rn(x[e], r)), w[e]));
+  for (int e = 0; e < E; ++e) x[e] = __fmul_rn(x[e], r);
+  round_to<ET>(x);
+#pragma unroll
+  for (int e = 0; e < E; ++e) x[e] = __fmul_rn(x[e], w[e]);
+  round_to<ET>(x);
   float pt[E];
 #pragma unroll
   for (int e = 0; e < E; ++e) pt[e] = rotary_partner<LPR>(x[e]);
+  {
+    // x cos and p sin rounded apart before their sum, as the reference's
+    // elementwise ops round them: no fused multiply-add here.
+#pragma clang fp contract(off)
 #pragma unroll
-  for (int e = 0; e < E; ++e) {
-    const float a = __fmul_rn(x[e], c[e]), b = __fmul_rn(pt[e], s[e]);
-    x[e] = round_to<ET>(first_half ? __fsub_rn(a, b) : __fadd_rn(a, b));
+    for (int e = 0; e < E; ++e) x[e] = x[e] * c[e] + pt[e] * s[e];
   }
 }
 

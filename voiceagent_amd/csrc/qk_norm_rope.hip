@@ -1,8 +1,10 @@
 // Standalone Qwen3 q/k prologue: RMSNorm + half-split rotary embedding of
 // every query and key head row of a batch of tokens (the prefill side of
 // Qwen3Attention.forward, qwen_asr_vllm/models/qwen3.py:42-48; the decode side
-// is fused into the paged decode kernel).  One group of LPR lanes per head
-// row; the per-row math lives in prologue.h.
+// is fused into the paged decode kernel).  One wave per token, one group of
+// LPR lanes per head row; the per-row math lives in prologue.h.
+#include <algorithm>
+
 #include "prologue.h"
 
 namespace va {
@@ -17,41 +19,79 @@ struct QkParams {
   char* ko;
   int64_t ko_st, ko_sh;
   int32_t num_tokens, hq, hkv;
+  int32_t waves_per_token, groups_per_wave;  // row groups split over waves
   PrologueParams pp;
 };
 
 constexpr int kQkThreads = 256;
+constexpr int kQkChunk = 8;  // row groups whose loads a lane keeps in flight at once
+constexpr int64_t kQkTargetWaves = 4096;  // ~16 per CU: below it a token spreads over waves
 
+// A token's Hq + Hkv head rows go RPW at a time (one row per LPR-lane group)
+// over waves_per_token waves, groups_per_wave row groups each, all of a
+// wave's row loads in flight at once (up to kQkChunk groups at a time).
+// Large batches take one wave per token; small ones spread a token over
+// several waves, so that no wave computes a long chain alone.  What the rows
+// of a token share is loaded once per wave: the position, the two norm weight
+// slices and this lane's cos / sin slice (the same for every row, as a lane
+// keeps its column).  Row loads are issued together with the position,
+// before the rotary loads that depend on it, so a wave costs two round trips
+// whatever its row count; rows past the wave's last read its last row and are
+// not stored, so no load sits behind a branch (row groups wholly past it are
+// not computed either).
 template <typename ET, int D>
 __global__ __launch_bounds__(kQkThreads) void qk_norm_rope_kernel(QkParams p) {
   constexpr int E = ET::kPerVec;
   constexpr int LPR = D / E;     // lanes per head row
-  constexpr int RPW = 64 / LPR;  // rows per wave
+  constexpr int RPW = 64 / LPR;  // rows per wave instruction
   static_assert(LPR >= 2 && LPR <= 64 && 64 % LPR == 0, "unsupported head_dim");
   const int lane = threadIdx.x & 63;
   const int col = lane % LPR;
-  const int64_t wave = (int64_t)blockIdx.x * (kQkThreads / 64) + threadIdx.x / 64;
-  const int64_t row = wave * RPW + lane / LPR;
+  const int sub = lane / LPR;
+  const int64_t w = (int64_t)blockIdx.x * (kQkThreads / 64) + threadIdx.x / 64;
+  const int64_t tok = w / p.waves_per_token;
+  if (tok >= p.num_tokens) return;  // whole waves
   const int heads = p.hq + p.hkv;
-  // Rows are whole lane groups, so a group is either in range or not.
-  if (row >= (int64_t)p.num_tokens * heads) return;
-  const int64_t tok = row / heads;
-  const int hh = (int)(row % heads);
-  const bool isq = hh < p.hq;
-  const char* src = isq ? p.q + tok * p.q_st + hh * p.q_sh
-                        : p.k + tok * p.k_st + (int64_t)(hh - p.hq) * p.k_sh;
-  char* dst = isq ? p.qo + tok * p.qo_st + hh * p.qo_sh
-                  : p.ko + tok * p.ko_st + (int64_t)(hh - p.hq) * p.ko_sh;
-  const uint4 raw = ld16(src + col * 16);
+  const int r0 = (int)(w % p.waves_per_token) * p.groups_per_wave * RPW;  // first row
+  const int r1 = r0 + p.groups_per_wave * RPW < heads ? r0 + p.groups_per_wave * RPW : heads;
+  if (r0 >= heads) return;  // whole waves
   int64_t pos = load_index(p.pp.pos, tok, p.pp.pos_i64);
-  pos = pos < 0 ? 0 : (pos >= p.pp.max_pos ? p.pp.max_pos - 1 : pos);
-  const WeightRaw<E> wr = load_weights_raw<E>(isq ? p.pp.q_w : p.pp.k_w, p.pp.w_dtype, col * E);
-  float x[E], w[E], c[E], s[E];
-  load_rotary<E, LPR>(p.pp, pos, col, D, c, s);
-  ET::unpack(raw, x);
-  convert_weights<E>(wr, p.pp.w_dtype, w);
-  qk_prologue<ET, LPR, E>(x, w, p.pp.eps, D, c, s, col < LPR / 2);
-  st16(dst + col * 16, ET::pack(x));
+  // With no query (key) heads the other side's weights stand in; unused.
+  const WeightRaw<E> wqr = load_weights_raw<E>(p.hq > 0 ? p.pp.q_w : p.pp.k_w, p.pp.w_dtype, col * E);
+  const WeightRaw<E> wkr = load_weights_raw<E>(p.hkv > 0 ? p.pp.k_w : p.pp.q_w, p.pp.w_dtype, col * E);
+  const char* const qrow = p.q + tok * p.q_st + col * 16;
+  const char* const krow = p.k + tok * p.k_st + col * 16;
+  char* const qdst = p.qo + tok * p.qo_st + col * 16;
+  char* const kdst = p.ko + tok * p.ko_st + col * 16;
+  float c[E], s[E], wq[E], wk[E];
+  for (int h0 = r0; h0 < r1; h0 += kQkChunk * RPW) {
+    uint4 raw[kQkChunk];
+#pragma unroll
+    for (int j = 0; j < kQkChunk; ++j) {
+      int hh = h0 + j * RPW + sub;
+      hh = hh < r1 ? hh : r1 - 1;
+      raw[j] = ld16(hh < p.hq ? qrow + hh * p.q_sh : krow + (int64_t)(hh - p.hq) * p.k_sh);
+    }
+    if (h0 == r0) {
+      pos = pos < 0 ? 0 : (pos >= p.pp.max_pos ? p.pp.max_pos - 1 : pos);
+      load_rotary<E, LPR>(p.pp, pos, col, D, c, s);
+      convert_weights<E>(wqr, p.pp.w_dtype, wq);
+      convert_weights<E>(wkr, p.pp.w_dtype, wk);
+    }
+#pragma unroll
+    for (int j = 0; j < kQkChunk; ++j) {
+      if (h0 + j * RPW >= r1) break;  // whole row groups past the wave's last row
+      const int hh = h0 + j * RPW + sub;
+      const bool isq = hh < p.hq;
+      float x[E], wv[E];
+      ET::unpack(raw[j], x);
+#pragma unroll
+      for (int e = 0; e < E; ++e) wv[e] = isq ? wq[e] : wk[e];
+      qk_prologue<ET, LPR, E>(x, wv, p.pp.eps, D, c, s);
+      if (hh < r1)
+        st16(isq ? qdst + hh * p.qo_sh : kdst + (int64_t)(hh - p.hq) * p.ko_sh, ET::pack(x));
+    }
+  }
 }
 
 template <typename ET>
@@ -129,12 +169,19 @@ extern "C" int va_qk_norm_rope(const va_qk_norm_rope_args* a, void* stream) {
   p.pp.pos_i64 = pr.positions_dtype == VA_I64;
   p.pp.pos = pr.positions;
 
+  // Waves per token: enough for ~16 waves per CU when the batch is small
+  // (decode-sized), one per token when it is large.
   const int E = 16 / eb;
   const int rpw = 64 / (a->head_dim / E);
-  const int64_t rows = (int64_t)a->num_tokens * (a->num_heads + a->num_kv_heads);
-  const int64_t waves = (rows + rpw - 1) / rpw;
+  const int groups = (a->num_heads + a->num_kv_heads + rpw - 1) / rpw;
+  int wpt = (int)std::min<int64_t>(groups, std::max<int64_t>(1, (kQkTargetWaves + a->num_tokens - 1) / a->num_tokens));
+  const int gpw = (groups + wpt - 1) / wpt;
+  wpt = (groups + gpw - 1) / gpw;
+  const int64_t waves = (int64_t)a->num_tokens * wpt;
   const int64_t blocks = (waves + kQkThreads / 64 - 1) / (kQkThreads / 64);
-  VA_CHECK_ARG(blocks <= INT32_MAX, "va_qk_norm_rope: too many rows");
+  VA_CHECK_ARG(blocks <= INT32_MAX, "va_qk_norm_rope: too many tokens");
+  p.waves_per_token = wpt;
+  p.groups_per_wave = gpw;
   const dim3 grid((unsigned)blocks);
   const hipStream_t st = (hipStream_t)stream;
   bool ok = false;
