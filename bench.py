@@ -539,16 +539,40 @@ def bench_prologue(args, dev, stream, dec):
             ops.paged_decode(qn, batch.k_pools[i], batch.v_pools[i], batch.block_tables,
                              batch.cu_seqlens_k, new_k=kn, new_v=nvs[i], out=outs[i], **common)
 
+    # A prefill-sized batch (config 3's prompts, one position per token): the
+    # standalone kernel, which runs in front of every prefill.
+    lens = workloads.cfg3_lens(0)
+    total = sum(lens)
+    hq, hkv, d = workloads.HQ, workloads.HKV, workloads.HEAD_DIM
+    qp = torch.randn(layers, total, hq, d, generator=g, device=dev).to(torch.bfloat16)
+    kp = torch.randn(layers, total, hkv, d, generator=g, device=dev).to(torch.bfloat16)
+    qpo, kpo = torch.empty_like(qp), torch.empty_like(kp)
+    ppos = torch.cat([torch.arange(n) for n in lens]).to(dev)
+    ppros = [ops.QKPrologue(wq[i], wk[i], 1e-6, cs, ppos) for i in range(layers)]
+
+    def prefill_prologue():
+        for i in range(layers):
+            ops.qk_norm_rope(qp[i], kp[i], ppros[i], q_out=qpo[i], k_out=kpo[i])
+
     res = {}
-    for name, fn in (("fused", fused), ("two_launch", two_launch)):
+    for name, fn in (("fused", fused), ("two_launch", two_launch), ("prefill", prefill_prologue)):
         ms, _ = timed_graph(fn, args.steps, args.warmup, stream)
         res[name] = ms * 1000.0 / layers
+    # q and k rows read and written, the positions and each token's cos | sin row.
+    pbytes = total * (hq + hkv) * d * 2 * 2 + total * (8 + d * 4)
+    pgbs = pbytes / (res["prefill"] * 1e-6) / 1e9
     log(f"[prologue] decode + q/k norm + rope: fused {res['fused']:.2f} us/layer, "
-        f"two launches {res['two_launch']:.2f} us/layer")
+        f"two launches {res['two_launch']:.2f} us/layer; standalone over config 3's "
+        f"{total} prompt tokens {res['prefill']:.2f} us/layer ({pgbs:.0f} GB/s of "
+        f"{pbytes / 1e6:.1f} MB)")
+    del qp, kp, qpo, kpo
     return {"fused_us_per_layer": round(res["fused"], 2),
             "two_launch_us_per_layer": round(res["two_launch"], 2),
+            "prefill_cfg3_us_per_layer": round(res["prefill"], 2),
+            "prefill_cfg3_gbs": round(pgbs, 1), "prefill_cfg3_bytes": pbytes,
             "config": "cfg2 decode step (B=32, 28 layers) with Qwen3 q/k RMSNorm + RoPE "
-                      "applied to the raw projections"}
+                      "applied to the raw projections; the standalone kernel alone over "
+                      "config 3's prompts"}
 
 
 MAX_MODEL_LEN = 65536  # max_position_embeddings of the decoder (qwen_asr_vllm/config.py:71)
