@@ -122,9 +122,11 @@ int va_store_kvcache(const va_store_args* args, void* stream);
  * convention with the fp32 cache [max_position, head_dim] = [cos | sin],
  *   out[i]       = to_dtype(y[i] cos[i] - y[i + D/2] sin[i]),
  *   out[i + D/2] = to_dtype(y[i + D/2] cos[i] + y[i] sin[i]),    i < D/2
- * at the token's position (layers/rotary_embedding.py:9-32).  Products and
- * sums are rounded separately (no fused multiply-add), as torch evaluates
- * them. */
+ * at the token's position (layers/rotary_embedding.py:9-32).  The rotation's
+ * products are rounded before their sum (no fused multiply-add), as torch
+ * evaluates them; the mean of squares is summed in another order than
+ * torch's (with fused multiply-adds), so 1/sqrt(mean + eps) can differ from
+ * torch's in its last bit. */
 typedef struct va_qk_prologue {
   const void* q_norm_weight;  /* [head_dim] in weight_dtype                 */
   const void* k_norm_weight;  /* [head_dim] in weight_dtype                 */
