@@ -120,6 +120,32 @@ def test_tts_page_layout_with_fused_write(dev, page):
     assert _err(out[:, :, 0], ref) <= TOL
 
 
+@pytest.mark.parametrize("masked", [False, True])
+@pytest.mark.parametrize("lens", [[5, 900], [1, 2, 17, 1000]])
+def test_fixed_partitions_from_a_short_bound(dev, masked, lens):
+    # An automatic split under a short max_seq_len (here 1024) uses fixed
+    # partitions whose first tiles go out before the lengths arrive: short
+    # contexts leave partitions wholly past their end (fetched, then
+    # dropped), and the current row is written and attended in the same
+    # launch.
+    q, kp, vp, table, lt = _nhd_case(lens, 16, torch.bfloat16, seed=len(lens) + masked)
+    B = len(lens)
+    g = torch.Generator().manual_seed(11)
+    nk = torch.randn(B, 8, 128, generator=g).to(torch.bfloat16)
+    nv = torch.randn(B, 8, 128, generator=g).to(torch.bfloat16)
+    valid = (torch.rand(B, 1024, generator=g) < 0.8) if masked else None
+    ek, ev = oracle.write_current_kv(kp, vp, table, lt, nk, nv, layout=oracle.NHD)
+    kd, vd = kp.to(dev), vp.to(dev)
+    print(f"fixed partitions lens={lens} masked={masked}", flush=True)
+    out = ops.paged_decode(q.to(dev), kd, vd, table.to(dev), lt.to(dev), max_seq_len=1024,
+                           scale=128 ** -0.5, new_k=nk.to(dev), new_v=nv.to(dev),
+                           valid_mask=None if valid is None else valid.to(dev))
+    torch.cuda.synchronize()
+    assert torch.equal(kd.cpu(), ek) and torch.equal(vd.cpu(), ev)
+    ref = oracle.paged_decode(q, ek, ev, table, lt, 128 ** -0.5, valid_mask=valid)
+    assert _err(out, ref) <= TOL
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("max_seq_len", [4000, 65536, 100])
 def test_max_seq_len_as_upper_bound(dev, dtype, max_seq_len):

@@ -80,6 +80,10 @@ static int elem_bytes_of(int dtype);
 // (see plan_decode).
 constexpr int64_t kNoSplitBytes = 192 * 1024;
 
+// Longest max_seq_len whose automatic split uses fixed partitions (see
+// plan_decode).
+constexpr int kStaticSplitMax = 4096;
+
 // Context length whose K and V rows of one kv head fill kNoSplitBytes.
 static int nosplit_tokens_for(const va_decode_args* a) {
   const int64_t per_token = (int64_t)a->head_dim * elem_bytes_of(a->dtype) * 2;
@@ -125,6 +129,21 @@ static DecodePlan plan_decode(const va_decode_args* a) {
     const int64_t by_len = (max_len + kDynGrain - 1) / kDynGrain;
     if (parts > by_len) parts = by_len;
     if (parts > kMaxParts) parts = kMaxParts;
+    if (parts > 1 && max_len <= kStaticSplitMax) {
+      // A short max_seq_len fixes the partitions: each workgroup knows its
+      // tokens before the length arrives and requests its first tiles at
+      // once, as an unsplit launch does.  (Short bounds are the exact ones
+      // of eager steps and the TTS talker; a decode graph captured at
+      // max_model_len has a long one and keeps per-length partitions.)
+      P = (int)((max_len + parts - 1) / parts);
+      P = (P + kDynGrain - 1) / kDynGrain * kDynGrain;
+      pl.split_tokens = P;
+      pl.max_parts = (max_len + P - 1) / P;
+      pl.ml_bytes = ((size_t)pairs * pl.max_parts * G * 2 * 4 + 255) / 256 * 256;
+      pl.o_bytes = (size_t)pairs * pl.max_parts * G * a->head_dim * 4;
+      pl.total_bytes = pl.ml_bytes + pl.o_bytes;
+      return pl;
+    }
     if (parts > 1) {
       pl.dyn_split = 1;
       pl.split_tokens = kDynGrain;

@@ -264,9 +264,9 @@ __global__ __launch_bounds__(MfmaDecodeShape<D>::W * 64, 1) void paged_decode_mf
     return bits;
   };
   uint32_t mbits = 0xffffu;
-  // With one partition per pair the partition starts at token 0, so the
-  // words go out with the other start-up loads (see `early` below).
-  if (has_mask && p.max_parts == 1) mask_load((wave + W * lane) * kChunk);
+  // With fixed partitions the partition's start is known, so the words go
+  // out with the other start-up loads (see `early` below).
+  if (has_mask && !p.dyn_split) mask_load(start + (wave + W * lane) * kChunk);
   uint4 kcur = make_uint4(0, 0, 0, 0), vcur = make_uint4(0, 0, 0, 0);
   if (p.new_k != nullptr) {
     kcur = ld16(p.new_k + b * p.nk_sb + h * p.nk_sh + col * 16);
@@ -342,9 +342,11 @@ __global__ __launch_bounds__(MfmaDecodeShape<D>::W * 64, 1) void paged_decode_mf
     }
   };
 
-  // With one partition per pair (start 0, the common decode batch) the first
-  // S tiles are issued now, before the length is known: a block id outside
-  // [0, num_blocks) reads zeros and tokens past the context are masked, so the
+  // With fixed partitions (one per pair, the common decode batch, or a split
+  // planned from a short max_seq_len) the first S tiles of the partition are
+  // issued now, before the length is known: a block id outside
+  // [0, num_blocks) reads zeros, tokens past the context are masked, and a
+  // partition wholly past it only waits for its tiles and exits, so the
   // early tiles are safe to fetch, and the length's round trip leaves the
   // critical path.  The vector loads above are waited for first, so the
   // compiler's own waits for them do not fall after the DMA (where they
@@ -352,7 +354,7 @@ __global__ __launch_bounds__(MfmaDecodeShape<D>::W * 64, 1) void paged_decode_mf
   // rotary rows depend on the position and are requested after the DMA, so
   // the prologue arithmetic waits for the early tiles anyway, which it
   // precedes only by a few hundred cycles.
-  const bool early = p.max_parts == 1;
+  const bool early = !p.dyn_split;
   if (early) {
     if constexpr (!kProlog) {
 #pragma unroll
@@ -364,7 +366,11 @@ __global__ __launch_bounds__(MfmaDecodeShape<D>::W * 64, 1) void paged_decode_mf
     asm volatile("" ::"v"(tab));
     if constexpr (kMask)
       asm volatile("" ::"v"(mraw[0]), "v"(mraw[1]), "v"(mraw[2]), "v"(mraw[3]), "v"(mraw[4]));
-    for (int k = 0; k < S; ++k) issue(k);
+    // Only tiles inside the partition: a short one leaves most waves' slots
+    // past it.  The last partition also takes any tokens past its P, so it
+    // requests all of its first tiles.
+    for (int k = 0; k < S; ++k)
+      if (part == p.max_parts - 1 || (wave + W * k) * kChunk < P) issue(k);
   }
   if constexpr (kProlog) load_rotary<E, LPR>(p.pro, pos, col, D, pro_c, pro_s);
 
