@@ -581,8 +581,10 @@ MAX_MODEL_LEN = 65536  # max_position_embeddings of the decoder (qwen_asr_vllm/c
 def bench_longform(args, dev, stream):
     """Config 5: long-form decode, (i) one 16384-token context, (ii) 8 contexts
     U[4096, 16384]; 28 layers with their own pools, fused store, contexts split
-    into partitions and merged (the split the library picks by default).
-    Each variant also runs with max_seq_len = max_model_len, as the engine's
+    into partitions and merged.  The exact-maximum rows split as an eager
+    engine step does (PagedAttention passes SPLIT_EXACT: its max_seqlen_k is
+    the batch's longest context, model_runner.py:213).  Each variant also runs
+    with max_seq_len = max_model_len and the automatic split, as the engine's
     decode graph passes it (qwen_asr_vllm/engine/graph_runner.py:85-93)."""
     res = {}
     layers = workloads.LAYERS
@@ -602,7 +604,9 @@ def bench_longform(args, dev, stream):
                            device=dev) * 0.5).to(torch.bfloat16)
         outs = torch.empty_like(qs)
 
-        def make_step(max_seq_len, kps, vps, kv_scale=1.0):
+        exact_split = args.split if args.split else ops.SPLIT_EXACT
+
+        def make_step(max_seq_len, kps, vps, kv_scale=1.0, split=exact_split):
             def step():
                 for i in range(layers):
                     ops.paged_decode(qs[i], kps[i], vps[i],
@@ -610,7 +614,7 @@ def bench_longform(args, dev, stream):
                                      lens_cumulative=True, max_seq_len=max_seq_len,
                                      scale=batch.scale, new_k=nks[i], new_v=nvs[i],
                                      new_slots=batch.slot_mapping, out=outs[i],
-                                     split_tokens=args.split, k_scale=kv_scale,
+                                     split_tokens=split, k_scale=kv_scale,
                                      v_scale=kv_scale)
             return step
 
@@ -619,7 +623,8 @@ def bench_longform(args, dev, stream):
                             args.steps, args.warmup, stream, name=f"longform_{variant}")
         us = ms * 1000.0 / layers
         gbs = nbytes / (us * 1e-6) / 1e9
-        ms_g, _ = timed_graph(make_step(MAX_MODEL_LEN, batch.k_pools, batch.v_pools),
+        ms_g, _ = timed_graph(make_step(MAX_MODEL_LEN, batch.k_pools, batch.v_pools,
+                                        split=args.split),
                               args.steps, args.warmup, stream)
         us_g = ms_g * 1000.0 / layers
         log(f"[longform {variant}] B={B} ctx sum {sum(lens)}: {us:.2f} us/layer, {gbs:.0f} GB/s "

@@ -39,7 +39,7 @@
 extern "C" {
 #endif
 
-#define VA_ATTN_ABI_VERSION 4
+#define VA_ATTN_ABI_VERSION 5
 
 /* status codes */
 #define VA_OK 0
@@ -191,7 +191,8 @@ typedef struct va_decode_args {
   int32_t new_slots_dtype;
   int32_t num_seqs, num_heads, num_kv_heads, head_dim;
   int32_t max_seq_len;    /* upper bound of every len; sizes the grid     */
-  int32_t split_tokens;   /* tokens per context partition, 0 = automatic  */
+  int32_t split_tokens;   /* tokens per context partition, 0 = automatic, */
+                          /* VA_SPLIT_EXACT: automatic, exact bound       */
   float scale;            /* softmax scale                                */
   void* workspace;        /* partial results; see va_paged_decode_workspace_bytes */
   size_t workspace_bytes; /* (no initialisation needed; launches sharing one   */
@@ -218,6 +219,17 @@ typedef struct va_decode_args {
  * depends on the current device's compute-unit count, so query the size with
  * the same device current as the launch. */
 size_t va_paged_decode_workspace_bytes(const va_decode_args* args);
+
+/* split_tokens = VA_SPLIT_EXACT: the automatic split, told that max_seq_len
+ * is the exact longest context of the batch (an eager step's maximum, as
+ * qwen_asr_vllm/engine/model_runner.py:213 computes it).  Its partitions are
+ * then fixed from max_seq_len at any length, and each workgroup requests its
+ * first tiles before the lengths arrive; with 0 that holds only up to 4096
+ * tokens, above which each workgroup sizes its partition from its own
+ * length (right for a bound that is only an upper limit, such as the
+ * max_model_len a captured decode graph passes).  The workspace bound is
+ * the automatic split's either way. */
+#define VA_SPLIT_EXACT (-1)
 
 /* One-token GQA attention over a paged pool: split-context partitions, then
  * (only when a context spans several) a merge pass.  Replaces the decode use of

@@ -51,6 +51,8 @@ def test_prepare_batch_mixed_prefill_prefix_and_decode():
     assert ctx.block_tables.tolist() == [[5, 2, 11], [1, 4, 6], [8, 9, -1]]
     for t in (ctx.cu_seqlens_q, ctx.cu_seqlens_k, ctx.slot_mapping, ctx.block_tables):
         assert t.dtype == torch.int32
+    # an eager step's max_seqlen_k is the exact longest context
+    assert ctx.max_seqlen_k_exact
 
 
 def test_prepare_batch_rejects_bad_progress():
@@ -67,6 +69,7 @@ def test_graph_metadata_stage_pads_rows():
     assert bucket == 4
     ctx = meta.context(bucket)
     assert ctx.max_seqlen_q == 1 and ctx.max_seqlen_k == 64
+    assert not ctx.max_seqlen_k_exact  # max_model_len is only a bound
     assert ctx.cu_seqlens_q.tolist() == [0, 1, 2, 3, 4]
     # real rows accumulate full lengths; the padding row adds a key length of 1
     assert ctx.cu_seqlens_k.tolist() == [0, 20, 21, 54, 55]

@@ -147,6 +147,29 @@ def test_fixed_partitions_from_a_short_bound(dev, masked, lens):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("lens,max_seq_len", [
+    ([7, 300, 9000], 9000), ([9000], 9000), ([7, 300, 9000], 5000), ([20, 30], 30)])
+def test_exact_bound_split(dev, dtype, lens, max_seq_len):
+    # split_tokens = SPLIT_EXACT (an eager step's exact longest context) fixes
+    # the partitions from max_seq_len at any length; a context longer than
+    # the bound (5000 here) is still attended whole, by the last partition.
+    q, kp, vp, table, lt = _nhd_case(lens, 16, dtype, seed=max_seq_len % 89 + len(lens))
+    print(f"exact split lens={lens} max_seq_len={max_seq_len} {dtype}", flush=True)
+    out = ops.paged_decode(q.to(dev), kp.to(dev), vp.to(dev), table.to(dev), lt.to(dev),
+                           max_seq_len=max_seq_len, scale=128 ** -0.5,
+                           split_tokens=ops.SPLIT_EXACT)
+    ref = oracle.paged_decode(q, kp, vp, table, lt, 128 ** -0.5)
+    assert _err(out, ref) <= (TOL if dtype != torch.float32 else 1e-5)
+
+
+def test_split_tokens_below_exact_is_rejected(dev):
+    q, kp, vp, table, lt = _nhd_case([40, 40], 16, torch.bfloat16, seed=1)
+    with pytest.raises(Exception, match="split_tokens"):
+        ops.paged_decode(q.to(dev), kp.to(dev), vp.to(dev), table.to(dev), lt.to(dev),
+                         max_seq_len=40, scale=0.1, split_tokens=-2)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("max_seq_len", [4000, 65536, 100])
 def test_max_seq_len_as_upper_bound(dev, dtype, max_seq_len):
     # A decode graph is captured with max_seqlen_k = max_model_len

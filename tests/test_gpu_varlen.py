@@ -285,6 +285,45 @@ def test_paged_attention_layer_prefill_then_decode(dev):
         assert torch.equal(kv[0].cpu(), kc) and torch.equal(kv[1].cpu(), vc), step
 
 
+@pytest.mark.parametrize("exact", [False, True])
+def test_paged_attention_layer_long_decode_exact_bound(dev, exact):
+    """A decode step whose context says its max_seqlen_k is exact (an eager
+    step's, max_seqlen_k_exact) splits with fixed partitions; one that does
+    not, with the automatic split.  Both match the oracle, pools bit for bit."""
+    g = torch.Generator().manual_seed(23)
+    bs, hq, hkv, d = 16, 16, 8, 128
+    lens = [5000, 300]
+    need = [(n + bs - 1) // bs for n in lens]
+    nb = sum(need) + 4
+    perm = torch.randperm(nb, generator=g).tolist()
+    width = max(need)
+    rows, cur = [], 0
+    for m in need:
+        rows.append(perm[cur:cur + m] + [-1] * (width - m))
+        cur += m
+    table = torch.tensor(rows, dtype=torch.int32)
+    kp = (torch.randn(nb, bs, hkv, d, generator=g) * 0.5).to(torch.bfloat16)
+    vp = (torch.randn(nb, bs, hkv, d, generator=g) * 0.5).to(torch.bfloat16)
+    q = torch.randn(2, hq, d, generator=g).to(torch.bfloat16)
+    nk = torch.randn(2, hkv, d, generator=g).to(torch.bfloat16)
+    nv = torch.randn(2, hkv, d, generator=g).to(torch.bfloat16)
+    lt = torch.tensor(lens, dtype=torch.int32)
+    slots = torch.tensor([rows[s][(n - 1) // bs] * bs + (n - 1) % bs for s, n in enumerate(lens)],
+                         dtype=torch.int32)
+    layer = PagedAttention(hq, d, d ** -0.5, hkv)
+    layer.k_cache, layer.v_cache = kp.to(dev), vp.to(dev)
+    ctx = AttentionContext(torch.arange(3, dtype=torch.int32, device=dev), _cu(lens).to(dev), 1,
+                           max(lens), slots.to(dev), table.to(dev), max_seqlen_k_exact=exact)
+    print(f"layer decode lens={lens} exact={exact}", flush=True)
+    with attention_context(ctx):
+        out = layer(q.to(dev), nk.to(dev), nv.to(dev))
+    torch.cuda.synchronize()
+    ek, ev = oracle.write_current_kv(kp, vp, table, lt, nk, nv, layout=oracle.NHD)
+    assert torch.equal(layer.k_cache.cpu(), ek) and torch.equal(layer.v_cache.cpu(), ev)
+    ref = oracle.paged_decode(q, ek, ev, table, lt, d ** -0.5)
+    assert _err(out, ref) <= TOL
+
+
 @pytest.mark.parametrize("fuse", [True, False])
 def test_paged_attention_layer_hnd_pool_matches_nhd(dev, fuse):
     """The same engine sequence (prefix-cached prefill, then decode steps) on an

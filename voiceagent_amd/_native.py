@@ -21,8 +21,9 @@ VA_BF16, VA_F16, VA_F32 = 0, 1, 2
 VA_I32, VA_I64 = 0, 1
 VA_LENS_PER_SEQ, VA_LENS_CUMULATIVE = 0, 1
 VA_KV_NATIVE, VA_KV_FP8_E4M3 = 0, 1
-ABI_VERSION = 4  # VA_ATTN_ABI_VERSION of the header these structs mirror
+ABI_VERSION = 5  # VA_ATTN_ABI_VERSION of the header these structs mirror
 DECODE_NOALLOC_SCRATCH_BYTES = 4 << 20  # VA_DECODE_NOALLOC_SCRATCH_BYTES
+VA_SPLIT_EXACT = -1  # split_tokens: automatic split, max_seq_len exact
 
 DTYPE_CODES = {torch.bfloat16: VA_BF16, torch.float16: VA_F16, torch.float32: VA_F32}
 INDEX_CODES = {torch.int32: VA_I32, torch.int64: VA_I64}

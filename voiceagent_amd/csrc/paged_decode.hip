@@ -103,7 +103,8 @@ static DecodePlan plan_decode(const va_decode_args* a) {
   if (unit <= 0) unit = 128;
   int max_len = a->max_seq_len > 0 ? a->max_seq_len : 1;
   if (a->key_limit > 0 && a->key_limit < max_len) max_len = a->key_limit;
-  int P = a->split_tokens;
+  const bool exact = a->split_tokens == VA_SPLIT_EXACT;
+  int P = exact ? 0 : a->split_tokens;
   const int64_t pairs = (int64_t)a->num_seqs * a->num_kv_heads;
   if (P <= 0) {
     // Split contexts only as far as needed to give every CU one workgroup:
@@ -129,12 +130,13 @@ static DecodePlan plan_decode(const va_decode_args* a) {
     const int64_t by_len = (max_len + kDynGrain - 1) / kDynGrain;
     if (parts > by_len) parts = by_len;
     if (parts > kMaxParts) parts = kMaxParts;
-    if (parts > 1 && max_len <= kStaticSplitMax) {
-      // A short max_seq_len fixes the partitions: each workgroup knows its
-      // tokens before the length arrives and requests its first tiles at
-      // once, as an unsplit launch does.  (Short bounds are the exact ones
-      // of eager steps and the TTS talker; a decode graph captured at
-      // max_model_len has a long one and keeps per-length partitions.)
+    if (parts > 1 && (exact || max_len <= kStaticSplitMax)) {
+      // A short or exact (VA_SPLIT_EXACT) max_seq_len fixes the partitions:
+      // each workgroup knows its tokens before the length arrives and
+      // requests its first tiles at once, as an unsplit launch does.  (Short
+      // bounds are the exact ones of eager steps and the TTS talker; a
+      // decode graph captured at max_model_len has a long one and keeps
+      // per-length partitions.)
       P = (int)((max_len + parts - 1) / parts);
       P = (P + kDynGrain - 1) / kDynGrain * kDynGrain;
       pl.split_tokens = P;
@@ -327,6 +329,8 @@ int va::paged_decode_impl(const va_decode_args* a, void* stream) {
                    a->new_slots_dtype == VA_I64,
                "va_paged_decode: new_slots_dtype");
   VA_CHECK_ARG(a->max_seq_len >= 0, "va_paged_decode: max_seq_len < 0");
+  VA_CHECK_ARG(a->split_tokens >= VA_SPLIT_EXACT,
+               "va_paged_decode: split_tokens %d (>= 0, or VA_SPLIT_EXACT)", a->split_tokens);
   VA_CHECK_ARG(a->table_width >= 0, "va_paged_decode: table_width < 0");
   VA_CHECK_ARG(a->key_limit >= 0 && a->table_read_width >= 0,
                "va_paged_decode: key_limit and table_read_width must be non-negative");

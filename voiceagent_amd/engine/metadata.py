@@ -78,6 +78,7 @@ def prepare_batch(
         max_seqlen_k=max_k,
         slot_mapping=torch.tensor(slot_mapping, **i32),
         block_tables=torch.tensor(padded, **i32).reshape(len(tables), width),
+        max_seqlen_k_exact=True,
     )
     return torch.tensor(positions, dtype=torch.int64, device=device), context
 

@@ -81,6 +81,13 @@ def store_kvcache(
                       k_scale=k_scale, v_scale=v_scale)
 
 
+def _decode_split(context) -> int:
+    """Decode split of this step: fixed partitions from an exact max_seqlen_k
+    (an eager step's), the automatic split for a bound (a graph's
+    max_model_len, or a context that does not say)."""
+    return ops.SPLIT_EXACT if context.max_seqlen_k_exact else 0
+
+
 class PagedAttention(nn.Module):
     fuse_store = True
     kv_layout = ops.LAYOUT_NHD
@@ -133,6 +140,7 @@ class PagedAttention(nn.Module):
                 max_seq_len=context.max_seqlen_k,
                 scale=self.scale,
                 layout=self.kv_layout,
+                split_tokens=_decode_split(context),
                 k_scale=self.k_scale,
                 v_scale=self.v_scale,
             )
@@ -190,6 +198,7 @@ class PagedAttention(nn.Module):
             new_v=v,
             new_slots=context.slot_mapping,
             prologue=prologue,
+            split_tokens=_decode_split(context),
             k_scale=self.k_scale,
             v_scale=self.v_scale,
         )

@@ -27,6 +27,12 @@ class AttentionContext:
     """Physical KV slot of each query token (int32); ``-1`` skips the write."""
     block_tables: torch.Tensor | None = None
     """[num_seqs, width] int32 block ids; padding beyond a sequence is ignored."""
+    max_seqlen_k_exact: bool = False
+    """True when max_seqlen_k is the batch's exact longest context, as an eager
+    step computes it (qwen_asr_vllm/engine/model_runner.py:213); decode then
+    fixes its context partitions from it at any length (ops.SPLIT_EXACT).  Not
+    a field of the reference's context: its runner leaves the default, and a
+    graph's max_model_len bound must too."""
 
 
 _CONTEXT = AttentionContext()

@@ -16,6 +16,10 @@ import torch
 
 from voiceagent_amd import _native as N
 
+# split_tokens for a max_seq_len that is the batch's exact longest context
+# (an eager step's): the automatic split with fixed partitions at any length
+# (va_paged_decode, VA_SPLIT_EXACT).
+SPLIT_EXACT = N.VA_SPLIT_EXACT
 LAYOUT_NHD = "nhd"  # [num_blocks, block_size, Hkv, D]  (engine, model_runner.py:116-131)
 LAYOUT_HND = "hnd"  # [pages, Hkv, page_size, D]        (TTS, qwen_tts_outer_paged_cache.py:116-119)
 # An FP8 KV pool holds OCP e4m3 codes (torch.float8_e4m3fn); an element's
@@ -459,7 +463,10 @@ def paged_decode(
     keeps the split partials in the library's own scratch buffer instead of a
     workspace; ``out`` must then be given, so that nothing is allocated.
     An FP8 (float8_e4m3fn) pool is read as code * k_scale / v_scale, and the
-    current row is stored into it quantised.
+    current row is stored into it quantised.  ``split_tokens``: 0 splits
+    contexts automatically; ``SPLIT_EXACT`` does too, for a ``max_seq_len``
+    that is the batch's exact longest context (partitions fixed from it); a
+    positive value fixes the partition size.
     """
     fast = _FAST if _FAST_LOADED else _fast_calls()
     if fast is not None and not no_alloc and layout in (LAYOUT_NHD, LAYOUT_HND):
