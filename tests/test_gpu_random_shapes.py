@@ -1,8 +1,9 @@
 """Seeded random combinations of the decode and varlen options, against the
 oracle: dtype, head_dim, group size, kv heads, block size (including block
 sizes that take the general decode kernel), pool layout, index dtypes,
-cumulative lengths, key mask, fused current-row write, and exact or
-upper-bound max_seq_len; causal and bidirectional varlen; and causal prefill
+cumulative lengths, key mask, fused current-row write, and an exact
+max_seq_len (automatic or exact-bound split) or an upper bound of 4096 or
+65536; causal and bidirectional varlen; and causal prefill
 over a paged prefix with the store fused.  Each case is small enough for the
 CPU oracle.
 
@@ -35,10 +36,12 @@ def _decode_case(seed):
     return dict(dtype=dtype, d=d, g=g, hkv=hkv, bs=bs, layout=layout, lens=lens,
                 table_i64=r.random() < 0.5, cumulative=r.random() < 0.5,
                 mask=r.random() < 0.4, fused=r.random() < 0.5, bound=r.random() < 0.3,
-                width_extra=r.choice([-50, 0, 7]))
+                width_extra=r.choice([-50, 0, 7]),
+                # drawn last, so the earlier draws of a seed stay as they were
+                bound_len=r.choice([4096, 65536]), exact=r.random() < 0.5)
 
 
-@pytest.mark.parametrize("seed", range(40))
+@pytest.mark.parametrize("seed", range(60))
 def test_random_decode_options(dev, seed):
     c = _decode_case(seed)
     print(f"decode case {seed}: {c}", flush=True)
@@ -76,7 +79,9 @@ def test_random_decode_options(dev, seed):
     kd, vd = kp.to(dev), vp.to(dev)
     out = ops.paged_decode(q.to(dev), kd, vd, table.to(dev), lens_arg.to(dev),
                            lens_cumulative=c["cumulative"],
-                           max_seq_len=4096 if c["bound"] else max(lens), scale=d ** -0.5,
+                           max_seq_len=c["bound_len"] if c["bound"] else max(lens),
+                           split_tokens=ops.SPLIT_EXACT if c["exact"] and not c["bound"] else 0,
+                           scale=d ** -0.5,
                            layout=c["layout"], valid_mask=None if valid is None else valid.to(dev),
                            new_k=None if nk is None else nk.to(dev),
                            new_v=None if nv is None else nv.to(dev))
