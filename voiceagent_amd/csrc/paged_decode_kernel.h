@@ -451,7 +451,7 @@ __global__ __launch_bounds__((DecodeShape<ET, D, G>::NW * 64),
   // trip overlaps that of the K/V rows.
   auto prepare_query = [&]() {
     if constexpr (kProlog) {
-        float w[E];
+      float w[E];
       convert_weights<E>(pro_wq, p.pro.w_dtype, w);
 #pragma unroll
       for (int g = 0; g < G; ++g) {

@@ -343,7 +343,7 @@ __global__ __launch_bounds__(MfmaDecodeShape<D>::W * 64, 1) void paged_decode_mf
   };
 
   // With fixed partitions (one per pair, the common decode batch, or a split
-  // planned from a short max_seq_len) the first S tiles of the partition are
+  // planned from a short or exact max_seq_len) the first S tiles of the partition are
   // issued now, before the length is known: a block id outside
   // [0, num_blocks) reads zeros, tokens past the context are masked, and a
   // partition wholly past it only waits for its tiles and exits, so the
