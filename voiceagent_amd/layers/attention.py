@@ -85,7 +85,7 @@ def _decode_split(context) -> int:
     """Decode split of this step: fixed partitions from an exact max_seqlen_k
     (an eager step's), the automatic split for a bound (a graph's
     max_model_len, or a context that does not say)."""
-    return ops.SPLIT_EXACT if context.max_seqlen_k_exact else 0
+    return ops.SPLIT_EXACT if getattr(context, "max_seqlen_k_exact", False) else 0
 
 
 class PagedAttention(nn.Module):
