@@ -645,6 +645,11 @@ def bench_longform(args, dev, stream):
                         "frac": round(gbs / HBM_PEAK_GBS, 4), "bytes_per_layer": nbytes,
                         "batch": B, "context_tokens": sum(lens),
                         "us_per_layer_max_model_len": round(us_g, 2),
+                        "split": ("exact-bound (SPLIT_EXACT, as an eager step)" if not args.split
+                                  else f"split_tokens {args.split}"),
+                        "split_max_model_len": ("automatic (as a captured decode graph)"
+                                                if not args.split
+                                                else f"split_tokens {args.split}"),
                         "fp8": {"us_per_layer": round(us8, 2), "gbs": round(gbs8, 1),
                                 "frac": round(gbs8 / HBM_PEAK_GBS, 4),
                                 "bytes_per_layer": nbytes8}}
