@@ -92,10 +92,12 @@ def _fp8_batch(lens, dev, seed, dtype=torch.bfloat16, hq=16, hkv=8, d=128, bs=16
         (torch.float16, 16, 8, 128, 32, ops.LAYOUT_NHD, "exact", True, False),    # key mask
         (torch.bfloat16, 8, 1, 64, 16, ops.LAYOUT_HND, "graph", True, True),      # G = 8, D = 64
         (torch.float16, 4, 4, 256, 16, ops.LAYOUT_NHD, "exact", False, True),     # G = 1, D = 256
+        (torch.bfloat16, 16, 8, 128, 16, ops.LAYOUT_NHD, "exact_split", True, True),  # fixed, 5000
     ],
 )
 def test_decode_over_fp8_pool(dev, dtype, hq, hkv, d, bs, layout, bound, masked, fused):
-    lens = [1, 9, 16, 17, 100, 257, 600, 2100]
+    # exact_split: SPLIT_EXACT over a bound above the automatic fixed-partition range
+    lens = [1, 17, 600, 5000] if bound == "exact_split" else [1, 9, 16, 17, 100, 257, 600, 2100]
     ks, vs = 0.05, 0.08
     table, kp, vp, q, nk, nv = _fp8_batch(lens, dev, seed=d + bs, dtype=dtype, hq=hq, hkv=hkv,
                                           d=d, bs=bs, layout=layout, k_scale=ks, v_scale=vs)
@@ -106,7 +108,8 @@ def test_decode_over_fp8_pool(dev, dtype, hq, hkv, d, bs, layout, bound, masked,
     print(f"fp8 decode {dtype} G={hq // hkv} D={d} bs={bs} {layout} {bound} masked={masked}",
           flush=True)
     out = ops.paged_decode(q.to(dev), kd, vd, table.to(dev), lens_t.to(dev),
-                           max_seq_len=max(lens) if bound == "exact" else 65536,
+                           max_seq_len=65536 if bound == "graph" else max(lens),
+                           split_tokens=ops.SPLIT_EXACT if bound == "exact_split" else 0,
                            scale=d ** -0.5, layout=layout,
                            valid_mask=None if valid is None else valid.to(dev),
                            new_k=nk.to(dev) if fused else None,
