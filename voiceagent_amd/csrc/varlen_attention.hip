@@ -532,6 +532,8 @@ __global__ __launch_bounds__(kVarlenThreads, 2) void varlen_attention_kernel(Var
       const char* s_v = s_k + TILE_B;
 
       // Store steps run only on tiles that hold some of the block's new rows.
+      // The rows go out non-temporally: nothing in the launch reads them back
+      // (config 3: 40.4 -> 39.6 us per launch).
       if (fused_store && st_key0 < kb + kKeyTile &&
           st_key0 + (cur.pos_end - cur.pos0) > kb) {
         const int64_t cap = (int64_t)p.num_blocks * p.block_size;
@@ -552,8 +554,8 @@ __global__ __launch_bounds__(kVarlenThreads, 2) void varlen_attention_kernel(Var
                                 cur.h * p.s_head + c * 16;
             const int r = key - kb;
             const int off = r * ROWB + ((c ^ swz<D>(r)) << 4);
-            st16(p.kp + dst, lds_read16(s_k, off));
-            st16(p.vp + dst, lds_read16(s_v, off));
+            st16_nt(p.kp + dst, lds_read16(s_k, off));
+            st16_nt(p.vp + dst, lds_read16(s_v, off));
           }
         }
       }
