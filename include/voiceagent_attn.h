@@ -291,10 +291,10 @@ typedef struct va_varlen_args {
    * slot_mapping[i] (slot < 0 skips), as store_kvcache would. */
   const void* slot_mapping;
   int32_t slot_dtype;
-  /* Scratch for an FP8 pool's paged prefix (see va_varlen_workspace_bytes;
-   * no initialisation needed).  The prefix keys are dequantised into it
-   * (bf16 / f16) before attention; with an FP8 pool, max_seqlen_k must
-   * bound every k_len. */
+  /* Unused (no varlen launch needs a workspace; va_varlen_workspace_bytes
+   * returns 0).  An FP8 pool's prefix rows are converted to the 16-bit type
+   * (code * scale, rounded once) inside the kernel, tile by tile, and its
+   * new rows are stored quantised after the attention. */
   void* workspace;
   size_t workspace_bytes;
 } va_varlen_args;
@@ -304,9 +304,8 @@ typedef struct va_varlen_args {
  * fused), or non-causal block-diagonal (audio encoder windows). */
 int va_varlen_attention(const va_varlen_args* args, void* stream);
 
-/* Bytes of workspace va_varlen_attention needs (0 unless the pool is FP8 and
- * keys come from it): num_seqs x ceil(max_seqlen_k / block_size) blocks of
- * dequantised prefix rows plus their block table. */
+/* Bytes of workspace va_varlen_attention needs: always 0 (kept for callers
+ * written against the earlier contract). */
 size_t va_varlen_workspace_bytes(const va_varlen_args* args);
 
 /* ----------------------------------------------------------------- misc */

@@ -125,6 +125,22 @@ def test_decode_workspace_sizing():
     assert lib.va_paged_decode_workspace_bytes(ctypes.byref(bad)) == 0
 
 
+def test_varlen_needs_no_workspace_even_for_long_fp8_prefixes():
+    # An FP8 pool's prefix is converted inside the kernel: no workspace, at
+    # any max_seqlen_k (the former prefix copy took num_seqs x
+    # ceil(max_seqlen_k / block_size) blocks: ~4.3 GB at 16 x 65536 tokens).
+    lib = N.lib()
+    args = N.new_args(N.VarlenArgs)
+    args.num_seqs, args.num_heads, args.num_kv_heads, args.head_dim = 16, 16, 8, 128
+    args.max_seqlen_q, args.max_seqlen_k = 512, 65536
+    args.pool.k = args.pool.v = 1 << 20  # a pool is described; nothing is dereferenced
+    args.pool.block_size, args.pool.num_blocks = 16, 1 << 16
+    args.pool.kv_format = N.VA_KV_FP8_E4M3
+    args.pool.k_scale = args.pool.v_scale = 1.0
+    args.block_tables = 1 << 20
+    assert lib.va_varlen_workspace_bytes(ctypes.byref(args)) == 0
+
+
 def test_ops_refuse_cpu_tensors():
     q = torch.zeros(2, 16, 128)
     pool = torch.zeros(4, 16, 8, 128)

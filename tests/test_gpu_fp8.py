@@ -200,6 +200,86 @@ def test_prefill_over_fp8_prefix_with_fused_store(dev, dtype):
     assert _err(out2, ref2) <= 2e-2
 
 
+def _fp8_prefix_case(gen, table_cols=None):
+    """Prompts continuing paged prefixes, with the pool as FP8 codes and as a
+    bf16 pool holding the same values rounded once (bf16(code * scale))."""
+    hq, hkv, d, bs = 16, 8, 128, 16
+    prefix = [0, 16, 37, 300, 5, 129]
+    qlens = [50, 1, 64, 129, 200, 3]
+    klens = [p + q for p, q in zip(prefix, qlens)]
+    need = [math.ceil(k / bs) for k in klens]
+    nb = sum(need) + 4
+    perm = torch.randperm(nb, generator=gen).tolist()
+    rows, cur = [], 0
+    for n in need:
+        rows.append(perm[cur:cur + n] + [-1] * (max(need) - n))
+        cur += n
+    table = torch.tensor(rows, dtype=torch.int32)
+    if table_cols is not None:
+        table = table[:, :table_cols].contiguous()
+    ks, vs = 0.04, 0.1
+    kp = oracle.quantize_fp8(torch.randn(nb, bs, hkv, d, generator=gen), ks)
+    vp = oracle.quantize_fp8(torch.randn(nb, bs, hkv, d, generator=gen), vs)
+    kb = oracle.dequantize_fp8(kp, ks).to(torch.bfloat16)
+    vb = oracle.dequantize_fp8(vp, vs).to(torch.bfloat16)
+    total = sum(qlens)
+    q = torch.randn(total, hq, d, generator=gen).to(torch.bfloat16)
+    k = torch.randn(total, hkv, d, generator=gen).to(torch.bfloat16)
+    v = torch.randn(total, hkv, d, generator=gen).to(torch.bfloat16)
+    cu_q = torch.tensor([0] + list(torch.tensor(qlens).cumsum(0)), dtype=torch.int32)
+    cu_k = torch.tensor([0] + list(torch.tensor(klens).cumsum(0)), dtype=torch.int32)
+    return dict(q=q, k=k, v=v, cu_q=cu_q, cu_k=cu_k, qlens=qlens, klens=klens, table=table,
+                kp=kp, vp=vp, kb=kb, vb=vb, ks=ks, vs=vs, d=d)
+
+
+def _prefill(c, dev, fp8, new_rows=True, max_k=None):
+    kc, vc = (c["kp"], c["vp"]) if fp8 else (c["kb"], c["vb"])
+    return ops.varlen_attention(
+        c["q"].to(dev), c["k"].to(dev) if new_rows else None, c["v"].to(dev) if new_rows else None,
+        c["cu_q"].to(dev), c["cu_k"].to(dev), max(c["qlens"]),
+        max(c["klens"]) if max_k is None else max_k, scale=c["d"] ** -0.5, causal=True,
+        k_cache=kc.to(dev), v_cache=vc.to(dev), block_tables=c["table"].to(dev),
+        k_scale=c["ks"] if fp8 else 1.0, v_scale=c["vs"] if fp8 else 1.0)
+
+
+@pytest.mark.parametrize("new_rows", [True, False])
+def test_fp8_prefix_prefill_equals_bf16_pool_of_its_values(dev, new_rows):
+    # The kernel converts each staged code to code * scale rounded once to
+    # bf16: the launch must give the bits of the same launch over a bf16 pool
+    # holding those values.
+    c = _fp8_prefix_case(torch.Generator().manual_seed(31))
+    got = _prefill(c, dev, True, new_rows)
+    want = _prefill(c, dev, False, new_rows)
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)
+    ref = oracle.varlen_attention(c["q"], c["k"] if new_rows else None,
+                                  c["v"] if new_rows else None, c["cu_q"], c["cu_k"],
+                                  c["d"] ** -0.5, True, k_cache=c["kp"], v_cache=c["vp"],
+                                  block_tables=c["table"], k_scale=c["ks"], v_scale=c["vs"])
+    assert _err(got, ref) <= 2e-2
+
+
+def test_fp8_prefix_reads_columns_past_the_table_width_as_bf16_does(dev):
+    # Three table columns for prefixes of up to 19 blocks: keys whose column
+    # is at or past the width read block 0 on both pool dtypes alike (the
+    # TTS padding semantics, qwen_tts_paged_attention.py:458-465).
+    c = _fp8_prefix_case(torch.Generator().manual_seed(32), table_cols=3)
+    got = _prefill(c, dev, True)
+    want = _prefill(c, dev, False)
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)
+
+
+def test_fp8_prefix_ignores_max_seqlen_k(dev):
+    # Key ranges come from cu_seqlens_k only: an underestimated max_seqlen_k
+    # changes nothing (the former prefix copy dropped keys past it).
+    c = _fp8_prefix_case(torch.Generator().manual_seed(33))
+    got = _prefill(c, dev, True, max_k=1)
+    want = _prefill(c, dev, True)
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)
+
+
 def test_paged_attention_layer_prefill_then_decode_on_fp8_pool(dev):
     # The engine's sequence through the drop-in layer: a prefill that fills
     # the FP8 cache, then decode steps that attend it and append to it.

@@ -110,6 +110,13 @@ def test_bucket_set_captured_largest_first_replays_match_oracle_and_eager(dev):
         torch.cuda.synchronize()
         got = [o[:batch].clone() for o in outs[bucket]]
         pools_after = kv.cpu()
+        # Padding rows [batch, bucket) (slot -1, table 0, k_len 1;
+        # graph_runner.py:157-160, 178-180) are discarded by the caller but
+        # must be finite.
+        for i in range(LAYERS):
+            pad = outs[bucket][i][batch:bucket]
+            assert pad.shape[0] == bucket - batch
+            assert bool(torch.isfinite(pad).all()), (step, i, "non-finite padding row")
 
         # Oracle: the store of every real row, then the decode over the pool.
         slots = meta.slot_mapping[:batch].cpu()

@@ -65,3 +65,35 @@ def test_noalloc_rejects_a_split_beyond_its_scratch(dev):
     with pytest.raises(ops.AttentionArgumentError, match="out"):
         ops.paged_decode(q, pool, pool.clone(), table, lens, max_seq_len=4096, scale=0.1,
                          no_alloc=True)
+
+
+def test_noalloc_calls_on_two_streams_are_ordered(dev):
+    # Both calls split their contexts, so both use the one scratch buffer of
+    # the GPU; the second, on another stream and issued without a host sync,
+    # must wait for the first (ops orders them on the GPU).
+    def batch(lens, seed):
+        nb = sum((n + 15) // 16 for n in lens) + 8
+        return workloads.make_decode_batch(lens, num_blocks=nb, dtype=torch.bfloat16,
+                                           kv_std=0.5, device=dev, seed=seed)
+
+    def call(b, out, no_alloc, max_seq_len):
+        ops.paged_decode(b.q, b.k_pools[0], b.v_pools[0], b.block_tables, b.cu_seqlens_k,
+                         lens_cumulative=True, max_seq_len=max_seq_len, scale=b.scale, out=out,
+                         no_alloc=no_alloc)
+
+    b1, b2 = batch([16384], 95), batch([3000, 2500, 4100], 96)
+    ref1, ref2 = torch.empty_like(b1.q), torch.empty_like(b2.q)
+    call(b1, ref1, False, 16384)
+    call(b2, ref2, False, 65536)
+    torch.cuda.synchronize()
+    s1, s2 = torch.cuda.Stream(dev), torch.cuda.Stream(dev)
+    for rep in range(3):
+        out1, out2 = torch.full_like(ref1, float("nan")), torch.full_like(ref2, float("nan"))
+        torch.cuda.synchronize()
+        print(f"two-stream no_alloc rep {rep}", flush=True)
+        with torch.cuda.stream(s1):
+            call(b1, out1, True, 16384)
+        with torch.cuda.stream(s2):
+            call(b2, out2, True, 65536)
+        torch.cuda.synchronize()
+        assert torch.equal(out1, ref1) and torch.equal(out2, ref2), rep

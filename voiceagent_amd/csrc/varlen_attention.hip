@@ -31,6 +31,7 @@
 // table while the tile is loaded; the new keys come from k/v.  The fused
 // store copies an item's new K/V rows from the staged tiles to slot_mapping.
 #include <atomic>
+#include <type_traits>
 
 #include "common.h"
 #include "fastdiv.h"
@@ -69,6 +70,8 @@ struct VarlenParams {
   int32_t num_seqs, num_kv_heads;
   FastDiv bs_div, hkv_div;  // block_size, num_kv_heads
   int32_t slot_small;       // num_blocks * block_size <= 2^31: slots divide in 32 bits
+  float k_scale, v_scale;   // FP8 pool: element = code * scale
+  int32_t kv_f8;            // the pool holds e4m3 codes (strides in bytes of codes)
 };
 
 template <bool kBF16>
@@ -132,8 +135,14 @@ __device__ inline s16x4_t lds_read_tr(const char* base, int off) {
 }
 
 // kPaged: keys j < k_len - q_len come from the pool through the block table
-// (launches with a pool); otherwise every key comes from k/v.
-template <bool kBF16, int D, int G, bool kCausal, bool kPaged, bool kOnce>
+// (launches with a pool); otherwise every key comes from k/v.  kF8 (with
+// kPaged): the pool holds OCP e4m3 codes.  A tile's pool rows are copied as
+// codes into a code area of LDS and converted, at the top of the tile's
+// step, into the 16-bit stage as code * scale rounded to the 16-bit type
+// (every e4m3 value converts exactly; the product is rounded once), before
+// the next tile's copy may reuse the code area.  Rows from k/v are staged
+// as 16-bit rows, as without a pool.
+template <bool kBF16, int D, int G, bool kCausal, bool kPaged, bool kOnce, bool kF8 = false>
 __global__ __launch_bounds__(kVarlenThreads, 2) void varlen_attention_kernel(VarlenParams p) {
   constexpr int BQ = kRowsPerWG / G;       // query positions per workgroup
   constexpr int DS = D / 32;               // k-steps of the S^T MFMA
@@ -153,6 +162,16 @@ __global__ __launch_bounds__(kVarlenThreads, 2) void varlen_attention_kernel(Var
   // reduced.
   static_assert(kStages == 2, "the tile loop alternates two stages");
   __shared__ __align__(1024) char s_kv[kStages * 2 * TILE_B];
+  // FP8 pool: the codes of one tile's pool rows (K, then V), row-major and
+  // unswizzled: row r's 16-code chunk c at r D + 16 c.
+  static_assert(!kF8 || kPaged, "FP8 codes come from a pool");
+  constexpr int CODE_B = kKeyTile * D;     // bytes of one tile of codes, K or V
+  constexpr int CCPR = D / 16;             // 16-code chunks per code row
+  constexpr int CRPI = 64 / CCPR;          // code rows per DMA instruction
+  constexpr int NIC = CODE_B / 1024 / 4;   // code DMA instructions per wave per tile, K or V
+  static_assert(!kF8 || NIC * 4 * 1024 == CODE_B, "code DMA split");
+  __shared__ __align__(1024) char s_code[kF8 ? 2 * CODE_B : 16];
+  using ET = std::conditional_t<kBF16, BF16, F16>;
 
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
@@ -284,6 +303,8 @@ __global__ __launch_bounds__(kVarlenThreads, 2) void varlen_attention_kernel(Var
 
   const uint32_t lds_base = __builtin_amdgcn_readfirstlane(
       (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)s_kv);
+  const uint32_t code_base = __builtin_amdgcn_readfirstlane(
+      (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)s_code);
 
   // ---- DMA of key tile [kb, kb + 64) into stage st ----
   // (h, pool_prefix, kend, new_base, table_row) are the item's; all uniform.
@@ -335,7 +356,7 @@ __global__ __launch_bounds__(kVarlenThreads, 2) void varlen_attention_kernel(Var
     uint2 braw[NI];
 #pragma unroll
     for (int i = 0; i < NI; ++i) braw[i] = make_uint2(0u, 0u);
-    if (kPaged && kb < pool_prefix) {
+    if (kPaged && !kF8 && kb < pool_prefix) {
       int64_t e[NI];
       bool ok[NI];
 #pragma unroll
@@ -355,6 +376,56 @@ __global__ __launch_bounds__(kVarlenThreads, 2) void varlen_attention_kernel(Var
           if (ok[i]) braw[i].x = reinterpret_cast<const uint32_t*>(p.table)[e[i]];
       }
     }
+    // FP8 pool: the tile's pool rows as codes.  Lane l of code instruction i
+    // copies chunk l % CCPR of code row (wave NIC + i) CRPI + l / CCPR.
+    const char* kc[kF8 ? NIC : 1];
+    const char* vc[kF8 ? NIC : 1];
+    if constexpr (kF8) {
+#pragma unroll
+      for (int i = 0; i < NIC; ++i) {
+        kc[i] = zero_row;
+        vc[i] = zero_row;
+      }
+      if (kb < pool_prefix) {
+        int crow0 = wave * NIC * CRPI + lane / CCPR;
+        asm volatile("" : "+v"(crow0));
+        uint2 craw[NIC];
+        bool cok[NIC];
+        int64_t ce[NIC];
+#pragma unroll
+        for (int i = 0; i < NIC; ++i) {
+          const int j = kb + crow0 + i * CRPI;
+          const int col = (int)fast_div((uint32_t)j, p.bs_div);
+          cok[i] = j < pool_prefix && j < kend && col < p.table_width;
+          ce[i] = table_row + col;
+          craw[i] = make_uint2(0u, 0u);
+        }
+        if (p.table_i64) {
+#pragma unroll
+          for (int i = 0; i < NIC; ++i)
+            if (cok[i]) craw[i] = reinterpret_cast<const uint2*>(p.table)[ce[i]];
+        } else {
+#pragma unroll
+          for (int i = 0; i < NIC; ++i)
+            if (cok[i]) craw[i].x = reinterpret_cast<const uint32_t*>(p.table)[ce[i]];
+        }
+        // As for 16-bit rows: a column at or past the table width keeps
+        // block id 0 (read as block 0, the TTS padding semantics).
+#pragma unroll
+        for (int i = 0; i < NIC; ++i) {
+          const int j = kb + crow0 + i * CRPI;
+          const int64_t bid = p.table_i64 ? (int64_t)(((uint64_t)craw[i].y << 32) | craw[i].x)
+                                          : (int64_t)(int32_t)craw[i].x;
+          if (j < pool_prefix && j < kend && bid >= 0 && bid < p.num_blocks) {
+            const int64_t off = bid * p.s_blk +
+                                (int64_t)fast_mod((uint32_t)j, p.bs_div) * p.s_slot +
+                                h * p.s_head + (lane % CCPR) * 16;
+            kc[i] = p.kp + off;
+            vc[i] = p.vp + off;
+          }
+        }
+      }
+    }
     const char* ka[NI];
     const char* va_[NI];
 #pragma unroll
@@ -366,6 +437,8 @@ __global__ __launch_bounds__(kVarlenThreads, 2) void varlen_attention_kernel(Var
       va_[i] = zero_row;
       if (j < kend) {
         if (kPaged && j < pool_prefix) {
+          // An FP8 pool row is staged by the code copy and its conversion.
+          if constexpr (kF8) continue;
           const int64_t bid = p.table_i64 ? (int64_t)(((uint64_t)braw[i].y << 32) | braw[i].x)
                                           : (int64_t)(int32_t)braw[i].x;
           if (bid >= 0 && bid < p.num_blocks) {
@@ -391,6 +464,16 @@ __global__ __launch_bounds__(kVarlenThreads, 2) void varlen_attention_kernel(Var
       for (int i = 0; i < NI; ++i) {
         dma16(ka[i], dst0 + i * 1024);
         dma16(va_[i], dst0 + TILE_B + i * 1024);
+      }
+    }
+    if constexpr (kF8) {
+      if (kb < pool_prefix) {
+        const uint32_t cdst = code_base + (uint32_t)(wave * NIC * 1024);
+#pragma unroll
+        for (int i = 0; i < NIC; ++i) {
+          dma16(kc[i], cdst + i * 1024);
+          dma16(vc[i], cdst + CODE_B + i * 1024);
+        }
       }
     }
   };
@@ -505,6 +588,35 @@ __global__ __launch_bounds__(kVarlenThreads, 2) void varlen_attention_kernel(Var
           asm volatile("" ::"v"(qreg[tt][ds].x), "v"(qreg[tt][ds].y), "v"(qreg[tt][ds].z),
                        "v"(qreg[tt][ds].w));
       asm volatile("" ::"v"(st_slot.x), "v"(st_slot.y));
+      // FP8 pool: convert this tile's pool rows from the code area into the
+      // stage (16-byte chunks at their swizzled positions), then free the
+      // code area for the next tile's copy below.
+      if constexpr (kF8) {
+        if (kb < cur.pool_prefix) {
+          char* const s_kt = s_kv + stage * 2 * TILE_B;
+          for (int e = tid; e < 2 * kKeyTile * CCPR; e += kVarlenThreads) {
+            const int is_v = e >= kKeyTile * CCPR ? 1 : 0;
+            const int rc = e - is_v * kKeyTile * CCPR;
+            const int r = rc / CCPR, c = rc % CCPR;
+            if (kb + r < cur.pool_prefix) {
+              const uint4 codes = lds_read16(s_code + is_v * CODE_B, r * D + c * 16);
+              const float sc = is_v ? p.v_scale : p.k_scale;
+              char* const dst = s_kt + is_v * TILE_B + r * ROWB;
+              float f[8];
+              ET::unpack(f8_dequant8<ET>(make_uint2(codes.x, codes.y)), f);
+#pragma unroll
+              for (int i = 0; i < 8; ++i) f[i] *= sc;
+              *reinterpret_cast<uint4*>(dst + (((2 * c) ^ swz<D>(r)) << 4)) = ET::pack(f);
+              ET::unpack(f8_dequant8<ET>(make_uint2(codes.z, codes.w)), f);
+#pragma unroll
+              for (int i = 0; i < 8; ++i) f[i] *= sc;
+              *reinterpret_cast<uint4*>(dst + (((2 * c + 1) ^ swz<D>(r)) << 4)) = ET::pack(f);
+            }
+          }
+          wait_lgkmcnt0();
+          __syncthreads();
+        }
+      }
       // The next tile (this item's tile t + 1, or the next item's first)
       // goes to the other stage.  A whole tile from k/v is issued in NI
       // pairs spread over the S^T loop below: issued back to back, its DMAs
@@ -759,9 +871,10 @@ __global__ __launch_bounds__(kVarlenThreads, 2) void varlen_attention_kernel(Var
 // Launch the persistent grid: per XCD, as many workgroups as the kernel
 // keeps resident on one XCD's CUs, or fewer when the XCD's item list (at
 // most items_per_xcd long) is shorter.
-template <bool kBF16, int D, int G, bool kCausal, bool kPaged, bool kOnce = false>
+template <bool kBF16, int D, int G, bool kCausal, bool kPaged, bool kOnce = false,
+          bool kF8 = false>
 static void launch_persistent(const VarlenParams& p, int64_t items_per_xcd, hipStream_t st) {
-  const auto kern = varlen_attention_kernel<kBF16, D, G, kCausal, kPaged, kOnce>;
+  const auto kern = varlen_attention_kernel<kBF16, D, G, kCausal, kPaged, kOnce, kF8>;
   // Resident workgroups per CU, queried once (a failed query is not cached:
   // the launch then assumes 1, which is correct but leaves slots idle).
   static std::atomic<int> cached{0};
@@ -786,7 +899,9 @@ static void launch_persistent(const VarlenParams& p, int64_t items_per_xcd, hipS
 
 template <bool kBF16, int D, int G, bool kCausal>
 static void launch_varlen_c(const VarlenParams& p, int64_t items_per_xcd, hipStream_t st) {
-  if (p.has_pool)
+  if (p.has_pool && p.kv_f8)
+    launch_persistent<kBF16, D, G, kCausal, true, false, true>(p, items_per_xcd, st);
+  else if (p.has_pool)
     launch_persistent<kBF16, D, G, kCausal, true>(p, items_per_xcd, st);
   else if (!kCausal && p.num_qblocks == 1)
     launch_persistent<kBF16, D, G, kCausal, false, true>(p, items_per_xcd, st);
@@ -825,102 +940,15 @@ static bool dispatch_varlen(int D, int G, const VarlenParams& p, bool causal,
   }
 }
 
-// ------------------------------------------------------- FP8 pool prefix
-// With an FP8 pool the attention kernel above reads the paged prefix from a
-// 16-bit copy: f8_prefix_gather_kernel dequantises, for every sequence s and
-// table column c < ceil(prefix_s / block_size) (prefix_s = k_len - q_len,
-// or k_len when every key comes from the pool), block table[s][c] into
-// workspace block s W + c, laid out [slot][kv head][d], and maps (s, c) to
-// it in a workspace table (-1 for an unmapped block or a column past the
-// prefix).  The copy holds code * scale rounded to the 16-bit type.  The
-// new rows are quantised into the FP8 pool by the store kernel after the
-// attention.
-struct F8GatherParams {
-  const char* kp;
-  const char* vp;
-  int64_t s_blk, s_slot, s_head;  // bytes of the FP8 pool
-  int32_t block_size, num_blocks, num_kv_heads, head_dim;
-  const void* table;
-  int64_t t_sb;
-  int32_t table_i64, table_width;
-  const int32_t* cu_q;
-  const int32_t* cu_k;
-  int32_t all_from_pool;  // k is NULL: every key comes from the pool
-  int32_t width;          // W, workspace columns per sequence
-  float k_scale, v_scale;
-  int32_t* out_table;     // [num_seqs, W]
-  char* out_k;            // [num_seqs W, block_size, num_kv_heads, head_dim]
-  char* out_v;
-};
-
-template <typename ET>
-__global__ __launch_bounds__(256) void f8_prefix_gather_kernel(F8GatherParams g) {
-  const int c = blockIdx.x;
-  const int s = blockIdx.y;
-  const int ql = g.cu_q[s + 1] - g.cu_q[s];
-  const int kl = g.cu_k[s + 1] - g.cu_k[s];
-  const int prefix = g.all_from_pool ? kl : kl - ql;
-  const int64_t entry = (c * (int64_t)g.block_size < prefix)
-                            ? (c < g.table_width ? load_index(g.table, s * g.t_sb + c, g.table_i64)
-                                                 : 0)
-                            : -1;
-  const bool ok = entry >= 0 && entry < g.num_blocks;
-  const int64_t dst_blk = (int64_t)s * g.width + c;
-  if (threadIdx.x == 0) g.out_table[dst_blk] = ok ? (int32_t)dst_blk : -1;
-  if (!ok) return;
-  const int cpr = g.head_dim / 16;  // 16-code chunks per row
-  const int per = g.block_size * g.num_kv_heads * cpr;
-  const int64_t row_elems = (int64_t)g.num_kv_heads * g.head_dim;
-  for (int e = threadIdx.x; e < 2 * per; e += blockDim.x) {
-    const int is_v = e >= per;
-    const int r = is_v ? e - per : e;
-    const int ch = r % cpr;
-    const int head = (r / cpr) % g.num_kv_heads;
-    const int slot = r / (cpr * g.num_kv_heads);
-    const uint4 codes = ld16((is_v ? g.vp : g.kp) + entry * g.s_blk + slot * g.s_slot +
-                             head * g.s_head + ch * 16);
-    const float sc = is_v ? g.v_scale : g.k_scale;
-    char* dst = (is_v ? g.out_v : g.out_k) +
-                ((dst_blk * g.block_size + slot) * row_elems + (int64_t)head * g.head_dim +
-                 ch * 16) * 2;
-    float f[8];
-    ET::unpack(f8_dequant8<ET>(make_uint2(codes.x, codes.y)), f);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) f[i] *= sc;
-    st16(dst, ET::pack(f));
-    ET::unpack(f8_dequant8<ET>(make_uint2(codes.z, codes.w)), f);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) f[i] *= sc;
-    st16(dst + 16, ET::pack(f));
-  }
-}
-
-struct F8Layout {
-  int64_t width;  // W
-  size_t table_bytes, block_bytes, total;
-};
-
-// Workspace of the FP8 prefix copy (zero when the call reads no FP8 pool).
-static F8Layout f8_layout(const va_varlen_args* a) {
-  F8Layout l{};
-  if (a->pool.k == nullptr || a->pool.kv_format != VA_KV_FP8_E4M3 || a->block_tables == nullptr ||
-      a->pool.block_size <= 0 || a->num_seqs <= 0 || a->max_seqlen_k <= 0)
-    return l;
-  l.width = (a->max_seqlen_k + a->pool.block_size - 1) / a->pool.block_size;
-  const size_t blocks = (size_t)a->num_seqs * (size_t)l.width;
-  l.table_bytes = (blocks * 4 + 255) / 256 * 256;
-  l.block_bytes = blocks * (size_t)a->pool.block_size * a->num_kv_heads * a->head_dim * 2;
-  l.total = l.table_bytes + 2 * l.block_bytes;
-  return l;
-}
-
 static int varlen_native(const va_varlen_args* a, void* stream);
 
 }  // namespace va
 
+// No launch needs a workspace: an FP8 pool's prefix rows are converted
+// inside the attention kernel, tile by tile.
 extern "C" size_t va_varlen_workspace_bytes(const va_varlen_args* a) {
-  if (a == nullptr || a->struct_size != sizeof(va_varlen_args)) return 0;
-  return va::f8_layout(a).total;
+  (void)a;
+  return 0;
 }
 
 extern "C" int va_varlen_attention(const va_varlen_args* a, void* stream) {
@@ -937,86 +965,13 @@ extern "C" int va_varlen_attention(const va_varlen_args* a, void* stream) {
                "va_varlen_attention: unknown kv_format %d", a->pool.kv_format);
   if (!has_pool || a->pool.kv_format == VA_KV_NATIVE) return varlen_native(a, stream);
 
-  // ---- FP8 pool: dequantised prefix copy, attention over it, then the store ----
-  VA_CHECK_ARG(a->dtype == VA_BF16 || a->dtype == VA_F16,
-               "va_varlen_attention: dtype must be VA_BF16 or VA_F16 (MFMA path)");
-  VA_CHECK_ARG(a->pool.v && a->block_tables && a->pool.block_size > 0 && a->pool.num_blocks >= 0 &&
-                   a->table_width >= 0 && a->cu_seqlens_q && a->cu_seqlens_k,
-               "va_varlen_attention: incomplete pool description");
+  // ---- FP8 pool: attention with the prefix converted in the kernel, then
+  // the quantising store of the new rows ----
   VA_CHECK_ARG(a->pool.k_scale > 0.f && a->pool.v_scale > 0.f,
                "va_varlen_attention: FP8 pool scales must be positive");
-  VA_CHECK_ARG(a->head_dim % 16 == 0 && a->num_kv_heads > 0,
-               "va_varlen_attention: FP8 pool head_dim must be a multiple of 16");
-  VA_CHECK_ARG(a->max_seqlen_k > 0, "va_varlen_attention: an FP8 pool needs max_seqlen_k, the "
-                                    "bound of every k_len");
-  VA_CHECK_ARG(a->table_dtype == VA_I32 || a->table_dtype == VA_I64,
-               "va_varlen_attention: table_dtype");
-  const int64_t pstrides[] = {a->pool.stride_block, a->pool.stride_slot, a->pool.stride_head};
-  for (int64_t s : pstrides)
-    VA_CHECK_ARG(s % 16 == 0, "va_varlen_attention: FP8 pool strides must be 16-byte multiples");
-  VA_CHECK_ARG((uintptr_t)a->pool.k % 16 == 0 && (uintptr_t)a->pool.v % 16 == 0,
-               "va_varlen_attention: pointers must be 16-byte aligned");
-  const F8Layout lay = f8_layout(a);
-  VA_CHECK_ARG(lay.width <= 65535 && a->num_seqs <= 65535,
-               "va_varlen_attention: max_seqlen_k / block_size too large for the FP8 prefix copy");
-  if (a->workspace == nullptr || a->workspace_bytes < lay.total) {
-    set_error("va_varlen_attention: workspace of %zu bytes needed for the FP8 prefix copy, %zu "
-              "given",
-              lay.total, a->workspace_bytes);
-    return VA_ERR_WORKSPACE;
-  }
-  VA_CHECK_ARG((uintptr_t)a->workspace % 16 == 0, "va_varlen_attention: workspace alignment");
-  char* ws = (char*)a->workspace;
-  F8GatherParams g;
-  g.kp = (const char*)a->pool.k;
-  g.vp = (const char*)a->pool.v;
-  g.s_blk = a->pool.stride_block;
-  g.s_slot = a->pool.stride_slot;
-  g.s_head = a->pool.stride_head;
-  g.block_size = a->pool.block_size;
-  g.num_blocks = a->pool.num_blocks;
-  g.num_kv_heads = a->num_kv_heads;
-  g.head_dim = a->head_dim;
-  g.table = a->block_tables;
-  g.t_sb = a->table_stride_seq;
-  g.table_i64 = a->table_dtype == VA_I64;
-  g.table_width = a->table_width;
-  g.cu_q = a->cu_seqlens_q;
-  g.cu_k = a->cu_seqlens_k;
-  g.all_from_pool = a->k == nullptr;
-  g.width = (int32_t)lay.width;
-  g.k_scale = a->pool.k_scale;
-  g.v_scale = a->pool.v_scale;
-  g.out_table = (int32_t*)ws;
-  g.out_k = ws + lay.table_bytes;
-  g.out_v = ws + lay.table_bytes + lay.block_bytes;
-  const hipStream_t st = (hipStream_t)stream;
-  const dim3 grid((unsigned)lay.width, (unsigned)a->num_seqs);
-  if (a->dtype == VA_BF16)
-    hipLaunchKernelGGL(f8_prefix_gather_kernel<BF16>, grid, dim3(256), 0, st, g);
-  else
-    hipLaunchKernelGGL(f8_prefix_gather_kernel<F16>, grid, dim3(256), 0, st, g);
-  int rc = check_launch("va_varlen_attention (FP8 prefix copy)");
-  if (rc != VA_OK) return rc;
-
   va_varlen_args b = *a;
-  b.pool.k = g.out_k;
-  b.pool.v = g.out_v;
-  b.pool.stride_block = (int64_t)a->pool.block_size * a->num_kv_heads * a->head_dim;
-  b.pool.stride_slot = (int64_t)a->num_kv_heads * a->head_dim;
-  b.pool.stride_head = a->head_dim;
-  b.pool.num_blocks = (int32_t)((int64_t)a->num_seqs * lay.width);
-  b.pool.kv_format = VA_KV_NATIVE;
-  b.block_tables = g.out_table;
-  b.table_dtype = VA_I32;
-  b.table_stride_seq = lay.width;
-  b.table_width = (int32_t)lay.width;
   b.slot_mapping = nullptr;
-  b.workspace = nullptr;
-  b.workspace_bytes = 0;
-  VA_CHECK_ARG((int64_t)a->num_seqs * lay.width <= INT32_MAX,
-               "va_varlen_attention: FP8 prefix copy too large");
-  rc = varlen_native(&b, stream);
+  int rc = varlen_native(&b, stream);
   if (rc != VA_OK || a->slot_mapping == nullptr) return rc;
 
   va_store_args sa{};
@@ -1063,12 +1018,20 @@ int va::varlen_native(const va_varlen_args* a, void* stream) {
                "va_varlen_attention: table_dtype");
   VA_CHECK_ARG(a->slot_mapping == nullptr || a->slot_dtype == VA_I32 || a->slot_dtype == VA_I64,
                "va_varlen_attention: slot_dtype");
+  // An FP8 pool holds one byte per element (its strides count bytes).
+  const bool f8 = has_pool && a->pool.kv_format == VA_KV_FP8_E4M3;
+  VA_CHECK_ARG(!f8 || a->head_dim % 16 == 0,
+               "va_varlen_attention: FP8 pool head_dim must be a multiple of 16");
+  const int64_t kv_eb = f8 ? 1 : 2;
   const int64_t strides[] = {a->q_stride_tok,  a->q_stride_head,      a->k_stride_tok,
                              a->k_stride_head, a->v_stride_tok,       a->v_stride_head,
-                             a->out_stride_tok, a->out_stride_head,   a->pool.stride_block,
-                             a->pool.stride_slot, a->pool.stride_head};
+                             a->out_stride_tok, a->out_stride_head};
   for (int64_t s : strides)
     VA_CHECK_ARG((s * 2) % 16 == 0, "va_varlen_attention: strides must be 16-byte multiples");
+  const int64_t pstrides[] = {a->pool.stride_block, a->pool.stride_slot, a->pool.stride_head};
+  for (int64_t s : pstrides)
+    VA_CHECK_ARG((s * kv_eb) % 16 == 0,
+                 "va_varlen_attention: pool strides must be 16-byte multiples");
   const uintptr_t ptrs[] = {(uintptr_t)a->q, (uintptr_t)a->k, (uintptr_t)a->v, (uintptr_t)a->out,
                             (uintptr_t)a->pool.k, (uintptr_t)a->pool.v};
   for (uintptr_t p : ptrs)
@@ -1114,9 +1077,12 @@ int va::varlen_native(const va_varlen_args* a, void* stream) {
   p.has_pool = has_pool;
   p.kp = (char*)a->pool.k;
   p.vp = (char*)a->pool.v;
-  p.s_blk = a->pool.stride_block * 2;
-  p.s_slot = a->pool.stride_slot * 2;
-  p.s_head = a->pool.stride_head * 2;
+  p.s_blk = a->pool.stride_block * kv_eb;
+  p.s_slot = a->pool.stride_slot * kv_eb;
+  p.s_head = a->pool.stride_head * kv_eb;
+  p.kv_f8 = f8;
+  p.k_scale = f8 ? a->pool.k_scale : 1.0f;
+  p.v_scale = f8 ? a->pool.v_scale : 1.0f;
   p.block_size = has_pool ? a->pool.block_size : 1;
   p.num_blocks = a->pool.num_blocks;
   p.table = a->block_tables;

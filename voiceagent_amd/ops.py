@@ -413,6 +413,24 @@ def decode_workspace(device: torch.device, nbytes: int, floor: int = 0,
     return ws
 
 
+# Stream of the last no_alloc decode per device (their scratch buffer is
+# shared by every stream of a GPU).
+_NOALLOC_STREAM: dict[int, torch.cuda.Stream] = {}
+
+
+def _order_noalloc(index: int) -> None:
+    """Order a no_alloc decode after the previous one on its GPU when they
+    run on different streams: the current stream waits (on the GPU) for the
+    other.  Skipped under graph capture, where a wait on work outside the
+    capture is not allowed."""
+    cur = torch.cuda.current_stream(index)
+    prev = _NOALLOC_STREAM.get(index)
+    if (prev is not None and prev.cuda_stream != cur.cuda_stream
+            and not torch.cuda.is_current_stream_capturing()):
+        cur.wait_stream(prev)
+    _NOALLOC_STREAM[index] = cur
+
+
 def reserve_decode_workspace(device: torch.device, num_heads: int, num_kv_heads: int,
                              head_dim: int, stream: torch.cuda.Stream | None = None) -> None:
     """Allocate the decode workspace of `stream` (torch's current stream by
@@ -461,7 +479,12 @@ def paged_decode(
     kernel_seq_len / kernel_page_count bounds); the current row is written at
     len - 1 either way.  ``no_alloc`` launches va_paged_decode_noalloc, which
     keeps the split partials in the library's own scratch buffer instead of a
-    workspace; ``out`` must then be given, so that nothing is allocated.
+    workspace; ``out`` must then be given, so that nothing is allocated.  That
+    buffer is one per GPU, shared by every stream: no_alloc calls on two
+    streams would race on it, so a no_alloc call issued on another stream than
+    the previous one on its GPU first makes its stream wait for that stream
+    (on the GPU, outside graph capture; under capture the caller must order
+    them).
     An FP8 (float8_e4m3fn) pool is read as code * k_scale / v_scale, and the
     current row is stored into it quantised.  ``split_tokens``: 0 splits
     contexts automatically; ``SPLIT_EXACT`` does too, for a ``max_seq_len``
@@ -562,6 +585,7 @@ def paged_decode(
     index = _device_index(device)
     with _current(index):  # the split plan depends on the device's CU count
         if no_alloc:
+            _order_noalloc(index)
             N.check("va_paged_decode_noalloc",
                     lib.va_paged_decode_noalloc(ctypes.byref(args), _raw_stream(index)))
             return out
@@ -603,10 +627,11 @@ def varlen_attention(
     ``k``/``v`` rows aligned with the queries (all from the pool if ``k`` is
     None).  ``slot_mapping`` fuses store_kvcache of k/v into the same launch.
     ``max_seqlen_q`` must be at least every q_len, as for flash-attn: it sizes
-    the launch, and query rows past it are not computed.  With an FP8 pool
-    (float8_e4m3fn codes, values code * k_scale / v_scale) ``max_seqlen_k``
-    must bound every k_len: the paged prefix is dequantised into a workspace
-    first.
+    the launch, and query rows past it are not computed.  ``max_seqlen_k`` is
+    not read: key ranges come from ``cu_seqlens_k``.  An FP8 pool
+    (float8_e4m3fn codes, values code * k_scale / v_scale) is converted tile
+    by tile inside the kernel (no workspace); its new rows are stored
+    quantised after the attention.
     """
     fast = _FAST if _FAST_LOADED else _fast_calls()
     if (fast is not None and layout in (LAYOUT_NHD, LAYOUT_HND) and
@@ -685,12 +710,6 @@ def varlen_attention(
     lib = N.lib()
     index = _device_index(device)
     with _current(index):
-        if k_cache is not None and k_cache.dtype == FP8_KV_DTYPE:
-            nbytes = lib.va_varlen_workspace_bytes(ctypes.byref(args))
-            ws = decode_workspace(device, nbytes, kind="varlen")
-            if ws is not None:
-                args.workspace = ws.data_ptr()
-                args.workspace_bytes = ws.numel()
         N.check("va_varlen_attention",
                 lib.va_varlen_attention(ctypes.byref(args), _raw_stream(index)))
     return out
