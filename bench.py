@@ -554,9 +554,49 @@ def bench_prologue(args, dev, stream, dec):
         for i in range(layers):
             ops.qk_norm_rope(qp[i], kp[i], ppros[i], q_out=qpo[i], k_out=kpo[i])
 
+    # Config 3's prefill (fused store into a block-16 pool) with the prologue:
+    # the keys through the standalone kernel and the queries normalised and
+    # rotated inside the varlen launch, against the standalone kernel over q
+    # and k followed by the varlen launch.
+    vp_ = torch.randn(layers, total, hkv, d, generator=g, device=dev).to(torch.bfloat16)
+    cu = torch.zeros(len(lens) + 1, dtype=torch.int32)
+    cu[1:] = torch.cumsum(torch.tensor(lens, dtype=torch.int32), 0)
+    cu = cu.to(dev)
+    bs = workloads.BLOCK
+    nb = sum(math.ceil(n / bs) for n in lens) + 8
+    perm = torch.randperm(nb, generator=torch.Generator().manual_seed(12)).tolist()
+    rows, cur, slots = [], 0, []
+    for n in lens:
+        m = math.ceil(n / bs)
+        rows.append(perm[cur:cur + m] + [-1] * (max(math.ceil(x / bs) for x in lens) - m))
+        slots += [perm[cur + t // bs] * bs + t % bs for t in range(n)]
+        cur += m
+    table = torch.tensor(rows, dtype=torch.int32, device=dev)
+    slots = torch.tensor(slots, dtype=torch.int32, device=dev)
+    kpool = torch.zeros(layers, nb, bs, hkv, d, dtype=torch.bfloat16, device=dev)
+    vpool = torch.zeros_like(kpool)
+    pout = torch.empty_like(qp)
+
+    def prefill_call(i, q, k, prologue=None):
+        ops.varlen_attention(q, k, vp_[i], cu, cu, max(lens), max(lens), scale=d ** -0.5,
+                             causal=True, k_cache=kpool[i], v_cache=vpool[i], block_tables=table,
+                             slot_mapping=slots, out=pout[i], prologue=prologue)
+
+    def prefill_two_launch():
+        for i in range(layers):
+            ops.qk_norm_rope(qp[i], kp[i], ppros[i], q_out=qpo[i], k_out=kpo[i])
+            prefill_call(i, qpo[i], kpo[i])
+
+    def prefill_fused():
+        for i in range(layers):
+            ops.qk_norm_rope(None, kp[i], ppros[i], k_out=kpo[i])
+            prefill_call(i, qp[i], kpo[i], ppros[i])
+
     res = {}
-    for name, fn in (("fused", fused), ("two_launch", two_launch), ("prefill", prefill_prologue)):
-        ms, _ = timed_graph(fn, args.steps, args.warmup, stream)
+    for name, fn in (("fused", fused), ("two_launch", two_launch), ("prefill", prefill_prologue),
+                     ("prefill_two_launch", prefill_two_launch),
+                     ("prefill_fused", prefill_fused)):
+        ms, _ = timed_graph(fn, args.steps, args.warmup, stream, name=f"prologue_{name}")
         res[name] = ms * 1000.0 / layers
     # q and k rows read and written, the positions and each token's cos | sin row.
     pbytes = total * (hq + hkv) * d * 2 * 2 + total * (8 + d * 4)
@@ -565,14 +605,22 @@ def bench_prologue(args, dev, stream, dec):
         f"two launches {res['two_launch']:.2f} us/layer; standalone over config 3's "
         f"{total} prompt tokens {res['prefill']:.2f} us/layer ({pgbs:.0f} GB/s of "
         f"{pbytes / 1e6:.1f} MB)")
-    del qp, kp, qpo, kpo
+    log(f"[prologue] config 3 prefill with the prologue: fused (keys alone, queries in the "
+        f"varlen launch) {res['prefill_fused']:.2f} us/layer, two launches "
+        f"{res['prefill_two_launch']:.2f} us/layer")
+    del qp, kp, qpo, kpo, vp_, kpool, vpool, pout
     return {"fused_us_per_layer": round(res["fused"], 2),
             "two_launch_us_per_layer": round(res["two_launch"], 2),
             "prefill_cfg3_us_per_layer": round(res["prefill"], 2),
             "prefill_cfg3_gbs": round(pgbs, 1), "prefill_cfg3_bytes": pbytes,
+            "prefill_cfg3_with_prologue_fused_us_per_layer": round(res["prefill_fused"], 2),
+            "prefill_cfg3_with_prologue_two_launch_us_per_layer":
+                round(res["prefill_two_launch"], 2),
             "config": "cfg2 decode step (B=32, 28 layers) with Qwen3 q/k RMSNorm + RoPE "
                       "applied to the raw projections; the standalone kernel alone over "
-                      "config 3's prompts"}
+                      "config 3's prompts; config 3's prefill (fused store) with the "
+                      "prologue: keys through the standalone kernel and queries in the "
+                      "varlen launch, or both through the standalone kernel first"}
 
 
 MAX_MODEL_LEN = 65536  # max_position_embeddings of the decoder (qwen_asr_vllm/config.py:71)

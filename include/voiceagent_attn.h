@@ -39,7 +39,7 @@
 extern "C" {
 #endif
 
-#define VA_ATTN_ABI_VERSION 5
+#define VA_ATTN_ABI_VERSION 6
 
 /* status codes */
 #define VA_OK 0
@@ -297,11 +297,20 @@ typedef struct va_varlen_args {
    * new rows are stored quantised after the attention. */
   void* workspace;
   size_t workspace_bytes;
+  /* Optional Qwen3 query prologue (NULL: q is used as given).  When set, q
+   * holds the raw query projections: each query row is normalised with
+   * q_norm_weight and rotated at positions[token] (one position per query
+   * token, [total_q]) inside the launch, with the arithmetic of
+   * va_qk_norm_rope; k and the pool must already hold normalised, rotated
+   * keys (va_qk_norm_rope with num_heads = 0 does the keys alone).  Causal
+   * launches with head_dim 128; k_norm_weight is not read. */
+  const va_qk_prologue* prologue;
 } va_varlen_args;
 
 /* Variable-length attention over packed sequences: causal with bottom-right
- * alignment (prefill, optionally over a paged prefix and with the store
- * fused), or non-causal block-diagonal (audio encoder windows). */
+ * alignment (prefill, optionally over a paged prefix, with the store and the
+ * Qwen3 query prologue fused), or non-causal block-diagonal (audio encoder
+ * windows). */
 int va_varlen_attention(const va_varlen_args* args, void* stream);
 
 /* Bytes of workspace va_varlen_attention needs: always 0 (kept for callers

@@ -27,7 +27,7 @@ def test_header_functions_are_exported():
     assert declared == set(N.SIGNATURES), declared ^ set(N.SIGNATURES)
     for name in declared:
         assert hasattr(lib, name), name
-    assert lib.va_abi_version() == 5
+    assert lib.va_abi_version() == N.ABI_VERSION == 6
 
 
 @pytest.mark.parametrize(

@@ -49,13 +49,14 @@ def _prologue_inputs(T, hq, hkv, d, dtype, seed, max_pos=4096):
 
 # T = 257 spreads each token's rows over several waves; T = 4096 takes one
 # wave per token, with 72 rows in three chunks of loads (Hq 64) or a row group
-# holding both query and key rows (Hq 6).
+# holding both query and key rows (Hq 10), or, with at most 8 rows per token
+# (Hq 6 + Hkv 2), several tokens per wave.
 @pytest.mark.parametrize("dtype,hq,hkv,d,T", [
     (torch.bfloat16, 16, 8, 128, 257), (torch.float16, 16, 8, 128, 257),
     (torch.float32, 16, 8, 128, 257), (torch.bfloat16, 14, 14, 64, 257),
     (torch.bfloat16, 4, 1, 256, 257), (torch.bfloat16, 16, 8, 128, 4096),
-    (torch.bfloat16, 64, 8, 128, 4096), (torch.bfloat16, 6, 2, 128, 4096),
-    (torch.float32, 6, 2, 64, 4096)])
+    (torch.bfloat16, 64, 8, 128, 4096), (torch.bfloat16, 10, 2, 128, 4096),
+    (torch.bfloat16, 6, 2, 128, 4096), (torch.float32, 6, 2, 64, 4096)])
 def test_qk_norm_rope_matches_oracle(dev, dtype, hq, hkv, d, T):
     q, k, wq, wk, pos, cs = _prologue_inputs(T, hq, hkv, d, dtype, seed=d + hq)
     print(f"qk_norm_rope {dtype} T={T} Hq={hq} Hkv={hkv} D={d}", flush=True)
@@ -71,6 +72,30 @@ def test_qk_norm_rope_matches_oracle(dev, dtype, hq, hkv, d, T):
             print(f"  {name}: {exact:.4%} bit-exact, {nbad} beyond 1 ulp", flush=True)
             assert nbad == 0, name
             assert exact > 0.95, name
+
+
+@pytest.mark.parametrize("dtype,d,T", [
+    (torch.bfloat16, 128, 4099), (torch.float16, 64, 4097), (torch.float32, 128, 8561),
+    (torch.bfloat16, 256, 4097)])
+def test_keys_alone_take_several_tokens_per_wave(dev, dtype, d, T):
+    # 8 key heads and no query heads, at prompt size: each lane group of a
+    # wave takes its own token (T leaves the last wave lanes past the end,
+    # which store nothing).  The keys must be the bits that the kernel taking
+    # one token per wave gives beside 16 query heads, and meet the oracle.
+    q, k, wq, wk, pos, cs = _prologue_inputs(T, 16, 8, d, dtype, seed=T + d)
+    print(f"keys alone {dtype} T={T} D={d}", flush=True)
+    pro = ops.QKPrologue(wq.to(dev), wk.to(dev), 1e-6, cs.to(dev), pos.to(dev))
+    qd, kd = q.to(dev), k.to(dev)
+    alone = torch.full_like(kd, float("nan"))
+    assert ops.qk_norm_rope(None, kd, pro, k_out=alone)[0] is None
+    _, both = ops.qk_norm_rope(qd, kd, pro)
+    torch.cuda.synchronize()
+    assert torch.equal(alone, both)
+    _, rk = oracle.qk_norm_rope(q, k, pos, wq, wk, 1e-6, cs)
+    if dtype == torch.float32:
+        assert (alone.cpu() - rk).abs().max().item() <= 1e-5
+    else:
+        assert _close_16bit(alone, rk, dtype)[0] == 0
 
 
 def test_qk_norm_rope_in_place_and_strided(dev):
@@ -184,3 +209,113 @@ def test_fused_prologue_equals_two_launch_path_bitwise(dev, B):
     torch.cuda.synchronize()
     assert torch.equal(out1, out2)
     assert torch.equal(kp1, kp2) and torch.equal(vp1, vp2)
+
+
+def _prefill_case(seed, paged):
+    """Prompts (some continuing a paged prefix), raw q/k projections, random
+    per-token positions (not the key index: the launch must read them)."""
+    g = torch.Generator().manual_seed(seed)
+    hq, hkv, d, bs = 16, 8, 128, 16
+    qlens = [50, 1, 130, 257, 64, 3]
+    prefix = [0, 16, 37, 0, 200, 5] if paged else [0] * len(qlens)
+    klens = [p + n for p, n in zip(prefix, qlens)]
+    T = sum(qlens)
+    q, k, wq, wk, pos, cs = _prologue_inputs(T, hq, hkv, d, torch.bfloat16, seed=seed)
+    v = torch.randn(T, hkv, d, generator=g).to(torch.bfloat16)
+    cu_q = torch.tensor([0] + list(torch.tensor(qlens).cumsum(0)), dtype=torch.int32)
+    cu_k = torch.tensor([0] + list(torch.tensor(klens).cumsum(0)), dtype=torch.int32)
+    case = dict(q=q, k=k, v=v, wq=wq, wk=wk, pos=pos, cs=cs, cu_q=cu_q, cu_k=cu_k, qlens=qlens,
+                klens=klens, d=d)
+    if paged:
+        need = [-(-n // bs) for n in klens]
+        nb = sum(need) + 4
+        perm = torch.randperm(nb, generator=g).tolist()
+        rows, cur, slots = [], 0, []
+        for pfx, kl, n in zip(prefix, klens, need):
+            row = perm[cur:cur + n]
+            cur += n
+            rows.append(row + [-1] * (max(need) - n))
+            slots += [row[p // bs] * bs + p % bs for p in range(pfx, kl)]
+        case.update(table=torch.tensor(rows, dtype=torch.int32),
+                    slots=torch.tensor(slots, dtype=torch.int32),
+                    kp=torch.randn(nb, bs, hkv, d, generator=g).to(torch.bfloat16),
+                    vp=torch.randn(nb, bs, hkv, d, generator=g).to(torch.bfloat16))
+    return case
+
+
+def _run_prefill(c, dev, q, k, prologue=None):
+    kw = dict(scale=c["d"] ** -0.5, causal=True, prologue=prologue)
+    if "kp" in c:
+        kp, vp = c["kp"].to(dev), c["vp"].to(dev)
+        out = ops.varlen_attention(q, k, c["v"].to(dev), c["cu_q"].to(dev), c["cu_k"].to(dev),
+                                   max(c["qlens"]), max(c["klens"]), k_cache=kp, v_cache=vp,
+                                   block_tables=c["table"].to(dev),
+                                   slot_mapping=c["slots"].to(dev), **kw)
+        return out, kp, vp
+    out = ops.varlen_attention(q, k, c["v"].to(dev), c["cu_q"].to(dev), c["cu_k"].to(dev),
+                               max(c["qlens"]), max(c["klens"]), **kw)
+    return out, None, None
+
+
+@pytest.mark.parametrize("paged", [True, False])
+def test_fused_prefill_query_prologue_matches_oracle(dev, paged):
+    # The launch normalises and rotates q itself; the keys go through the
+    # standalone kernel alone (num_heads = 0).
+    c = _prefill_case(40 + paged, paged)
+    pro = ops.QKPrologue(c["wq"].to(dev), c["wk"].to(dev), 1e-6, c["cs"].to(dev),
+                         c["pos"].to(dev))
+    _, kn = ops.qk_norm_rope(None, c["k"].to(dev), pro)
+    q2, k2 = ops.qk_norm_rope(c["q"].to(dev), c["k"].to(dev), pro)
+    torch.cuda.synchronize()
+    assert torch.equal(kn, k2)  # the same per-row code for the keys
+    print(f"fused prefill prologue, paged={paged}", flush=True)
+    out, kp, vp = _run_prefill(c, dev, c["q"].to(dev), kn, prologue=pro)
+    ref_two, kp2, vp2 = _run_prefill(c, dev, q2, k2)
+    torch.cuda.synchronize()
+    rq, rk = oracle.qk_norm_rope(c["q"], c["k"], c["pos"], c["wq"], c["wk"], 1e-6, c["cs"])
+    if paged:
+        # The fused store wrote the processed keys (identical in both paths).
+        assert torch.equal(kp, kp2) and torch.equal(vp, vp2)
+        ek, ev = oracle.store_kvcache(rk, c["v"], c["kp"], c["vp"], c["slots"])
+        ref = oracle.varlen_attention(rq, rk, c["v"], c["cu_q"], c["cu_k"], c["d"] ** -0.5, True,
+                                      k_cache=c["kp"], v_cache=c["vp"], block_tables=c["table"])
+        assert (kp.cpu() - ek).abs().max().item() <= 2 * 2.0 ** -7 * ek.abs().max().item()
+    else:
+        ref = oracle.varlen_attention(rq, rk, c["v"], c["cu_q"], c["cu_k"], c["d"] ** -0.5, True)
+    err = (out.float().cpu() - ref).abs().max().item()
+    two = (out.float() - ref_two.float()).abs().max().item()
+    print(f"  max-abs vs oracle {err:.3e}, vs two-launch path {two:.3e}", flush=True)
+    assert err <= 2e-2
+    assert two <= 2e-2
+
+
+def test_qwen3_core_prefill_with_the_query_prologue_fused(dev):
+    # With varlen_fuse_prologue set, the layer routes a prefill batch through
+    # the fused launch: same result as the layer with the prologue unfused
+    # (the default: standalone kernel over q and k).
+    from voiceagent_amd.layers.context import AttentionContext, attention_context
+    from voiceagent_amd.layers.qwen3 import Qwen3AttentionCore
+
+    c = _prefill_case(44, True)
+    layers = []
+    for fuse in (True, False):
+        layer = Qwen3AttentionCore(16, 128, 8, max_position=4096).to(dev)
+        with torch.no_grad():
+            layer.q_norm_weight.copy_(c["wq"].float())
+            layer.k_norm_weight.copy_(c["wk"].float())
+        layer.q_norm_weight.data = layer.q_norm_weight.data.to(torch.bfloat16)
+        layer.k_norm_weight.data = layer.k_norm_weight.data.to(torch.bfloat16)
+        layer.cos_sin_cache = c["cs"].to(dev)
+        layer.k_cache, layer.v_cache = c["kp"].to(dev), c["vp"].to(dev)
+        layer.varlen_fuse_prologue = fuse
+        layers.append(layer)
+    ctx = AttentionContext(cu_seqlens_q=c["cu_q"].to(dev), cu_seqlens_k=c["cu_k"].to(dev),
+                           max_seqlen_q=max(c["qlens"]), max_seqlen_k=max(c["klens"]),
+                           slot_mapping=c["slots"].to(dev), block_tables=c["table"].to(dev))
+    outs = []
+    with attention_context(ctx):
+        for layer in layers:
+            outs.append(layer(c["pos"].to(dev), c["q"].to(dev), c["k"].to(dev), c["v"].to(dev)))
+    torch.cuda.synchronize()
+    assert (outs[0].float() - outs[1].float()).abs().max().item() <= 2e-2
+    assert torch.equal(layers[0].k_cache, layers[1].k_cache)

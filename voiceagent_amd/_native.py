@@ -21,7 +21,7 @@ VA_BF16, VA_F16, VA_F32 = 0, 1, 2
 VA_I32, VA_I64 = 0, 1
 VA_LENS_PER_SEQ, VA_LENS_CUMULATIVE = 0, 1
 VA_KV_NATIVE, VA_KV_FP8_E4M3 = 0, 1
-ABI_VERSION = 5  # VA_ATTN_ABI_VERSION of the header these structs mirror
+ABI_VERSION = 6  # VA_ATTN_ABI_VERSION of the header these structs mirror
 DECODE_NOALLOC_SCRATCH_BYTES = 4 << 20  # VA_DECODE_NOALLOC_SCRATCH_BYTES
 VA_SPLIT_EXACT = -1  # split_tokens: automatic split, max_seq_len exact
 
@@ -189,6 +189,7 @@ class VarlenArgs(ctypes.Structure):
         ("slot_dtype", c_int32),
         ("workspace", c_void_p),
         ("workspace_bytes", c_size_t),
+        ("prologue", ctypes.POINTER(QkPrologue)),
     ]
 
 

@@ -121,6 +121,14 @@ __device__ inline void convert_weights(const WeightRaw<E>& r, int dtype, float (
   }
 }
 
+// Norm weight i of a weight array of `dtype`, widened to float.
+__device__ inline float load_weight(const void* w, int dtype, int i) {
+  if (dtype == VA_F32) return reinterpret_cast<const float*>(w)[i];
+  const uint32_t u = reinterpret_cast<const uint16_t*>(w)[i];
+  if (dtype == VA_BF16) return __uint_as_float(u << 16);
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)u);
+}
+
 // The cos / sin factors of this lane's slice at `pos` (col = lane's index in
 // its row of LPR lanes).  The sin factors of the row's first half come
 // negated: element i < D/2 rotates to x_i cos - x_(i+D/2) sin, and

@@ -1,8 +1,9 @@
 // Standalone Qwen3 q/k prologue: RMSNorm + half-split rotary embedding of
 // every query and key head row of a batch of tokens (the prefill side of
 // Qwen3Attention.forward, qwen_asr_vllm/models/qwen3.py:42-48; the decode side
-// is fused into the paged decode kernel).  One wave per token, one group of
-// LPR lanes per head row; the per-row math lives in prologue.h.
+// is fused into the paged decode kernel).  One group of LPR lanes per head
+// row, a token's rows over one or more waves (or, with few rows per token,
+// several tokens per wave); the per-row math lives in prologue.h.
 #include <algorithm>
 
 #include "prologue.h"
@@ -99,12 +100,74 @@ __global__ __launch_bounds__(kQkThreads) void qk_norm_rope_kernel(QkParams p) {
   }
 }
 
+// Few head rows per token (at most kQkChunk, as for keys alone): a wave takes
+// RPW tokens, one per LPR-lane group, and every head row of them, all of its
+// row loads in flight at once.  A token per wave would leave each wave a
+// kilobyte or two behind two dependent round trips (position, then rotary);
+// over config 3's 8561 prompt tokens, 8 key heads of 128, that layout took
+// 15.0 us.  Each lane loads the position and rotary slice of its own token;
+// lanes past the last token read it and store nothing.
+template <typename ET, int D>
+__global__ __launch_bounds__(kQkThreads) void qk_norm_rope_tokens_kernel(QkParams p) {
+  constexpr int E = ET::kPerVec;
+  constexpr int LPR = D / E;
+  constexpr int RPW = 64 / LPR;  // tokens per wave
+  static_assert(LPR >= 2 && LPR <= 64 && 64 % LPR == 0, "unsupported head_dim");
+  const int lane = threadIdx.x & 63;
+  const int col = lane % LPR;
+  const int64_t w = (int64_t)blockIdx.x * (kQkThreads / 64) + threadIdx.x / 64;
+  if (w * RPW >= p.num_tokens) return;  // whole waves
+  const int64_t tok_raw = w * RPW + lane / LPR;
+  const bool live = tok_raw < p.num_tokens;
+  const int64_t tok = live ? tok_raw : p.num_tokens - 1;
+  const int heads = p.hq + p.hkv;  // <= kQkChunk (host)
+  int64_t pos = load_index(p.pp.pos, tok, p.pp.pos_i64);
+  const WeightRaw<E> wqr = load_weights_raw<E>(p.hq > 0 ? p.pp.q_w : p.pp.k_w, p.pp.w_dtype, col * E);
+  const WeightRaw<E> wkr = load_weights_raw<E>(p.hkv > 0 ? p.pp.k_w : p.pp.q_w, p.pp.w_dtype, col * E);
+  const char* const qrow = p.q + tok * p.q_st + col * 16;
+  const char* const krow = p.k + tok * p.k_st + col * 16;
+  char* const qdst = p.qo + tok * p.qo_st + col * 16;
+  char* const kdst = p.ko + tok * p.ko_st + col * 16;
+  uint4 raw[kQkChunk];
+#pragma unroll
+  for (int j = 0; j < kQkChunk; ++j) {
+    const int hh = j < heads ? j : heads - 1;
+    raw[j] = ld16_nt(hh < p.hq ? qrow + hh * p.q_sh : krow + (int64_t)(hh - p.hq) * p.k_sh);
+  }
+  pos = pos < 0 ? 0 : (pos >= p.pp.max_pos ? p.pp.max_pos - 1 : pos);
+  float c[E], s[E], wq[E], wk[E];
+  load_rotary<E, LPR>(p.pp, pos, col, D, c, s);
+  convert_weights<E>(wqr, p.pp.w_dtype, wq);
+  convert_weights<E>(wkr, p.pp.w_dtype, wk);
+#pragma unroll
+  for (int j = 0; j < kQkChunk; ++j) {
+    if (j >= heads) break;
+    const bool isq = j < p.hq;
+    float x[E], wv[E];
+    ET::unpack(raw[j], x);
+#pragma unroll
+    for (int e = 0; e < E; ++e) wv[e] = isq ? wq[e] : wk[e];
+    qk_prologue<ET, LPR, E>(x, wv, p.pp.eps, D, c, s);
+    if (live) st16_nt(isq ? qdst + j * p.qo_sh : kdst + (int64_t)(j - p.hq) * p.ko_sh, ET::pack(x));
+  }
+}
+
 template <typename ET>
 static bool launch_qk(int D, const QkParams& p, dim3 grid, hipStream_t st) {
   switch (D) {
     case 64: hipLaunchKernelGGL((qk_norm_rope_kernel<ET, 64>), grid, dim3(kQkThreads), 0, st, p); return true;
     case 128: hipLaunchKernelGGL((qk_norm_rope_kernel<ET, 128>), grid, dim3(kQkThreads), 0, st, p); return true;
     case 256: hipLaunchKernelGGL((qk_norm_rope_kernel<ET, 256>), grid, dim3(kQkThreads), 0, st, p); return true;
+    default: return false;
+  }
+}
+
+template <typename ET>
+static bool launch_qk_tokens(int D, const QkParams& p, dim3 grid, hipStream_t st) {
+  switch (D) {
+    case 64: hipLaunchKernelGGL((qk_norm_rope_tokens_kernel<ET, 64>), grid, dim3(kQkThreads), 0, st, p); return true;
+    case 128: hipLaunchKernelGGL((qk_norm_rope_tokens_kernel<ET, 128>), grid, dim3(kQkThreads), 0, st, p); return true;
+    case 256: hipLaunchKernelGGL((qk_norm_rope_tokens_kernel<ET, 256>), grid, dim3(kQkThreads), 0, st, p); return true;
     default: return false;
   }
 }
@@ -174,11 +237,29 @@ extern "C" int va_qk_norm_rope(const va_qk_norm_rope_args* a, void* stream) {
   p.pp.pos_i64 = pr.positions_dtype == VA_I64;
   p.pp.pos = pr.positions;
 
-  // Waves per token: enough for ~16 waves per CU when the batch is small
-  // (decode-sized), one per token when it is large.
   const int E = 16 / eb;
   const int rpw = 64 / (a->head_dim / E);
-  const int groups = (a->num_heads + a->num_kv_heads + rpw - 1) / rpw;
+  const int heads = a->num_heads + a->num_kv_heads;
+  const hipStream_t st = (hipStream_t)stream;
+  if (heads <= kQkChunk && a->num_tokens >= kQkTargetWaves) {
+    // Prompt-sized batches with few rows per token: RPW tokens per wave.
+    const int64_t waves = ((int64_t)a->num_tokens + rpw - 1) / rpw;
+    const dim3 grid((unsigned)((waves + kQkThreads / 64 - 1) / (kQkThreads / 64)));
+    bool ok = false;
+    switch (a->dtype) {
+      case VA_BF16: ok = launch_qk_tokens<BF16>(a->head_dim, p, grid, st); break;
+      case VA_F16: ok = launch_qk_tokens<F16>(a->head_dim, p, grid, st); break;
+      case VA_F32: ok = launch_qk_tokens<F32>(a->head_dim, p, grid, st); break;
+    }
+    if (!ok) {
+      set_error("va_qk_norm_rope: unsupported configuration");
+      return VA_ERR_UNSUPPORTED;
+    }
+    return check_launch("va_qk_norm_rope");
+  }
+  // Waves per token: enough for ~16 waves per CU when the batch is small
+  // (decode-sized), one per token when it is large.
+  const int groups = (heads + rpw - 1) / rpw;
   int wpt = (int)std::min<int64_t>(groups, std::max<int64_t>(1, (kQkTargetWaves + a->num_tokens - 1) / a->num_tokens));
   const int gpw = (groups + wpt - 1) / wpt;
   wpt = (groups + gpw - 1) / gpw;
@@ -188,7 +269,6 @@ extern "C" int va_qk_norm_rope(const va_qk_norm_rope_args* a, void* stream) {
   p.waves_per_token = wpt;
   p.groups_per_wave = gpw;
   const dim3 grid((unsigned)blocks);
-  const hipStream_t st = (hipStream_t)stream;
   bool ok = false;
   switch (a->dtype) {
     case VA_BF16: ok = launch_qk<BF16>(a->head_dim, p, grid, st); break;

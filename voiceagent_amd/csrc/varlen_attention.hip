@@ -35,6 +35,7 @@
 
 #include "common.h"
 #include "fastdiv.h"
+#include "prologue.h"
 
 namespace va {
 
@@ -72,6 +73,8 @@ struct VarlenParams {
   int32_t slot_small;       // num_blocks * block_size <= 2^31: slots divide in 32 bits
   float k_scale, v_scale;   // FP8 pool: element = code * scale
   int32_t kv_f8;            // the pool holds e4m3 codes (strides in bytes of codes)
+  int32_t has_pro;          // the Qwen3 query prologue runs on every query row
+  PrologueParams pro;
 };
 
 template <bool kBF16>
@@ -142,7 +145,12 @@ __device__ inline s16x4_t lds_read_tr(const char* base, int off) {
 // (every e4m3 value converts exactly; the product is rounded once), before
 // the next tile's copy may reuse the code area.  Rows from k/v are staged
 // as 16-bit rows, as without a pool.
-template <bool kBF16, int D, int G, bool kCausal, bool kPaged, bool kOnce, bool kF8 = false>
+//
+// kPro: q holds raw projections; each item's query rows are normalised and
+// rotated (Qwen3's q_norm + rotary_emb, prologue.h's arithmetic) in registers
+// at the item's first tile, with positions loaded beside the rows.
+template <bool kBF16, int D, int G, bool kCausal, bool kPaged, bool kOnce, bool kF8 = false,
+          bool kPro = false>
 __global__ __launch_bounds__(kVarlenThreads, 2) void varlen_attention_kernel(VarlenParams p) {
   constexpr int BQ = kRowsPerWG / G;       // query positions per workgroup
   constexpr int DS = D / 32;               // k-steps of the S^T MFMA
@@ -171,6 +179,9 @@ __global__ __launch_bounds__(kVarlenThreads, 2) void varlen_attention_kernel(Var
   constexpr int NIC = CODE_B / 1024 / 4;   // code DMA instructions per wave per tile, K or V
   static_assert(!kF8 || NIC * 4 * 1024 == CODE_B, "code DMA split");
   __shared__ __align__(1024) char s_code[kF8 ? 2 * CODE_B : 16];
+  // kPro: the query norm weights as fp32, written once per workgroup here and
+  // read by every item's prologue (the first tile's barrier orders them).
+  __shared__ __align__(16) float s_qw[kPro ? D : 4];
   using ET = std::conditional_t<kBF16, BF16, F16>;
 
   const int tid = threadIdx.x;
@@ -178,6 +189,9 @@ __global__ __launch_bounds__(kVarlenThreads, 2) void varlen_attention_kernel(Var
   const int lane = tid & 63;
   const int r16 = lane & 15;
   const int g4 = lane >> 4;
+  if constexpr (kPro) {
+    for (int i = tid; i < D; i += kVarlenThreads) s_qw[i] = load_weight(p.pro.q_w, p.pro.w_dtype, i);
+  }
 
   // ---- persistent schedule ----
   // Workgroup 8 j + x runs on XCD x (MI355X hands workgroup i of a launch to
@@ -482,12 +496,18 @@ __global__ __launch_bounds__(kVarlenThreads, 2) void varlen_attention_kernel(Var
   // Two 16-row tiles per wave: row 16 (2 wave + tt) + r16 of the block is
   // query position pos0 + row % BQ of head h G + row / BQ.
   uint4 qreg[2][DS];
+  // kPro: the rotary position of each of the lane's two query rows (the row
+  // of the item's last query for rows past the end, whose output is unused).
+  int64_t qrot[2] = {0, 0};
   auto load_q = [&](const Item& it) {
 #pragma unroll
     for (int tt = 0; tt < 2; ++tt) {
       const int row = 16 * (2 * wave + tt) + r16;
       const int qpos = it.pos0 + row % BQ;
       const int qhead = it.h * G + row / BQ;
+      if constexpr (kPro)
+        qrot[tt] = load_index(p.pro.pos, (int64_t)it.q0 + (qpos < it.ql ? qpos : it.ql - 1),
+                              p.pro.pos_i64);
 #pragma unroll
       for (int ds = 0; ds < DS; ++ds) {
         if (qpos < it.ql)
@@ -564,10 +584,14 @@ __global__ __launch_bounds__(kVarlenThreads, 2) void varlen_attention_kernel(Var
     float m[2] = {-1.0e30f, -1.0e30f};
     float l[2] = {0.f, 0.f};
     f32x4_t o[2][DT];
+    // With the query prologue the accumulators are zeroed after it, at the
+    // item's first tile, so they hold no registers while it runs.
+    if constexpr (!kPro) {
 #pragma unroll
-    for (int tt = 0; tt < 2; ++tt)
+      for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
-      for (int dt = 0; dt < DT; ++dt) o[tt][dt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        for (int dt = 0; dt < DT; ++dt) o[tt][dt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    }
 
     for (int t = 0; t < cur.ntiles; ++t) {
       const int kb = t * kKeyTile;
@@ -588,6 +612,98 @@ __global__ __launch_bounds__(kVarlenThreads, 2) void varlen_attention_kernel(Var
           asm volatile("" ::"v"(qreg[tt][ds].x), "v"(qreg[tt][ds].y), "v"(qreg[tt][ds].z),
                        "v"(qreg[tt][ds].w));
       asm volatile("" ::"v"(st_slot.x), "v"(st_slot.y));
+      // Qwen3 query prologue on the item's rows, in the B-operand layout:
+      // lane (r16, g4) holds elements 32 ds + 8 g4 + e of its row (ds < DS,
+      // e < 8), so element i < D/2 and its rotary partner i + D/2 sit in the
+      // same lane (ds and ds + DS/2), and a row's sum of squares is the sum
+      // over the four lanes r16 + 16 g4.  It runs before the next tile is
+      // requested: the compiler's wait for the cos / sin loads would
+      // otherwise also wait for that request.  Both rows' cos / sin are
+      // requested together (one round trip per item), into the registers
+      // the output accumulators take after this block; the weights come
+      // from LDS.
+      if constexpr (kPro) {
+        if (t == 0) {
+          static_assert(DS % 2 == 0, "rotary halves");
+          constexpr int HD = DS / 2;
+          f32x4_t cv[2][HD][2], sv[2][HD][2];
+#pragma unroll
+          for (int tt = 0; tt < 2; ++tt) {
+            int64_t P = qrot[tt];
+            P = P < 0 ? 0 : (P >= p.pro.max_pos ? p.pro.max_pos - 1 : P);
+            const float* crow = p.pro.cs + P * p.pro.cs_stride;
+#pragma unroll
+            for (int hh = 0; hh < HD; ++hh)
+#pragma unroll
+              for (int e4 = 0; e4 < 2; ++e4) {
+                cv[tt][hh][e4] = *reinterpret_cast<const f32x4_t*>(crow + 32 * hh + 8 * g4 + 4 * e4);
+                sv[tt][hh][e4] =
+                    *reinterpret_cast<const f32x4_t*>(crow + D / 2 + 32 * hh + 8 * g4 + 4 * e4);
+              }
+          }
+          // One row at a time, each called with a constant row index so that
+          // qreg and the factors stay in registers.
+          auto pro_row = [&](auto TT) {
+            constexpr int tt = decltype(TT)::value;
+            float x[DS][8];
+#pragma unroll
+            for (int ds = 0; ds < DS; ++ds) ET::unpack(qreg[tt][ds], x[ds]);
+            // The sum of squares in va_qk_norm_rope's order, so that the
+            // queries come out bit for bit as that kernel's do: there a lane
+            // holds one 8-element chunk c of the row (a fused multiply-add
+            // chain) and the 16 chunk sums meet in the tree
+            // ((c0 + c1) + (c2 + c3)) + ((c4 + c5) + (c6 + c7)) + ...  Here
+            // chunk c = 4 ds + g4 sits in lane g4 at ds: pairs (g4, g4 ^ 1)
+            // are lanes l, l ^ 16, quads lanes l ^ 32, and the rest is in
+            // the lane.
+            static_assert(DS == 4, "the standalone kernel's tree for head_dim 128");
+            float cs4[DS];
+#pragma unroll
+            for (int ds = 0; ds < DS; ++ds) {
+              cs4[ds] = 0.f;
+#pragma unroll
+              for (int e = 0; e < 8; ++e) cs4[ds] = fmaf(x[ds][e], x[ds][e], cs4[ds]);
+              cs4[ds] = sum_xor16(cs4[ds]);
+              cs4[ds] = sum_xor32(cs4[ds]);
+            }
+            const float ss = (cs4[0] + cs4[1]) + (cs4[2] + cs4[3]);
+            const float r = 1.0f / sqrtf(__fadd_rn(ss / (float)D, p.pro.eps));
+#pragma unroll
+            for (int ds = 0; ds < DS; ++ds) {
+#pragma unroll
+              for (int e = 0; e < 8; ++e) x[ds][e] = __fmul_rn(x[ds][e], r);
+              round_to<ET>(x[ds]);
+              const f32x4_t w0 = *reinterpret_cast<const f32x4_t*>(s_qw + 32 * ds + 8 * g4);
+              const f32x4_t w1 = *reinterpret_cast<const f32x4_t*>(s_qw + 32 * ds + 8 * g4 + 4);
+#pragma unroll
+              for (int e = 0; e < 8; ++e) x[ds][e] = __fmul_rn(x[ds][e], e < 4 ? w0[e] : w1[e - 4]);
+              round_to<ET>(x[ds]);
+            }
+            {
+              // Products rounded apart before their sum (no fused multiply-add).
+#pragma clang fp contract(off)
+#pragma unroll
+              for (int hh = 0; hh < HD; ++hh)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                  const float c = e < 4 ? cv[tt][hh][0][e] : cv[tt][hh][1][e - 4];
+                  const float sn = e < 4 ? sv[tt][hh][0][e] : sv[tt][hh][1][e - 4];
+                  const float a = x[hh][e], b2 = x[hh + HD][e];
+                  x[hh][e] = a * c - b2 * sn;
+                  x[hh + HD][e] = b2 * c + a * sn;
+                }
+            }
+#pragma unroll
+            for (int ds = 0; ds < DS; ++ds) qreg[tt][ds] = ET::pack(x[ds]);
+          };
+          pro_row(std::integral_constant<int, 0>{});
+          pro_row(std::integral_constant<int, 1>{});
+#pragma unroll
+          for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) o[tt][dt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        }
+      }
       // FP8 pool: convert this tile's pool rows from the code area into the
       // stage (16-byte chunks at their swizzled positions), then free the
       // code area for the next tile's copy below.
@@ -872,9 +988,9 @@ __global__ __launch_bounds__(kVarlenThreads, 2) void varlen_attention_kernel(Var
 // keeps resident on one XCD's CUs, or fewer when the XCD's item list (at
 // most items_per_xcd long) is shorter.
 template <bool kBF16, int D, int G, bool kCausal, bool kPaged, bool kOnce = false,
-          bool kF8 = false>
+          bool kF8 = false, bool kPro = false>
 static void launch_persistent(const VarlenParams& p, int64_t items_per_xcd, hipStream_t st) {
-  const auto kern = varlen_attention_kernel<kBF16, D, G, kCausal, kPaged, kOnce, kF8>;
+  const auto kern = varlen_attention_kernel<kBF16, D, G, kCausal, kPaged, kOnce, kF8, kPro>;
   // Resident workgroups per CU, queried once (a failed query is not cached:
   // the launch then assumes 1, which is correct but leaves slots idle).
   static std::atomic<int> cached{0};
@@ -899,6 +1015,17 @@ static void launch_persistent(const VarlenParams& p, int64_t items_per_xcd, hipS
 
 template <bool kBF16, int D, int G, bool kCausal>
 static void launch_varlen_c(const VarlenParams& p, int64_t items_per_xcd, hipStream_t st) {
+  // The fused query prologue: causal launches at head_dim 128 over a 16-bit
+  // pool or none (the host checks this before launching).
+  if constexpr (kCausal && D == 128) {
+    if (p.has_pro) {
+      if (p.has_pool)
+        launch_persistent<kBF16, D, G, true, true, false, false, true>(p, items_per_xcd, st);
+      else
+        launch_persistent<kBF16, D, G, true, false, false, false, true>(p, items_per_xcd, st);
+      return;
+    }
+  }
   if (p.has_pool && p.kv_f8)
     launch_persistent<kBF16, D, G, kCausal, true, false, true>(p, items_per_xcd, st);
   else if (p.has_pool)
@@ -1083,6 +1210,35 @@ int va::varlen_native(const va_varlen_args* a, void* stream) {
   p.kv_f8 = f8;
   p.k_scale = f8 ? a->pool.k_scale : 1.0f;
   p.v_scale = f8 ? a->pool.v_scale : 1.0f;
+  p.has_pro = a->prologue != nullptr;
+  p.pro = PrologueParams{};
+  if (a->prologue != nullptr) {
+    const va_qk_prologue& pr = *a->prologue;
+    VA_CHECK_ARG(a->causal != 0 && a->head_dim == 128 && !f8,
+                 "va_varlen_attention: the fused query prologue needs a causal launch, "
+                 "head_dim 128 and a 16-bit pool or none");
+    VA_CHECK_ARG(pr.q_norm_weight && pr.cos_sin_cache && pr.positions && pr.max_position > 0 &&
+                     pr.cos_sin_stride >= a->head_dim,
+                 "va_varlen_attention: prologue weight / rotary cache / positions");
+    VA_CHECK_ARG(pr.weight_dtype == VA_BF16 || pr.weight_dtype == VA_F16 ||
+                     pr.weight_dtype == VA_F32,
+                 "va_varlen_attention: prologue weight_dtype");
+    VA_CHECK_ARG(pr.positions_dtype == VA_I32 || pr.positions_dtype == VA_I64,
+                 "va_varlen_attention: prologue positions_dtype");
+    VA_CHECK_ARG((uintptr_t)pr.q_norm_weight % 16 == 0 && (uintptr_t)pr.cos_sin_cache % 16 == 0 &&
+                     (pr.cos_sin_stride * 4) % 16 == 0,
+                 "va_varlen_attention: prologue weight and rotary cache must be 16-byte aligned "
+                 "(rows too)");
+    p.pro.q_w = pr.q_norm_weight;
+    p.pro.k_w = pr.q_norm_weight;
+    p.pro.w_dtype = pr.weight_dtype;
+    p.pro.eps = pr.eps;
+    p.pro.cs = pr.cos_sin_cache;
+    p.pro.cs_stride = pr.cos_sin_stride;
+    p.pro.max_pos = pr.max_position;
+    p.pro.pos_i64 = pr.positions_dtype == VA_I64;
+    p.pro.pos = pr.positions;
+  }
   p.block_size = has_pool ? a->pool.block_size : 1;
   p.num_blocks = a->pool.num_blocks;
   p.table = a->block_tables;

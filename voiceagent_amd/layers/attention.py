@@ -26,9 +26,12 @@ store-then-attend order with two launches.
 the rotary cos/sin cache and the tokens' positions): q and k are then the
 raw projections, and the layer applies RMSNorm and RoPE to them as
 Qwen3Attention.forward does before calling attention (models/qwen3.py:42-48).
-A decode batch with the fused store applies it inside the decode launch; any
-other batch runs ``ops.qk_norm_rope`` first.  Qwen3Attention then passes the
-prologue instead of calling q_norm, k_norm and rotary_emb itself.
+A decode batch with the fused store applies it inside the decode launch.  A
+prefill batch (head_dim 128, 16-bit pool or none) runs ``ops.qk_norm_rope``
+over the keys alone and lets the varlen launch normalise and rotate the
+queries itself; any other batch runs ``ops.qk_norm_rope`` over both first.
+Qwen3Attention then passes the prologue instead of calling q_norm, k_norm and
+rotary_emb itself.
 
 ``kv_layout`` names the pool layout: ``"nhd"`` ``[num_blocks, block_size,
 Hkv, D]`` as model_runner.py:116-131 allocates it (the default), or
@@ -90,6 +93,14 @@ def _decode_split(context) -> int:
 
 class PagedAttention(nn.Module):
     fuse_store = True
+    # True: prefill batches let the varlen launch apply the query prologue
+    # (the keys alone go through the standalone kernel first).  Off by
+    # default: over config 3 both ways take 66 us per layer, as each item
+    # of the varlen launch fetches the cos / sin rows of its 64 positions
+    # for one KV head (8 times the standalone kernel's rotary traffic per
+    # position), which costs what the saved query round trip through HBM
+    # saves.  False: the standalone kernel over q and k, then the launch.
+    varlen_fuse_prologue = False
     kv_layout = ops.LAYOUT_NHD
     k_scale = 1.0  # FP8 pools: value of a key code = code * k_scale
     v_scale = 1.0
@@ -109,10 +120,15 @@ class PagedAttention(nn.Module):
         context = get_attention_context()
         num_seqs = context.cu_seqlens_k.numel() - 1
         decode = context.max_seqlen_q == 1 and q.shape[0] == num_seqs
+        q_pro = None  # the prologue the varlen launch applies to q itself
         if prologue is not None:
             if self.k_cache.numel() and decode and self.fuse_store:
                 return self._decode_fused(q, k, v, context, prologue)
-            q, k = ops.qk_norm_rope(q, k, prologue)
+            if not decode and self._varlen_takes_prologue(q):
+                _, k = ops.qk_norm_rope(None, k, prologue)
+                q_pro = prologue
+            else:
+                q, k = ops.qk_norm_rope(q, k, prologue)
         if not self.k_cache.numel():
             # Memory-profiling pass before the cache exists: packed causal varlen.
             return ops.varlen_attention(
@@ -125,6 +141,7 @@ class PagedAttention(nn.Module):
                 context.max_seqlen_k,
                 scale=self.scale,
                 causal=True,
+                prologue=q_pro,
             )
         if decode:
             if self.fuse_store:
@@ -162,6 +179,7 @@ class PagedAttention(nn.Module):
                 layout=self.kv_layout,
                 k_scale=self.k_scale,
                 v_scale=self.v_scale,
+                prologue=q_pro,
             )
         self._store(k, v, context.slot_mapping)
         return ops.varlen_attention(
@@ -180,7 +198,15 @@ class PagedAttention(nn.Module):
             layout=self.kv_layout,
             k_scale=self.k_scale,
             v_scale=self.v_scale,
+            prologue=q_pro,
         )
+
+    def _varlen_takes_prologue(self, q: torch.Tensor) -> bool:
+        """Whether the varlen launch can apply the query prologue itself:
+        head_dim 128, 16-bit q, and a 16-bit pool or none."""
+        return (self.varlen_fuse_prologue and q.shape[-1] == 128 and
+                q.dtype in (torch.bfloat16, torch.float16) and
+                (not self.k_cache.numel() or self.k_cache.dtype == q.dtype))
 
     def _decode_fused(self, q, k, v, context, prologue: ops.QKPrologue | None) -> torch.Tensor:
         """One launch: (prologue,) store of the new rows, paged decode."""

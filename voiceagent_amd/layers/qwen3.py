@@ -12,7 +12,11 @@ model runner binds its cache slices the same way
   writes the new K/V row and attends (reference: q_norm, k_norm, rotary,
   store_kvcache and attention as separate launches).
 * Other batches run the standalone prologue kernel over q and k, then the
-  varlen path of :class:`PagedAttention`.
+  varlen path of :class:`PagedAttention`.  With ``varlen_fuse_prologue``
+  set (off by default: no faster over config 3), prefill batches with
+  head_dim 128 and a 16-bit pool or none run the standalone kernel over the
+  keys alone, and the varlen launch normalises and rotates the queries
+  itself, in registers, at each item's first key tile.
 
 The norm weights and the rotary table mirror the reference modules: weights
 ``q_norm.weight`` / ``k_norm.weight`` of shape [head_dim]
@@ -78,5 +82,8 @@ class Qwen3AttentionCore(PagedAttention):
                 new_slots=context.slot_mapping,
                 prologue=pro,
             )
+        if self.fuse_prologue:
+            # Prefill batches: the varlen launch applies the query prologue.
+            return super().forward(q, k, v, prologue=pro)
         qn, kn = ops.qk_norm_rope(q, k, pro)
         return super().forward(qn, kn, v)

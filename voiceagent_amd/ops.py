@@ -214,16 +214,20 @@ def _prologue_struct(pro: QKPrologue, head_dim: int, n_positions: int) -> N.QkPr
 
 
 def qk_norm_rope(
-    q: torch.Tensor,
+    q: torch.Tensor | None,
     k: torch.Tensor,
     prologue: QKPrologue,
     *,
     q_out: torch.Tensor | None = None,
     k_out: torch.Tensor | None = None,
-) -> tuple[torch.Tensor, torch.Tensor]:
+) -> tuple[torch.Tensor | None, torch.Tensor]:
     """Apply the Qwen3 q/k prologue to q [T, Hq, D] and k [T, Hkv, D] (one
     position per token).  Outputs are allocated contiguous when not given and
-    may be q / k themselves (in place)."""
+    may be q / k themselves (in place).  ``q`` None: the keys alone (a
+    prefill whose varlen launch applies the query prologue itself); the
+    first result is then None."""
+    if q is None:
+        return None, _k_norm_rope(k, prologue, k_out)
     fast = _FAST if _FAST_LOADED else _fast_calls()
     if fast is not None:
         index = q.get_device()
@@ -269,6 +273,29 @@ def qk_norm_rope(
     args.prologue = _prologue_struct(prologue, d, T)
     N.call("va_qk_norm_rope", args, device)
     return q_out, k_out
+
+
+def _k_norm_rope(k: torch.Tensor, prologue: QKPrologue,
+                 k_out: torch.Tensor | None) -> torch.Tensor:
+    """The key side of qk_norm_rope alone (num_heads = 0 in the C ABI)."""
+    device = _check_gpu(k, k_out, prologue.k_norm_weight, prologue.cos_sin_cache,
+                        prologue.positions)
+    _require(k.dim() == 3, "k must be [T, Hkv, D]")
+    _rows(k, "k")
+    T, hkv, d = (int(x) for x in k.shape)
+    if k_out is None:
+        k_out = torch.empty(k.shape, dtype=k.dtype, device=device)
+    _require(k_out.shape == k.shape and k_out.dtype == k.dtype, "k_out must match k")
+    _rows(k_out, "k_out")
+    args = N.new_args(N.QkNormRopeArgs)
+    args.dtype = _dtype_code(k)
+    args.k, args.k_stride_tok, args.k_stride_head = k.data_ptr(), k.stride(0), k.stride(1)
+    args.k_out = k_out.data_ptr()
+    args.k_out_stride_tok, args.k_out_stride_head = k_out.stride(0), k_out.stride(1)
+    args.num_tokens, args.num_heads, args.num_kv_heads, args.head_dim = T, 0, hkv, d
+    args.prologue = _prologue_struct(prologue, d, T)
+    N.call("va_qk_norm_rope", args, device)
+    return k_out
 
 
 # -------------------------------------------------------------------- decode
@@ -618,6 +645,7 @@ def varlen_attention(
     out: torch.Tensor | None = None,
     k_scale: float = 1.0,
     v_scale: float = 1.0,
+    prologue: QKPrologue | None = None,
 ) -> torch.Tensor:
     """Packed variable-length attention (flash_attn_varlen_func semantics).
 
@@ -631,10 +659,13 @@ def varlen_attention(
     not read: key ranges come from ``cu_seqlens_k``.  An FP8 pool
     (float8_e4m3fn codes, values code * k_scale / v_scale) is converted tile
     by tile inside the kernel (no workspace); its new rows are stored
-    quantised after the attention.
+    quantised after the attention.  With a ``prologue`` (causal, head_dim
+    128, a 16-bit pool or none), q holds the raw query projections and the
+    launch normalises and rotates them at ``prologue.positions`` (one per
+    query token); k and the pool must hold processed keys.
     """
     fast = _FAST if _FAST_LOADED else _fast_calls()
-    if (fast is not None and layout in (LAYOUT_NHD, LAYOUT_HND) and
+    if (fast is not None and prologue is None and layout in (LAYOUT_NHD, LAYOUT_HND) and
             (k_cache is None or k_cache.dtype != FP8_KV_DTYPE)):
         index = q.get_device()
         if index >= 0 and index == torch.cuda.current_device():
@@ -695,6 +726,11 @@ def varlen_attention(
                  slot_mapping.is_contiguous(), "slot_mapping must have one entry per query")
         fields.update(slot_mapping=slot_mapping.data_ptr(),
                       slot_dtype=_index_code(slot_mapping, "slot_mapping"))
+    pro_struct = None
+    if prologue is not None:
+        _check_gpu(q, prologue.q_norm_weight, prologue.cos_sin_cache, prologue.positions)
+        pro_struct = _prologue_struct(prologue, d, total_q)  # kept alive through the call
+        fields["prologue"] = ctypes.pointer(pro_struct)
     if out is None:
         out = torch.empty_like(q)
     os_ = out.stride()
