@@ -130,16 +130,17 @@ constexpr float kDecLazy = 8.0f;
 
 // kMask: the launch has a key_valid_mask (a separate instantiation, so the
 // kernel without one carries none of its loads or branches).  kF8: the pool
-// holds OCP e4m3 codes; a staged tile of codes is converted, exactly, into a
-// 16-bit tile in the wave's conversion area, which the matrix-core reads
-// below use as they use a staged 16-bit tile.  k_scale is folded into the
-// softmax scale and v_scale into the output.
+// holds OCP e4m3 codes.  S^T reads a staged K tile's codes, eight per lane,
+// and converts them, exactly, in registers; a staged V tile is converted
+// into a 16-bit tile in the wave's conversion area, which the transposed
+// reads below use as they use a staged 16-bit tile.  k_scale is folded into
+// the softmax scale and v_scale into the output.
 template <typename ET, int D, int G, bool kProlog, bool kMask, bool kF8>
 __global__ __launch_bounds__(MfmaDecodeShape<D>::W * 64, 1) void paged_decode_mfma_kernel(
     DecodeParams p) {
   using Sh = MfmaDecodeShape<D>;
   using M = DecodeMma<ET>;
-  constexpr int W = Sh::W, S = Sh::S, ROWB = Sh::ROWB;
+  constexpr int W = Sh::W, ROWB = Sh::ROWB;
   constexpr int TILE_B = Sh::TILE_B, DS = Sh::DS, DT = Sh::DT;
   constexpr int LPR = Sh::LPR, RPL = Sh::RPL, E = 8;
   // A tile as the DMA stages it: 16-bit rows, or rows of D e4m3 codes.
@@ -149,7 +150,13 @@ __global__ __launch_bounds__(MfmaDecodeShape<D>::W * 64, 1) void paged_decode_mf
   constexpr int NI = kChunk / RPI;          // DMA instructions per tile, K or V
   constexpr int PTILE = kChunk * PROWB;     // staged bytes of one K (or V) tile
   constexpr int STAGE_B = 2 * PTILE;
-  constexpr int CONV_B = kF8 ? 2 * TILE_B : 0;
+  // FP8: K is read as codes straight from its stage; only V goes through a
+  // 16-bit conversion area (one tile), so the wave's LDS holds more stages
+  // of codes than of 16-bit rows (3 for head_dim 128, at most 4).
+  constexpr int CONV_B = kF8 ? TILE_B : 0;
+  constexpr int S_F8 = (Sh::WAVE_B - CONV_B) / STAGE_B;
+  constexpr int S = kF8 ? (S_F8 > 4 ? 4 : S_F8) : Sh::S;  // stages of the wave's ring
+  static_assert(S >= 2, "two stages at least");
   constexpr int WAVE_B = S * STAGE_B + CONV_B;  // LDS bytes per wave
   static_assert(WAVE_B <= Sh::WAVE_B, "FP8 stages and conversion area fit the 16-bit ring");
   constexpr int NT = W * 64;
@@ -301,13 +308,16 @@ __global__ __launch_bounds__(MfmaDecodeShape<D>::W * 64, 1) void paged_decode_mf
   // ---- tile DMA: instruction i of a tile moves rows RPI i .. RPI i + RPI - 1;
   // lane l writes row RPI i + l / CPR at chunk position l % CPR, i.e. reads
   // logical chunk (l % CPR) ^ swz(row) of that row ----
-  // (Codes are staged unswizzled: the conversion reads them in order.)
-  uint32_t loff[NI];
+  // FP8: K code chunks go to chunk (c ^ row % CPR) of their row, so that
+  // the 8-code reads of S^T spread over the banks; V codes are staged in
+  // order, as the conversion reads them.
+  uint32_t loff[NI], loffv[NI];
 #pragma unroll
   for (int i = 0; i < NI; ++i) {
     const int row = RPI * i + lane / CPR;
-    const int pos = kF8 ? lane % CPR : (lane % CPR) ^ dec_swz<D>(row);
+    const int pos = kF8 ? (lane % CPR) ^ (row % CPR) : (lane % CPR) ^ dec_swz<D>(row);
     loff[i] = (uint32_t)(row * p.s_slot) + (uint32_t)(pos << 4);
+    loffv[i] = kF8 ? (uint32_t)(row * p.s_slot) + (uint32_t)((lane % CPR) << 4) : loff[i];
   }
   const char* zero_row = reinterpret_cast<const char*>(&kDecZeroRow);
   const int64_t head_off = (int64_t)h * p.s_head;
@@ -335,7 +345,7 @@ __global__ __launch_bounds__(MfmaDecodeShape<D>::W * 64, 1) void paged_decode_mf
 #pragma unroll
       for (int i = 0; i < NI; ++i) dma16_nt(loff[i], kb, dst + i * 1024);
 #pragma unroll
-      for (int i = 0; i < NI; ++i) dma16_nt(loff[i], vb, dst + PTILE + i * 1024);
+      for (int i = 0; i < NI; ++i) dma16_nt(loffv[i], vb, dst + PTILE + i * 1024);
     } else {
 #pragma unroll
       for (int i = 0; i < 2 * NI; ++i) dma16(zero_row, dst + i * 1024);
@@ -506,28 +516,23 @@ __global__ __launch_bounds__(MfmaDecodeShape<D>::W * 64, 1) void paged_decode_mf
     char* sK = s_wave + (k % S) * STAGE_B;
     char* sV = sK + PTILE;
     if constexpr (kF8) {
-      // Codes to 16-bit rows in the conversion area, each 16-byte chunk of
-      // the 16-bit tile at its swizzled position; then the stage is free
-      // and takes the wave's tile k + S right away.
-      char* cK = s_wave + S * STAGE_B;
-      char* cV = cK + TILE_B;
-      constexpr int NCH = PTILE / 16 / 64;  // code chunks per lane, K or V
+      // V codes to 16-bit rows in the conversion area, each 16-byte chunk of
+      // the 16-bit tile at its swizzled position (the transposed V reads
+      // below need 16-bit rows).  K stays as codes: S^T converts the eight
+      // codes of each A operand in registers.  The wave's LDS operations run
+      // in order, so the reads below see these writes.
+      char* cV = s_wave + S * STAGE_B;
+      constexpr int NCH = PTILE / 16 / 64;  // V code chunks per lane
 #pragma unroll
       for (int i = 0; i < NCH; ++i) {
         const int e = lane + 64 * i;
         const int row = e / CPR, c8 = e % CPR;
         const int p0 = ((2 * c8) ^ dec_swz<D>(row)) << 4;
         const int p1 = ((2 * c8 + 1) ^ dec_swz<D>(row)) << 4;
-        const uint4 ck = *reinterpret_cast<const uint4*>(sK + e * 16);
         const uint4 cv = *reinterpret_cast<const uint4*>(sV + e * 16);
-        *reinterpret_cast<uint4*>(cK + row * ROWB + p0) = f8_dequant8<ET>(make_uint2(ck.x, ck.y));
-        *reinterpret_cast<uint4*>(cK + row * ROWB + p1) = f8_dequant8<ET>(make_uint2(ck.z, ck.w));
         *reinterpret_cast<uint4*>(cV + row * ROWB + p0) = f8_dequant8<ET>(make_uint2(cv.x, cv.y));
         *reinterpret_cast<uint4*>(cV + row * ROWB + p1) = f8_dequant8<ET>(make_uint2(cv.z, cv.w));
       }
-      wait_lgkmcnt0();
-      if (k + S < ntw) issue(k + S);
-      sK = cK;
       sV = cV;
     }
     const int c = wave + W * k;  // partition chunk of this tile
@@ -549,7 +554,11 @@ __global__ __launch_bounds__(MfmaDecodeShape<D>::W * 64, 1) void paged_decode_mf
       if (slot >= 0 && slot < cap && rg == 0) {
         const int r = new_tok - tb;
         const int pos16 = (col ^ dec_swz<D>(r)) << 4;
-        *reinterpret_cast<uint4*>(sK + r * ROWB + pos16) = kcur;
+        if constexpr (kF8)  // the lane's eight codes, in the K stage's layout
+          *reinterpret_cast<uint2*>(sK + r * PROWB + (((col >> 1) ^ (r % CPR)) << 4) +
+                                    (col & 1) * 8) = kq;
+        else
+          *reinterpret_cast<uint4*>(sK + r * ROWB + pos16) = kcur;
         *reinterpret_cast<uint4*>(sV + r * ROWB + pos16) = vcur;
         const int64_t sb = p.slot_small ? (int64_t)fast_div((uint32_t)slot, p.bs_div)
                                         : slot / p.block_size;
@@ -562,9 +571,23 @@ __global__ __launch_bounds__(MfmaDecodeShape<D>::W * 64, 1) void paged_decode_mf
     mf_f32x4 sacc = mf_f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int j = 0; j < DS; ++j) {
-      const uint4 a =
-          *reinterpret_cast<const uint4*>(sK + r16 * ROWB + (((4 * j + c4) ^ kswz) << 4));
+      uint4 a;
+      if constexpr (kF8) {
+        // Codes 8 u .. 8 u + 7 of row r16 (u = 4 j + c4): half u & 1 of
+        // staged chunk (u / 2) ^ (r16 % CPR).
+        const int u = 4 * j + c4;
+        a = f8_dequant8<ET>(*reinterpret_cast<const uint2*>(
+            sK + r16 * PROWB + (((u >> 1) ^ (r16 % CPR)) << 4) + (u & 1) * 8));
+      } else {
+        a = *reinterpret_cast<const uint4*>(sK + r16 * ROWB + (((4 * j + c4) ^ kswz) << 4));
+      }
       sacc = M::qk(a, qb[j], sacc);
+    }
+    if constexpr (kF8) {
+      // Both halves of the stage have been read (V by the conversion, K
+      // just now): it takes the wave's tile k + S.
+      wait_lgkmcnt0();
+      if (k + S < ntw) issue(k + S);
     }
     float sv[4];
     const int rel = blk_ok ? end - tb - 4 * c4 : 0;  // token 4 c4 + i is live iff i < rel
