@@ -282,6 +282,10 @@ def bench_lib():
                                           ctypes.c_size_t, ctypes.c_int, ctypes.c_void_p]
         lib.va_bench_empty.restype = ctypes.c_int
         lib.va_bench_empty.argtypes = [ctypes.c_int, ctypes.c_void_p]
+        lib.va_bench_hbm_depth.restype = ctypes.c_int
+        lib.va_bench_hbm_depth.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_size_t,
+                                           ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                           ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]
         lib.va_bench_last_error.restype = ctypes.c_char_p
         lib.va_bench_last_error.argtypes = []
         _BENCH_LIB = lib
@@ -368,6 +372,60 @@ def copy_floor(name: str, read_bytes: int, write_bytes: int, launches: int, args
             "us_by_grid": {str(w): round(t, 2) for w, t in table.items()}}
 
 
+# (DMA KiB, register KiB) in flight per wave; x 8 waves per CU.
+DEPTH_CONFIGS = ((4, 0), (8, 0), (16, 0), (0, 4), (0, 8), (8, 4), (8, 8), (16, 4), (16, 8))
+# (workgroups, bytes per workgroup): one CU alone, 32 CUs (a decode's tail),
+# every CU.
+DEPTH_SHAPES = ((1, 8 << 20), (32, 4 << 20), (256, 2 << 20))
+
+
+def depth_probe(dev, stream) -> list:
+    """Per-CU HBM read rate against the bytes one CU keeps in flight
+    (va_bench_hbm_depth): every (shape, depth) three timed launches after one
+    untimed, each on a window of a 2 GiB buffer not read since it was filled
+    (cold: the 256 MB MALL holds the last bytes written or read).  Rates are
+    per workgroup, from its own start and end stamps."""
+    buf = torch.empty(2 << 30, dtype=torch.uint8, device=dev)
+    buf.fill_(1)
+    times = torch.zeros(2 * 256, dtype=torch.int64, device=dev)
+    sink = torch.zeros(256, dtype=torch.int32, device=dev)
+    torch.cuda.synchronize()
+    lib, cursor, rows = bench_lib(), 0, []
+    for wgs, per_wg in DEPTH_SHAPES:
+        for dma, vgpr in DEPTH_CONFIGS:
+            unit = 8 * (dma + vgpr) * 1024
+            read = per_wg // unit * unit  # bytes a workgroup actually reads
+            rates, agg = [], []
+            for rep in range(4):
+                need = wgs * per_wg
+                if cursor + need > buf.numel():
+                    cursor = 0
+                rc = lib.va_bench_hbm_depth(buf.data_ptr() + cursor, buf.numel() - cursor, per_wg,
+                                            wgs, dma, vgpr, times.data_ptr(), sink.data_ptr(),
+                                            stream.cuda_stream)
+                if rc != 0:
+                    raise ValueError(lib.va_bench_last_error().decode())
+                stream.synchronize()
+                cursor += need
+                if rep == 0:
+                    continue
+                t = times[:2 * wgs].view(wgs, 2).cpu().double()
+                dt = (t[:, 1] - t[:, 0]) * 10e-9  # 100 MHz ticks
+                rates += (read / dt / 1e9).tolist()
+                agg.append(wgs * read / ((t[:, 1].max() - t[:, 0].min()).item() * 10e-9) / 1e9)
+            rates.sort()
+            rows.append({"workgroups": wgs, "dma_kib_per_cu": 8 * dma, "vgpr_kib_per_cu": 8 * vgpr,
+                         "gbs_per_cu_median": round(rates[len(rates) // 2], 1),
+                         "gbs_per_cu_min": round(rates[0], 1), "gbs_per_cu_max": round(rates[-1], 1),
+                         "gbs_all": round(sum(agg) / len(agg), 1)})
+            r = rows[-1]
+            log(f"[depth] {wgs:3d} CUs, {8 * dma:3d} KiB DMA + {8 * vgpr:2d} KiB registers in flight "
+                f"per CU: {r['gbs_per_cu_median']:.1f} GB/s per CU (min {r['gbs_per_cu_min']:.1f}, "
+                f"max {r['gbs_per_cu_max']:.1f}), {r['gbs_all']:.0f} GB/s over all")
+    del buf
+    return rows
+
+
 def bench_floor(args, dev, stream):
     """HBM read floor for config 2's launch size: a contiguous read of the
     same number of bytes in one launch (va_bench_hbm_read), 28 launches per
@@ -411,8 +469,9 @@ def bench_floor(args, dev, stream):
               "encoder_cfg4": copy_floor("encoder cfg4", enc_all * 3 // 4, enc_all // 4, 18,
                                          args, dev, stream)}
     empty = launch_floor(args, stream)
+    depth = depth_probe(dev, stream)
     return {"us_per_launch": round(us, 2), "gbs": round(gbs, 1), "copy": copies,
-            "empty_launch_us": empty,
+            "empty_launch_us": empty, "per_cu_depth": depth,
             "frac": round(gbs / HBM_PEAK_GBS, 4), "bytes": nbytes, "mode": mode,
             "workgroups": wgs,
             "us_by_mode_grid": {f"{m}/{w}": round(t, 2) for (m, w), t in table.items()},

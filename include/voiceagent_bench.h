@@ -3,8 +3,9 @@
  *
  * Not part of the drop-in ABI (include/voiceagent_attn.h) and with no
  * counterpart in the reference: bench.py uses it to measure the HBM read
- * floor that the decode kernel's bandwidth is read against, and the mixed
- * read/write floor of the varlen launches.
+ * floor that the decode kernel's bandwidth is read against, the mixed
+ * read/write floor of the varlen launches, and one CU's read rate against
+ * the bytes it keeps in flight.
  */
 #ifndef VOICEAGENT_BENCH_H
 #define VOICEAGENT_BENCH_H
@@ -44,6 +45,20 @@ int va_bench_hbm_copy(const void* src, size_t read_bytes, void* dst, size_t writ
  * before it moves a byte.  Returns 0, or -1 on a bad argument
  * (va_bench_last_error()). */
 int va_bench_empty(int workgroups, void* stream);
+
+/* Per-CU read rate against the bytes in flight: one launch of `workgroups`
+ * 512-lane workgroups, each holding a 128 KiB LDS ring (so one per CU and
+ * no two on one CU), workgroup w reading the `bytes_per_wg` bytes at
+ * src + w bytes_per_wg (1 KiB aligned, inside `src_bytes`) in 1 KiB units
+ * per wave: `dma_kib_per_wave` (0, 4, 8 or 16) through non-temporal LDS DMA
+ * and `vgpr_kib_per_wave` (0, 4 or 8) through non-temporal register loads,
+ * that many in flight per wave at every request.  `times` (device) receives
+ * two 64-bit s_memrealtime stamps (100 MHz) per workgroup, start and end;
+ * `sink` needs one 32-bit word per workgroup and is, in practice, never
+ * written.  Returns 0, or -1 on a bad argument (va_bench_last_error()). */
+int va_bench_hbm_depth(const void* src, size_t src_bytes, size_t bytes_per_wg, int workgroups,
+                       int dma_kib_per_wave, int vgpr_kib_per_wave, void* times, void* sink,
+                       void* stream);
 
 const char* va_bench_last_error(void);
 

@@ -187,6 +187,18 @@ def test_bench_library_is_apart_from_the_drop_in_library():
     assert rc == -1 and b"mode" in blib.va_bench_last_error()
     rc = blib.va_bench_empty(0, None)  # no workgroups: rejected before any launch
     assert rc == -1 and b"workgroups" in blib.va_bench_last_error()
+    # The per-CU depth probe checks its depths, alignment and buffer on the host.
+    mib = 1 << 20
+    rc = blib.va_bench_hbm_depth(1024, 8 * mib, mib, 1, 12, 0, 16, 16, None)
+    assert rc == -1 and b"depths" in blib.va_bench_last_error()
+    rc = blib.va_bench_hbm_depth(1024, 8 * mib, mib, 1, 0, 0, 16, 16, None)
+    assert rc == -1 and b"depths" in blib.va_bench_last_error()
+    rc = blib.va_bench_hbm_depth(1024, 8 * mib, mib + 16, 1, 8, 0, 16, 16, None)
+    assert rc == -1 and b"aligned" in blib.va_bench_last_error()
+    rc = blib.va_bench_hbm_depth(1024, 8 * mib, 4 * mib, 4, 8, 4, 16, 16, None)
+    assert rc == -1 and b"exceed" in blib.va_bench_last_error()
+    rc = blib.va_bench_hbm_depth(1024, 8 * mib, 64 * 1024, 1, 16, 8, 16, 16, None)
+    assert rc == -1 and b"two rounds" in blib.va_bench_last_error()
 
 
 def test_host_fast_path_module_loads_and_declines_cpu_tensors():

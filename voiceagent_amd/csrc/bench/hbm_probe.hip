@@ -126,6 +126,92 @@ __global__ __launch_bounds__(kProbeThreads) void hbm_copy_probe_kernel(
 // Does nothing: the fixed cost of a launch of its grid.
 __global__ __launch_bounds__(kProbeThreads) void empty_probe_kernel() {}
 
+// Per-workgroup read rate against the bytes in flight.  Workgroup w (8
+// wave64s) reads `rounds` rounds of its slice src + w slice_stride; in each
+// round a wave takes NL + NV consecutive 1 KiB units of its own (unit j of
+// wave v at byte (8 j + v) KiB): the first NL through non-temporal LDS DMA
+// into the wave's NL KiB of a 128 KiB ring (so one workgroup fills a CU's
+// LDS and workgroups land on distinct CUs), the next NV through
+// non-temporal 16-byte register loads (XOR-folded, written to sink only on a
+// fixed value, so never in practice).  Before each request the wave waits
+// until at most NL + NV - 1 of its requests are in flight: 8 (NL + NV) KiB
+// per CU stay in flight.  The DMA uses the builtin form; with both kinds in
+// a round the compiler still waits for all in-flight requests once per round
+// before folding the registers (it does not count the DMAs issued after a
+// register load), so mixed depths hold only between those drains.  Thread 0
+// writes s_memrealtime (100 MHz) at the start and the end to times[2 w],
+// times[2 w + 1].
+constexpr int kDepthMaxDma = 16;  // KiB of LDS DMA per wave
+constexpr int kDepthWaves = kProbeThreads / 64;
+
+template <int NL, int NV>
+__global__ __launch_bounds__(kProbeThreads, 1) void hbm_depth_probe_kernel(
+    const char* src, int64_t slice_stride, int64_t rounds, uint64_t* times, uint32_t* sink) {
+  static_assert(NL >= 0 && NL <= kDepthMaxDma && NV >= 0 && NL + NV >= 1 && NL + NV < 64,
+                "depth");
+  __shared__ __align__(1024) char ring[kDepthWaves * kDepthMaxDma * 1024];
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const char* const base = src + (int64_t)blockIdx.x * slice_stride + lane * 16;
+  char* const myring = ring + wave * kDepthMaxDma * 1024 + lane * 16;
+  // Every round is the same code (the registers start at zero and are
+  // folded before each reload): a first round without the fold made the
+  // compiler's own wait for the loop-carried registers a full drain.
+  uint4 r[NV > 0 ? NV : 1];
+#pragma unroll
+  for (int s = 0; s < (NV > 0 ? NV : 1); ++s) r[s] = make_uint4(0u, 0u, 0u, 0u);
+  uint32_t acc = 0;
+  uint64_t t0 = 0;
+  __syncthreads();
+  if (threadIdx.x == 0) t0 = __builtin_amdgcn_s_memrealtime();
+  for (int64_t rd = 0; rd < rounds; ++rd) {
+    const int64_t j0 = rd * (NL + NV);
+#pragma unroll
+    for (int s = 0; s < NL; ++s) {
+      wait_vmcnt<NL + NV - 1>();
+      __builtin_amdgcn_global_load_lds(
+          reinterpret_cast<const void*>(base + (((j0 + s) * kDepthWaves + wave) << 10)),
+          reinterpret_cast<__attribute__((address_space(3))) void*>(
+              (__attribute__((address_space(3))) char*)(myring + s * 1024)),
+          16, 0, /*aux: nt*/ 2);
+    }
+#pragma unroll
+    for (int s = 0; s < NV; ++s) {
+      wait_vmcnt<NL + NV - 1>();
+      uint32_t f = r[s].x ^ r[s].y ^ r[s].z ^ r[s].w;
+      asm volatile("" : "+v"(f));
+      acc ^= f;
+      r[s] = ld16_nt(reinterpret_cast<const uint4*>(
+          base + (((j0 + NL + s) * kDepthWaves + wave) << 10)));
+    }
+  }
+#pragma unroll
+  for (int s = 0; s < NV; ++s) acc ^= r[s].x ^ r[s].y ^ r[s].z ^ r[s].w;
+  wait_vmcnt<0>();
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    times[2 * blockIdx.x] = t0;
+    times[2 * blockIdx.x + 1] = __builtin_amdgcn_s_memrealtime();
+  }
+  if (acc == kProbeMagic) sink[blockIdx.x] = acc;
+}
+
+template <int NL>
+static bool launch_depth_nv(int nv, dim3 grid, hipStream_t s, const char* src, int64_t stride,
+                            int64_t rounds, uint64_t* times, uint32_t* sink) {
+  switch (nv) {
+    case 0:
+      if constexpr (NL > 0) {
+        hipLaunchKernelGGL((hbm_depth_probe_kernel<NL, 0>), grid, dim3(kProbeThreads), 0, s, src, stride, rounds, times, sink);
+        return true;
+      }
+      return false;
+    case 4: hipLaunchKernelGGL((hbm_depth_probe_kernel<NL, 4>), grid, dim3(kProbeThreads), 0, s, src, stride, rounds, times, sink); return true;
+    case 8: hipLaunchKernelGGL((hbm_depth_probe_kernel<NL, 8>), grid, dim3(kProbeThreads), 0, s, src, stride, rounds, times, sink); return true;
+    default: return false;
+  }
+}
+
 }  // namespace
 }  // namespace va
 
@@ -188,6 +274,47 @@ extern "C" int va_bench_empty(int workgroups, void* stream) {
                      (hipStream_t)stream);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return bench_fail("va_bench_empty: launch failed: %s", hipGetErrorString(e));
+  return 0;
+}
+
+extern "C" int va_bench_hbm_depth(const void* src, size_t src_bytes, size_t bytes_per_wg,
+                                  int workgroups, int dma_kib_per_wave, int vgpr_kib_per_wave,
+                                  void* times, void* sink, void* stream) {
+  using namespace va;
+  if (src == nullptr || times == nullptr || sink == nullptr)
+    return bench_fail("va_bench_hbm_depth: null pointer");
+  if ((uintptr_t)src % 1024 != 0 || bytes_per_wg % 1024 != 0)
+    return bench_fail("va_bench_hbm_depth: src and bytes_per_wg must be 1 KiB aligned");
+  if (workgroups < 1 || workgroups > 4096)
+    return bench_fail("va_bench_hbm_depth: workgroups must be in [1, 4096]");
+  if ((dma_kib_per_wave != 0 && dma_kib_per_wave != 4 && dma_kib_per_wave != 8 &&
+       dma_kib_per_wave != 16) ||
+      (vgpr_kib_per_wave != 0 && vgpr_kib_per_wave != 4 && vgpr_kib_per_wave != 8) ||
+      dma_kib_per_wave + vgpr_kib_per_wave == 0)
+    return bench_fail("va_bench_hbm_depth: depths must be 0|4|8|16 KiB (DMA) and 0|4|8 KiB "
+                      "(registers) per wave, not both 0");
+  const int64_t per_round = (int64_t)kDepthWaves * (dma_kib_per_wave + vgpr_kib_per_wave) * 1024;
+  const int64_t rounds = (int64_t)bytes_per_wg / per_round;
+  if (rounds < 2) return bench_fail("va_bench_hbm_depth: bytes_per_wg below two rounds");
+  if ((uint64_t)bytes_per_wg * (uint64_t)workgroups > src_bytes)
+    return bench_fail("va_bench_hbm_depth: %d slices of %zu bytes exceed the %zu-byte buffer",
+                      workgroups, bytes_per_wg, src_bytes);
+  const hipStream_t s = (hipStream_t)stream;
+  const dim3 grid((unsigned)workgroups);
+  const char* c = reinterpret_cast<const char*>(src);
+  uint64_t* t = reinterpret_cast<uint64_t*>(times);
+  uint32_t* k = reinterpret_cast<uint32_t*>(sink);
+  const int64_t stride = (int64_t)bytes_per_wg;
+  bool ok = false;
+  switch (dma_kib_per_wave) {
+    case 0: ok = vgpr_kib_per_wave > 0 && launch_depth_nv<0>(vgpr_kib_per_wave, grid, s, c, stride, rounds, t, k); break;
+    case 4: ok = launch_depth_nv<4>(vgpr_kib_per_wave, grid, s, c, stride, rounds, t, k); break;
+    case 8: ok = launch_depth_nv<8>(vgpr_kib_per_wave, grid, s, c, stride, rounds, t, k); break;
+    case 16: ok = launch_depth_nv<16>(vgpr_kib_per_wave, grid, s, c, stride, rounds, t, k); break;
+  }
+  if (!ok) return bench_fail("va_bench_hbm_depth: unsupported depth");
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return bench_fail("va_bench_hbm_depth: launch failed: %s", hipGetErrorString(e));
   return 0;
 }
 
