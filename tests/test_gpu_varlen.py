@@ -116,6 +116,49 @@ def test_one_query_block_per_sequence(dev, dtype, hq, hkv, d):
     assert _err(out, ref) <= TOL
 
 
+@pytest.mark.parametrize("hq,hkv,d", [(14, 14, 64), (16, 8, 128)])
+def test_one_block_launch_many_items_per_workgroup(dev, hq, hkv, d):
+    # Thousands of ragged one-block sequences (and empty ones): each
+    # workgroup of the one-block launch runs many items, handing its K/V ring
+    # from item to item, and most blocks end inside their 128 rows.  A guard
+    # region after the output (where rows past the last sequence's end would
+    # land) keeps its sentinel.
+    bq = 128 // (hq // hkv)
+    g = torch.Generator().manual_seed(hq + d)
+    lens = torch.randint(0, bq + 1, (1500 if d == 64 else 900,), generator=g).tolist()
+    lens[-1] = 1  # the last sequence's block is nearly all past its end
+    b = workloads.make_varlen_batch(lens, hq, hkv, d, causal=False, seed=hq + d + 7)
+    total = sum(lens)
+    full = torch.full((total + bq, hq, d), 7.0, dtype=torch.bfloat16, device=dev)
+    out = ops.varlen_attention(b.q.to(dev), b.k.to(dev), b.v.to(dev), b.cu_seqlens.to(dev),
+                               b.cu_seqlens.to(dev), b.max_seqlen, b.max_seqlen, scale=b.scale,
+                               causal=False, out=full[:total])
+    torch.cuda.synchronize()
+    assert bool((full[total:] == 7.0).all())
+    ref = oracle.varlen_attention(b.q, b.k, b.v, b.cu_seqlens, b.cu_seqlens, b.scale, False)
+    assert _err(out, ref) <= TOL
+
+
+def test_one_block_launch_with_an_output_past_2_gib(dev):
+    # An output view whose rows lie more than 2^31 bytes apart in total: the
+    # row offsets need 64 bits.
+    lens = [5, 104, 64, 1, 128]
+    b = workloads.make_varlen_batch(lens, 14, 14, 64, causal=False, seed=3)
+    total = sum(lens)
+    row = 14 * 64
+    step = (1 << 31) // (total - 1) // row * row + row  # token stride in elements
+    big = torch.zeros(total * step, dtype=torch.bfloat16, device=dev)
+    out = big.as_strided((total, 14, 64), (step, 64, 1))
+    assert (total - 1) * step * 2 > (1 << 31)
+    ops.varlen_attention(b.q.to(dev), b.k.to(dev), b.v.to(dev), b.cu_seqlens.to(dev),
+                         b.cu_seqlens.to(dev), b.max_seqlen, b.max_seqlen, scale=b.scale,
+                         causal=False, out=out)
+    torch.cuda.synchronize()
+    ref = oracle.varlen_attention(b.q, b.k, b.v, b.cu_seqlens, b.cu_seqlens, b.scale, False)
+    assert _err(out, ref) <= TOL
+    del big
+
+
 def test_persistent_rounds_long_prompts(dev):
     # 8 prompts of ~2000 tokens, 8 kv heads: each XCD lists 8 pairs x 32 blocks,
     # so every workgroup takes several items in snake order and the level walk
