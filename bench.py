@@ -168,6 +168,31 @@ def bench_decode(args, dev, stream):
                 batch=batch, qs=qs, nks=nks, nvs=nvs)
 
 
+def bench_decode_warm(args, dev, stream, dec):
+    """Config 2's step with every one of the 28 launches on layer 0's pool
+    (46 MB, resident in the 256 MB MALL after the first): the kernel's own
+    start-up, rounds and tail without the cold HBM reads.  Not a headline
+    figure; it tells how much of the cold time the HBM reads themselves take."""
+    batch, layers = dec["batch"], workloads.LAYERS
+    outs = torch.empty_like(dec["qs"])
+
+    def step():
+        for i in range(layers):
+            ops.paged_decode(dec["qs"][i], batch.k_pools[0], batch.v_pools[0],
+                             batch.block_tables, batch.cu_seqlens_k, lens_cumulative=True,
+                             max_seq_len=batch.max_seq_len, scale=batch.scale,
+                             new_k=dec["nks"][i], new_v=dec["nvs"][i],
+                             new_slots=batch.slot_mapping, out=outs[i], split_tokens=args.split)
+
+    ms, _ = timed_graph(step, args.steps, args.warmup, stream, name="decode_cfg2_warm")
+    us = ms * 1000.0 / layers
+    gbs = dec["bytes_layer"] / (us * 1e-6) / 1e9
+    log(f"[decode warm] {us:.2f} us/layer with layer 0's pool in every launch ({gbs:.0f} GB/s; "
+        f"cold {dec['us_layer']:.2f})")
+    return {"us_per_layer": round(us, 2), "gbs": round(gbs, 1),
+            "note": "all 28 launches on layer 0's pool (MALL-resident); not the headline"}
+
+
 def decode_launch_bytes(lens, kv_elem: int = 2) -> int:
     """Algorithmic bytes of one config-2 decode launch (attention + fused
     store): K/V rows of every context token (kv_elem bytes per element: 2 for
@@ -1017,6 +1042,7 @@ def main():
         return
     extra = {}
     if args.only == "all":
+        extra["decode_warm"] = bench_decode_warm(args, dev, stream, dec)
         extra["fp8_decode"] = bench_decode_fp8(args, dev, stream, dec)
         extra["store"] = bench_store(args, dev, stream, dec)
         extra["qwen3_prologue"] = bench_prologue(args, dev, stream, dec)
