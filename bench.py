@@ -193,6 +193,47 @@ def bench_decode_warm(args, dev, stream, dec):
             "note": "all 28 launches on layer 0's pool (MALL-resident); not the headline"}
 
 
+def bench_decode_batches(args, dev, stream):
+    """Config 2's decode at larger batches (contexts U[60, 600], 28 cold layers):
+    with several rounds of workgroups the dispatcher hands each CU a new pair as
+    it frees, so the longest contexts no longer set the end alone.  Reported
+    beside the headline, not instead of it."""
+    res = {}
+    for B in (64, 128, 256):
+        lens = workloads.cfg2_lens(0, batch=B)
+        blocks = sum(math.ceil(n / workloads.BLOCK) for n in lens) + 64
+        batch = workloads.make_decode_batch(lens, num_blocks=blocks, num_layers=workloads.LAYERS,
+                                            dtype=torch.bfloat16, kv_std=0.5, device=dev, seed=0,
+                                            device_rng=True)
+        g = torch.Generator(device=dev).manual_seed(7)
+        layers = workloads.LAYERS
+        qs = torch.randn(layers, B, workloads.HQ, workloads.HEAD_DIM, generator=g, device=dev
+                         ).to(torch.bfloat16)
+        nks = (torch.randn(layers, B, workloads.HKV, workloads.HEAD_DIM, generator=g, device=dev)
+               * 0.5).to(torch.bfloat16)
+        nvs = torch.randn_like(nks) * 0.5
+        outs = torch.empty_like(qs)
+
+        def step():
+            for i in range(layers):
+                ops.paged_decode(qs[i], batch.k_pools[i], batch.v_pools[i], batch.block_tables,
+                                 batch.cu_seqlens_k, lens_cumulative=True,
+                                 max_seq_len=batch.max_seq_len, scale=batch.scale, new_k=nks[i],
+                                 new_v=nvs[i], new_slots=batch.slot_mapping, out=outs[i])
+
+        ms, _ = timed_graph(step, args.steps, args.warmup, stream, name=f"decode_b{B}")
+        us = ms * 1000.0 / layers
+        nbytes = decode_launch_bytes(lens)
+        gbs = nbytes / (us * 1e-6) / 1e9
+        log(f"[decode batch] B={B}: {us:.2f} us/layer, {gbs:.0f} GB/s of {nbytes / 1e6:.1f} MB "
+            f"({gbs / HBM_PEAK_GBS:.3f} of HBM peak)")
+        res[f"b{B}"] = {"us_per_layer": round(us, 2), "gbs": round(gbs, 1),
+                        "frac": round(gbs / HBM_PEAK_GBS, 4), "bytes_per_layer": nbytes}
+        del batch, qs, nks, nvs, outs
+        torch.cuda.empty_cache()
+    return res
+
+
 def decode_launch_bytes(lens, kv_elem: int = 2) -> int:
     """Algorithmic bytes of one config-2 decode launch (attention + fused
     store): K/V rows of every context token (kv_elem bytes per element: 2 for
@@ -981,8 +1022,9 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--split", type=int, default=0, help="decode split_tokens (0 = auto)")
-    ap.add_argument("--only", choices=["decode", "prefill", "encoder", "store", "longform",
-                                       "prologue", "kvformat", "floor", "tts", "fp8", "all"],
+    ap.add_argument("--only", choices=["decode", "batches", "prefill", "encoder", "store",
+                                       "longform", "prologue", "kvformat", "floor", "tts", "fp8",
+                                       "all"],
                     default="all")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
@@ -1016,6 +1058,9 @@ def main():
     if args.only == "longform":
         print(json.dumps({"longform": bench_longform(args, dev, stream)}))
         return
+    if args.only == "batches":
+        print(json.dumps({"decode_batches": bench_decode_batches(args, dev, stream)}))
+        return
     if args.only == "floor":
         print(json.dumps({"hbm_read_floor": bench_floor(args, dev, stream)}))
         return
@@ -1043,6 +1088,7 @@ def main():
     extra = {}
     if args.only == "all":
         extra["decode_warm"] = bench_decode_warm(args, dev, stream, dec)
+        extra["decode_batches"] = bench_decode_batches(args, dev, stream)
         extra["fp8_decode"] = bench_decode_fp8(args, dev, stream, dec)
         extra["store"] = bench_store(args, dev, stream, dec)
         extra["qwen3_prologue"] = bench_prologue(args, dev, stream, dec)
