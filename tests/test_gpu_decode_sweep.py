@@ -144,3 +144,29 @@ def test_random_decode_case_matches_oracle(dev, matrix_core, seed):
     tol = 1e-5 if c["dtype"] == torch.float32 else 2e-2
     err = (out.float().cpu() - ref.float()).abs().max().item()
     assert err <= tol, f"case {seed}: max error {err:.3e}"
+    if seed % 4 == 0:
+        # The same call captured in a HIP graph: every replay, with eager work
+        # between replays, gives the eager output bit for bit (the fused row is
+        # written again with the same values).
+        args = (q.to(dev), kd, vd, table.to(dev), lens_arg.to(dev))
+        kw = dict(max_seq_len=max_seq, scale=d ** -0.5, lens_cumulative=c["cumulative"],
+                  layout=layout, valid_mask=None if valid is None else valid.to(dev),
+                  new_k=None if nk is None else nk.to(dev),
+                  new_v=None if nv is None else nv.to(dev),
+                  new_slots=None if slots is None else slots.to(dev), split_tokens=split,
+                  key_limit=key_limit, table_read_width=read_width, k_scale=ks, v_scale=vs)
+        gout = torch.empty_like(out)
+        stream = torch.cuda.Stream(dev)
+        with torch.cuda.stream(stream):
+            ops.paged_decode(*args, out=gout, **kw)  # allocates the stream's workspace
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            ops.paged_decode(*args, out=gout, **kw)
+        for _ in range(2):
+            gout.fill_(7.0)
+            torch.cuda.synchronize()
+            graph.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(gout, out), f"case {seed}: graph replay differs from eager"
+        del graph
