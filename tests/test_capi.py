@@ -172,6 +172,42 @@ def test_tts_api_contract_errors_on_cpu():
         paged_attention_decode(q, kp, kp, page_table, seq_lens)
 
 
+def test_tts_value_checks_raise_in_the_reference_order():
+    # qwen_tts_paged_attention.py:333-341 checks positive lengths, then table
+    # capacity, then row by row an invalid used page before a short key mask.
+    # Each expected message below follows from that order for the case built.
+    from voiceagent_amd.agent import PagedAttentionKernelError
+    from voiceagent_amd.agent.paged_attention import _validate_inputs
+
+    kp = torch.zeros(8, 2, 2, 4)  # 8 pages of 2 tokens
+    q = torch.ones(2, 4, 1, 4)
+    table = torch.tensor([[3, 5, 99], [1, 7, 2]], dtype=torch.long)  # [0, 2] unused below
+
+    def check(lens, tbl=table, mask_width=None):
+        mask = None if mask_width is None else torch.ones(2, mask_width, dtype=torch.bool)
+        return _validate_inputs(q, kp, kp, tbl, torch.tensor(lens, dtype=torch.long), mask)
+
+    assert check([3, 5]) == (2, 4, 2, 2)  # entries past a row's used pages are not checked
+    assert check([3, 5], mask_width=5) == (2, 4, 2, 2)
+    with pytest.raises(PagedAttentionKernelError, match="positive"):
+        check([0, 7])  # 7 also exceeds the capacity of 6: the length check comes first
+    with pytest.raises(PagedAttentionKernelError, match="capacity"):
+        check([5, 7], mask_width=1)
+    with pytest.raises(PagedAttentionKernelError, match="invalid page"):
+        check([5, 5])  # row 0 now uses page 99
+    neg = table.clone()
+    neg[0, 2] = 0
+    neg[1, 1] = -1
+    with pytest.raises(PagedAttentionKernelError, match="invalid page"):
+        check([3, 3], tbl=neg)
+    with pytest.raises(PagedAttentionKernelError, match="shorter"):
+        check([3, 5], mask_width=4)
+    with pytest.raises(PagedAttentionKernelError, match="shorter"):
+        check([5, 3], tbl=neg, mask_width=4)  # row 0's short mask before row 1's page
+    with pytest.raises(PagedAttentionKernelError, match="invalid page"):
+        check([5, 3], mask_width=4)  # row 0's bad page before its own short mask
+
+
 def test_bench_library_is_apart_from_the_drop_in_library():
     # The read-floor probe lives in libvoiceagent_bench.so, declared in
     # include/voiceagent_bench.h; the drop-in library exports no diagnostics.

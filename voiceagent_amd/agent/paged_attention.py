@@ -88,17 +88,32 @@ def _validate_inputs(
             raise PagedAttentionKernelError(
                 "key_valid_mask must be [batch, max_seq] bool on device"
             )
-    if bool((seq_lens <= 0).any().item()):
-        raise PagedAttentionKernelError("sequence lengths must be positive")
+    # The reference checks row by row with one host sync per check; here every
+    # flag is computed on the device and read back in one transfer, and the
+    # first failing check raises in the reference's order: positive lengths,
+    # table capacity, then per row an invalid used entry before a short mask.
     page_size = key_pool.shape[2]
-    if bool((seq_lens > page_table.shape[1] * page_size).any().item()):
-        raise PagedAttentionKernelError("sequence length exceeds page table capacity")
+    width = page_table.shape[1]
     page_counts = (seq_lens + page_size - 1) // page_size
-    for row in range(query.shape[0]):
-        used = page_table[row, : int(page_counts[row].item())]
-        if bool(((used < 0) | (used >= key_pool.shape[0])).any().item()):
+    used = torch.arange(width, device=device) < page_counts[:, None]
+    bad_entry = (((page_table < 0) | (page_table >= key_pool.shape[0])) & used).any(dim=1)
+    row_code = bad_entry.to(torch.int64)
+    if key_valid_mask is not None:
+        short_mask = seq_lens > key_valid_mask.shape[1]
+        row_code = torch.where(bad_entry, row_code, 2 * short_mask.to(torch.int64))
+    flags = torch.cat([
+        (seq_lens <= 0).any().view(1).to(torch.int64),
+        (seq_lens > width * page_size).any().view(1).to(torch.int64),
+        row_code,
+    ]).tolist()
+    if flags[0]:
+        raise PagedAttentionKernelError("sequence lengths must be positive")
+    if flags[1]:
+        raise PagedAttentionKernelError("sequence length exceeds page table capacity")
+    for code in flags[2:]:
+        if code == 1:
             raise PagedAttentionKernelError("page table contains an invalid page table entry")
-        if key_valid_mask is not None and key_valid_mask.shape[1] < int(seq_lens[row].item()):
+        if code == 2:
             raise PagedAttentionKernelError("key_valid_mask is shorter than sequence length")
     return (
         int(query.shape[0]),
