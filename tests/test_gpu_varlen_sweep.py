@@ -139,3 +139,39 @@ def test_random_varlen_case_matches_oracle(dev, seed):
         assert diff.max().item() <= 2e-2, (
             f"case {seed}: max error {diff.max().item():.3e} where |ref| = "
             f"{ref.flatten()[at].abs().item():.3f}")
+    if seed % 4 == 0 and total_q:
+        # The launch captured in a HIP graph (the persistent schedule reads the
+        # lengths on the device, and nothing syncs or allocates).  A replay gives
+        # the eager output bit for bit (a fused store writes the same rows
+        # again); after new query values are written into the captured buffer,
+        # a replay gives what an eager call on them gives.
+        qd = q.to(dev)
+        call = dict(
+            k=None if k is None else k.to(dev), v=None if v is None else v.to(dev),
+            cu_seqlens_q=cu_q.to(dev), cu_seqlens_k=cu_k.to(dev), max_seqlen_q=max(q_lens),
+            max_seqlen_k=max(k_lens), scale=scale, causal=c["causal"], k_cache=kd, v_cache=vd,
+            block_tables=None if table is None else table.to(dev),
+            slot_mapping=None if slots is None else slots.to(dev), layout=layout,
+            k_scale=ks, v_scale=vs)
+        gout = torch.empty_like(out)
+        stream = torch.cuda.Stream(dev)
+        with torch.cuda.stream(stream):
+            ops.varlen_attention(qd, out=gout, **call)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            ops.varlen_attention(qd, out=gout, **call)
+        gout.fill_(7.0)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(gout, out), f"case {seed}: graph replay differs from eager"
+        q2 = torch.randn(q.shape, generator=gen).to(dt).to(dev)
+        want = ops.varlen_attention(q2, **call)
+        qd.copy_(q2)
+        gout.fill_(7.0)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(gout, want), f"case {seed}: replay on new queries differs from eager"
+        del graph
