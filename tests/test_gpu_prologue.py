@@ -74,6 +74,29 @@ def test_qk_norm_rope_matches_oracle(dev, dtype, hq, hkv, d, T):
             assert exact > 0.95, name
 
 
+@pytest.mark.parametrize("dtype,wdtype", [
+    (torch.bfloat16, torch.float32), (torch.bfloat16, torch.float16),
+    (torch.float16, torch.bfloat16), (torch.float32, torch.bfloat16)])
+@pytest.mark.parametrize("T", [257, 4096])
+def test_qk_norm_rope_weights_of_another_dtype(dev, dtype, wdtype, T):
+    # The norm weights' dtype is independent of the rows' (layernorm.py:19-25
+    # multiplies the rounded rows by the weight in place): the kernel unpacks
+    # 16-bit weights row by row and takes fp32 weights as they are.
+    q, k, wq, wk, pos, cs = _prologue_inputs(T, 16, 8, 128, dtype, seed=T + 3)
+    wq, wk = wq.float().mul(1.0 + 2.0 ** -9).to(wdtype), wk.float().to(wdtype)
+    print(f"qk_norm_rope rows {dtype} weights {wdtype} T={T}", flush=True)
+    pro = ops.QKPrologue(wq.to(dev), wk.to(dev), 1e-6, cs.to(dev), pos.to(dev))
+    qo, ko = ops.qk_norm_rope(q.to(dev), k.to(dev), pro)
+    torch.cuda.synchronize()
+    rq, rk = oracle.qk_norm_rope(q, k, pos, wq, wk, 1e-6, cs)
+    for got, want, name in ((qo, rq, "q"), (ko, rk, "k")):
+        if dtype == torch.float32:
+            assert (got.cpu() - want).abs().max().item() <= 1e-5, name
+        else:
+            nbad, exact = _close_16bit(got, want, dtype)
+            assert nbad == 0 and exact > 0.95, (name, nbad, exact)
+
+
 @pytest.mark.parametrize("dtype,d,T", [
     (torch.bfloat16, 128, 4099), (torch.float16, 64, 4097), (torch.float32, 128, 8561),
     (torch.bfloat16, 256, 4097)])

@@ -30,13 +30,24 @@ struct PrologueParams {
   const void* pos;
 };
 
+// An fp32 value the compiler may not fold into the operation that consumes
+// it.  On gfx950 a conversion to half can absorb the multiply or add that
+// produced its operand (v_fma_mixlo_f16), rounding once where the reference
+// rounds to fp32 first; whether it does depends on the surrounding code, so
+// two kernels running the same arithmetic could differ in the last bit.  No
+// instruction is emitted.
+__device__ inline void pin(float& x) { asm("" : "+v"(x)); }
+
 // Every element of x rounded to the element type (nearest even) and widened
 // back to float, two at a time (one packed conversion per pair; bf16 through
-// gfx950's v_cvt_pk_bf16_f32).
+// gfx950's v_cvt_pk_bf16_f32).  Each operand is first rounded to fp32, as the
+// reference's fp32 result is (pin).
 template <typename ET, int E>
 __device__ inline void round_to(float (&x)[E]) {
   static_assert(E % 2 == 0, "pairs");
   if constexpr (ET::kBytes == 2) {
+#pragma unroll
+    for (int i = 0; i < E; ++i) pin(x[i]);
 #pragma unroll
     for (int i = 0; i < E / 2; ++i) {
       if constexpr (ET::kIsBF16) {
@@ -121,6 +132,33 @@ __device__ inline void convert_weights(const WeightRaw<E>& r, int dtype, float (
   }
 }
 
+// The E norm weights of one row from raw words: 16-bit weights (kW16) from
+// r.a, as bfloat16 when `bf` is set and as half otherwise; fp32 weights from
+// r.a then r.b.  The values convert_weights gives.  A kernel that unpacks the
+// weights row by row keeps 8 words per weight array in registers instead of
+// E floats (the qk prologue kernel's occupancy depends on it).
+template <int E, bool kW16>
+__device__ inline void row_weights(const WeightRaw<E>& r, bool bf, float (&out)[E]) {
+  uint32_t wa[E / 2];
+  __builtin_memcpy(wa, &r.a, sizeof(wa));
+  if constexpr (kW16) {
+#pragma unroll
+    for (int e = 0; e < E / 2; ++e) {
+      const f16x2_t hv = __builtin_bit_cast(f16x2_t, wa[e]);
+      out[2 * e] = bf ? __uint_as_float(wa[e] << 16) : (float)hv.x;
+      out[2 * e + 1] = bf ? __uint_as_float(wa[e] & 0xffff0000u) : (float)hv.y;
+    }
+  } else {
+    uint32_t wb[E / 2];
+    __builtin_memcpy(wb, &r.b, sizeof(wb));
+#pragma unroll
+    for (int e = 0; e < E / 2; ++e) {
+      out[e] = __uint_as_float(wa[e]);
+      out[E / 2 + e] = __uint_as_float(wb[e]);
+    }
+  }
+}
+
 // Norm weight i of a weight array of `dtype`, widened to float.
 __device__ inline float load_weight(const void* w, int dtype, int i) {
   if (dtype == VA_F32) return reinterpret_cast<const float*>(w)[i];
@@ -137,12 +175,16 @@ template <int E, int LPR>
 __device__ inline void load_rotary(const PrologueParams& pp, int64_t pos, int col, int D,
                                    float (&c)[E], float (&s)[E]) {
   const float* row = pp.cs + pos * pp.cs_stride;
+  // Both halves through a pointer each, so that each loads as whole vectors
+  // (indexing the sin half from `row` left eight scalar loads, each with its
+  // own address held in registers).
+  const float* srow = row + D / 2;
   const int i0 = (col % (LPR / 2)) * E;
   const bool first_half = col < LPR / 2;
 #pragma unroll
   for (int e = 0; e < E; ++e) {
     c[e] = row[i0 + e];
-    const float sv = row[D / 2 + i0 + e];
+    const float sv = srow[i0 + e];
     s[e] = first_half ? -sv : sv;
   }
 }
@@ -176,6 +218,9 @@ __device__ inline void qk_prologue(float (&x)[E], const float (&w)[E], float eps
 #pragma unroll
     for (int e = 0; e < E; ++e) x[e] = x[e] * c[e] + pt[e] * s[e];
   }
+  // The caller's pack rounds the fp32 sums, not a fused form of them.
+#pragma unroll
+  for (int e = 0; e < E; ++e) pin(x[e]);
 }
 
 }  // namespace va

@@ -25,7 +25,13 @@ struct QkParams {
 };
 
 constexpr int kQkThreads = 256;
-constexpr int kQkChunk = 8;  // row groups whose loads a lane keeps in flight at once
+// Row groups whose loads a lane of qk_norm_rope_kernel keeps in flight at
+// once: six hold a token of 16 + 8 heads in one round trip and keep the
+// kernel at 90 VGPRs, five waves per SIMD (eight groups: 108 VGPRs, four).
+constexpr int kQkChunk = 6;
+// Head rows per token up to which prompt-sized batches take
+// qk_norm_rope_tokens_kernel (keys alone: 8 heads).
+constexpr int kQkTokenRows = 8;
 constexpr int64_t kQkTargetWaves = 4096;  // ~16 per CU: below it a token spreads over waves
 
 // A token's Hq + Hkv head rows go RPW at a time (one row per LPR-lane group)
@@ -39,8 +45,12 @@ constexpr int64_t kQkTargetWaves = 4096;  // ~16 per CU: below it a token spread
 // before the rotary loads that depend on it, so a wave costs two round trips
 // whatever its row count; rows past the wave's last read its last row and are
 // not stored, so no load sits behind a branch (row groups wholly past it are
-// not computed either).
-template <typename ET, int D>
+// not computed either).  The norm weights stay as loaded and are unpacked
+// row by row (kW16: 16-bit weights, 4 words per array instead of 8 floats):
+// at one wave per token, prompt batches run in rounds of the resident waves,
+// so the registers set the number of rounds (config 3's 8561 tokens: 25.5 us
+// at 164 VGPRs, three waves per SIMD; 24.4 at 98, four).
+template <typename ET, int D, bool kW16>
 __global__ __launch_bounds__(kQkThreads) void qk_norm_rope_kernel(QkParams p) {
   constexpr int E = ET::kPerVec;
   constexpr int LPR = D / E;     // lanes per head row
@@ -69,7 +79,8 @@ __global__ __launch_bounds__(kQkThreads) void qk_norm_rope_kernel(QkParams p) {
   // against 27.7 with the default policy; non-temporal loads alone lose
   // (28.3), stores alone win less (26.1), and a decode that reads the rows
   // next runs as before.
-  float c[E], s[E], wq[E], wk[E];
+  const bool wbf = p.pp.w_dtype == VA_BF16;
+  float c[E], s[E];
   for (int h0 = r0; h0 < r1; h0 += kQkChunk * RPW) {
     uint4 raw[kQkChunk];
 #pragma unroll
@@ -81,8 +92,6 @@ __global__ __launch_bounds__(kQkThreads) void qk_norm_rope_kernel(QkParams p) {
     if (h0 == r0) {
       pos = pos < 0 ? 0 : (pos >= p.pp.max_pos ? p.pp.max_pos - 1 : pos);
       load_rotary<E, LPR>(p.pp, pos, col, D, c, s);
-      convert_weights<E>(wqr, p.pp.w_dtype, wq);
-      convert_weights<E>(wkr, p.pp.w_dtype, wk);
     }
 #pragma unroll
     for (int j = 0; j < kQkChunk; ++j) {
@@ -91,8 +100,10 @@ __global__ __launch_bounds__(kQkThreads) void qk_norm_rope_kernel(QkParams p) {
       const bool isq = hh < p.hq;
       float x[E], wv[E];
       ET::unpack(raw[j], x);
-#pragma unroll
-      for (int e = 0; e < E; ++e) wv[e] = isq ? wq[e] : wk[e];
+      WeightRaw<E> wr;
+      wr.a = isq ? wqr.a : wkr.a;
+      if constexpr (!kW16) wr.b = isq ? wqr.b : wkr.b;
+      row_weights<E, kW16>(wr, wbf, wv);
       qk_prologue<ET, LPR, E>(x, wv, p.pp.eps, D, c, s);
       if (hh < r1)
         st16_nt(isq ? qdst + hh * p.qo_sh : kdst + (int64_t)(hh - p.hq) * p.ko_sh, ET::pack(x));
@@ -100,7 +111,7 @@ __global__ __launch_bounds__(kQkThreads) void qk_norm_rope_kernel(QkParams p) {
   }
 }
 
-// Few head rows per token (at most kQkChunk, as for keys alone): a wave takes
+// Few head rows per token (at most kQkTokenRows, as for keys alone): a wave takes
 // RPW tokens, one per LPR-lane group, and every head row of them, all of its
 // row loads in flight at once.  A token per wave would leave each wave a
 // kilobyte or two behind two dependent round trips (position, then rotary);
@@ -120,7 +131,7 @@ __global__ __launch_bounds__(kQkThreads) void qk_norm_rope_tokens_kernel(QkParam
   const int64_t tok_raw = w * RPW + lane / LPR;
   const bool live = tok_raw < p.num_tokens;
   const int64_t tok = live ? tok_raw : p.num_tokens - 1;
-  const int heads = p.hq + p.hkv;  // <= kQkChunk (host)
+  const int heads = p.hq + p.hkv;  // <= kQkTokenRows (host)
   int64_t pos = load_index(p.pp.pos, tok, p.pp.pos_i64);
   const WeightRaw<E> wqr = load_weights_raw<E>(p.hq > 0 ? p.pp.q_w : p.pp.k_w, p.pp.w_dtype, col * E);
   const WeightRaw<E> wkr = load_weights_raw<E>(p.hkv > 0 ? p.pp.k_w : p.pp.q_w, p.pp.w_dtype, col * E);
@@ -128,9 +139,9 @@ __global__ __launch_bounds__(kQkThreads) void qk_norm_rope_tokens_kernel(QkParam
   const char* const krow = p.k + tok * p.k_st + col * 16;
   char* const qdst = p.qo + tok * p.qo_st + col * 16;
   char* const kdst = p.ko + tok * p.ko_st + col * 16;
-  uint4 raw[kQkChunk];
+  uint4 raw[kQkTokenRows];
 #pragma unroll
-  for (int j = 0; j < kQkChunk; ++j) {
+  for (int j = 0; j < kQkTokenRows; ++j) {
     const int hh = j < heads ? j : heads - 1;
     raw[j] = ld16_nt(hh < p.hq ? qrow + hh * p.q_sh : krow + (int64_t)(hh - p.hq) * p.k_sh);
   }
@@ -140,7 +151,7 @@ __global__ __launch_bounds__(kQkThreads) void qk_norm_rope_tokens_kernel(QkParam
   convert_weights<E>(wqr, p.pp.w_dtype, wq);
   convert_weights<E>(wkr, p.pp.w_dtype, wk);
 #pragma unroll
-  for (int j = 0; j < kQkChunk; ++j) {
+  for (int j = 0; j < kQkTokenRows; ++j) {
     if (j >= heads) break;
     const bool isq = j < p.hq;
     float x[E], wv[E];
@@ -152,14 +163,20 @@ __global__ __launch_bounds__(kQkThreads) void qk_norm_rope_tokens_kernel(QkParam
   }
 }
 
-template <typename ET>
-static bool launch_qk(int D, const QkParams& p, dim3 grid, hipStream_t st) {
+template <typename ET, bool kW16>
+static bool launch_qk_w(int D, const QkParams& p, dim3 grid, hipStream_t st) {
   switch (D) {
-    case 64: hipLaunchKernelGGL((qk_norm_rope_kernel<ET, 64>), grid, dim3(kQkThreads), 0, st, p); return true;
-    case 128: hipLaunchKernelGGL((qk_norm_rope_kernel<ET, 128>), grid, dim3(kQkThreads), 0, st, p); return true;
-    case 256: hipLaunchKernelGGL((qk_norm_rope_kernel<ET, 256>), grid, dim3(kQkThreads), 0, st, p); return true;
+    case 64: hipLaunchKernelGGL((qk_norm_rope_kernel<ET, 64, kW16>), grid, dim3(kQkThreads), 0, st, p); return true;
+    case 128: hipLaunchKernelGGL((qk_norm_rope_kernel<ET, 128, kW16>), grid, dim3(kQkThreads), 0, st, p); return true;
+    case 256: hipLaunchKernelGGL((qk_norm_rope_kernel<ET, 256, kW16>), grid, dim3(kQkThreads), 0, st, p); return true;
     default: return false;
   }
+}
+
+template <typename ET>
+static bool launch_qk(int D, const QkParams& p, dim3 grid, hipStream_t st) {
+  return p.pp.w_dtype == VA_F32 ? launch_qk_w<ET, false>(D, p, grid, st)
+                                : launch_qk_w<ET, true>(D, p, grid, st);
 }
 
 template <typename ET>
@@ -241,7 +258,7 @@ extern "C" int va_qk_norm_rope(const va_qk_norm_rope_args* a, void* stream) {
   const int rpw = 64 / (a->head_dim / E);
   const int heads = a->num_heads + a->num_kv_heads;
   const hipStream_t st = (hipStream_t)stream;
-  if (heads <= kQkChunk && a->num_tokens >= kQkTargetWaves) {
+  if (heads <= kQkTokenRows && a->num_tokens >= kQkTargetWaves) {
     // Prompt-sized batches with few rows per token: RPW tokens per wave.
     const int64_t waves = ((int64_t)a->num_tokens + rpw - 1) / rpw;
     const dim3 grid((unsigned)((waves + kQkThreads / 64 - 1) / (kQkThreads / 64)));

@@ -694,7 +694,11 @@ __global__ __launch_bounds__(kVarlenThreads, 2) void varlen_attention_kernel(Var
                 }
             }
 #pragma unroll
-            for (int ds = 0; ds < DS; ++ds) qreg[tt][ds] = ET::pack(x[ds]);
+            for (int ds = 0; ds < DS; ++ds) {
+#pragma unroll
+              for (int e = 0; e < 8; ++e) pin(x[ds][e]);  // pack the fp32 sums
+              qreg[tt][ds] = ET::pack(x[ds]);
+            }
           };
           pro_row(std::integral_constant<int, 0>{});
           pro_row(std::integral_constant<int, 1>{});
