@@ -134,9 +134,9 @@ __device__ inline void convert_weights(const WeightRaw<E>& r, int dtype, float (
 
 // The E norm weights of one row from raw words: 16-bit weights (kW16) from
 // r.a, as bfloat16 when `bf` is set and as half otherwise; fp32 weights from
-// r.a then r.b.  The values convert_weights gives.  A kernel that unpacks the
-// weights row by row keeps 8 words per weight array in registers instead of
-// E floats (the qk prologue kernel's occupancy depends on it).
+// r.a then r.b.  The values convert_weights gives.  A kernel that unpacks
+// 16-bit weights row by row keeps E/2 words per weight array in registers
+// instead of E floats (the qk prologue kernel's occupancy depends on it).
 template <int E, bool kW16>
 __device__ inline void row_weights(const WeightRaw<E>& r, bool bf, float (&out)[E]) {
   uint32_t wa[E / 2];

@@ -46,10 +46,11 @@ constexpr int64_t kQkTargetWaves = 4096;  // ~16 per CU: below it a token spread
 // whatever its row count; rows past the wave's last read its last row and are
 // not stored, so no load sits behind a branch (row groups wholly past it are
 // not computed either).  The norm weights stay as loaded and are unpacked
-// row by row (kW16: 16-bit weights, 4 words per array instead of 8 floats):
-// at one wave per token, prompt batches run in rounds of the resident waves,
-// so the registers set the number of rounds (config 3's 8561 tokens: 25.5 us
-// at 164 VGPRs, three waves per SIMD; 24.4 at 98, four).
+// row by row (kW16: 16-bit weights, E/2 words per array instead of E
+// floats): at one wave per token, prompt batches run in rounds of the
+// resident waves, so the registers set the number of rounds (config 3's 8561
+// tokens: 25.5 us at 164 VGPRs, three waves per SIMD; 24.4 at 98, four; 23.8
+// at 90, five).
 template <typename ET, int D, bool kW16>
 __global__ __launch_bounds__(kQkThreads) void qk_norm_rope_kernel(QkParams p) {
   constexpr int E = ET::kPerVec;
