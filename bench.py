@@ -845,7 +845,42 @@ def bench_store(args, dev, stream, dec):
     us = ms * 1000.0 / workloads.LAYERS
     nbytes = workloads.store_bytes(B)
     log(f"[store] {us:.2f} us/layer ({nbytes} B, latency-bound)")
-    return dict(us_layer=us, gbs=nbytes / (us * 1e-6) / 1e9)
+    res = dict(us_layer=us, gbs=nbytes / (us * 1e-6) / 1e9)
+
+    # A prefill-sized store, as an unfused caller runs it: config 3's 8561 new K
+    # and V rows per layer scattered into a block-16 pool, 28 layers each with
+    # its own rows and pool (cold), slots in a shuffled block order.
+    lens = workloads.cfg3_lens(0)
+    total, layers, bs = sum(lens), workloads.LAYERS, workloads.BLOCK
+    g = torch.Generator(device=dev).manual_seed(21)
+    kr = torch.randn(layers, total, workloads.HKV, workloads.HEAD_DIM, generator=g,
+                     device=dev).to(torch.bfloat16)
+    vr = torch.randn_like(kr)
+    nb = sum(math.ceil(n / bs) for n in lens) + 8
+    perm = torch.randperm(nb, generator=torch.Generator().manual_seed(22)).tolist()
+    slots, cur = [], 0
+    for n in lens:
+        slots += [perm[cur + p // bs] * bs + p % bs for p in range(n)]
+        cur += math.ceil(n / bs)
+    slots = torch.tensor(slots, dtype=torch.int32, device=dev)
+    kp = torch.zeros(layers, nb, bs, workloads.HKV, workloads.HEAD_DIM, dtype=torch.bfloat16,
+                     device=dev)
+    vp = torch.zeros_like(kp)
+
+    def step_prefill():
+        for i in range(layers):
+            ops.store_kvcache(kr[i], vr[i], kp[i], vp[i], slots)
+
+    ms, _ = timed_graph(step_prefill, args.steps, args.warmup, stream, name="store_cfg3")
+    us3 = ms * 1000.0 / layers
+    nbytes3 = workloads.store_bytes(total)
+    gbs3 = nbytes3 / (us3 * 1e-6) / 1e9
+    log(f"[store cfg3] {total} rows: {us3:.2f} us/layer, {gbs3:.0f} GB/s of {nbytes3 / 1e6:.1f} MB "
+        f"({gbs3 / 8000:.3f} of HBM peak)")
+    res["cfg3_rows"] = dict(us_layer=round(us3, 2), gbs=round(gbs3, 1), bytes=nbytes3,
+                            frac=round(gbs3 / 8000, 4))
+    del kr, vr, kp, vp
+    return res
 
 
 def bench_prefill(args, dev, stream):

@@ -77,3 +77,38 @@ def test_store_prefill_sized(dev):
     store_kvcache(key.to(dev), val.to(dev), kc, vc, slots.to(dev))
     torch.cuda.synchronize()
     assert torch.equal(kc.cpu(), ek) and torch.equal(vc.cpu(), ev)
+
+
+@pytest.mark.parametrize("kind,slot_dtype", [
+    ("bf16", torch.int32), ("bf16", torch.int64), ("f32", torch.int64), ("fp8", torch.int32),
+    ("fp8", torch.int64)])
+def test_store_four_words_per_lane(dev, kind, slot_dtype):
+    # Launches of at least 256 workgroups' worth of words move four 16-byte words
+    # per lane per pass (all loads before the stores); 2051 tokens end on a partial
+    # pass, and every fifth slot is -1 and a few are past the pool (both skipped).
+    n, nb, bs = 2051, 160, 16
+    dtype = torch.float32 if kind == "f32" else torch.bfloat16
+    g = torch.Generator().manual_seed(40)
+    key = torch.randn(n, 8, 128, generator=g).to(dtype)
+    val = torch.randn(n, 8, 128, generator=g).to(dtype)
+    slots = torch.randperm(nb * bs, generator=g)[:n].to(slot_dtype)
+    slots[::5] = -1
+    slots[3::97] = nb * bs + 7
+    ref_slots = torch.where(slots >= nb * bs, torch.full_like(slots, -1), slots)
+    ks, vs = (0.05, 0.08) if kind == "fp8" else (1.0, 1.0)
+    if kind == "fp8":
+        kc = oracle.quantize_fp8(torch.randn(nb, bs, 8, 128, generator=g), ks)
+        vc = oracle.quantize_fp8(torch.randn(nb, bs, 8, 128, generator=g), vs)
+    else:
+        kc = torch.randn(nb, bs, 8, 128, generator=g).to(dtype)
+        vc = torch.randn(nb, bs, 8, 128, generator=g).to(dtype)
+    ek, ev = oracle.store_kvcache(key, val, kc, vc, ref_slots, k_scale=ks, v_scale=vs)
+    kd, vd = kc.to(dev), vc.to(dev)
+    print(f"store {kind} slots {slot_dtype} n={n}", flush=True)
+    ops.store_kvcache(key.to(dev), val.to(dev), kd, vd, slots.to(dev), k_scale=ks, v_scale=vs)
+    torch.cuda.synchronize()
+    if kind == "fp8":
+        assert torch.equal(kd.cpu().view(torch.uint8), ek.view(torch.uint8))
+        assert torch.equal(vd.cpu().view(torch.uint8), ev.view(torch.uint8))
+    else:
+        assert torch.equal(kd.cpu(), ek) and torch.equal(vd.cpu(), ev)
