@@ -531,9 +531,12 @@ def bench_floor(args, dev, stream):
                                    workloads.HEAD_DIM) * 2 // 3  # q + k + v
     pre_w = pre_r  # output + stored K/V rows
     enc_all = workloads.varlen_bytes(wins, 14, 14, 64)
+    # store_kvcache of config 3's rows: K and V read, then written.
+    st_rw = workloads.store_bytes(sum(pre_lens)) // 2
     copies = {"prefill_cfg3": copy_floor("prefill cfg3", pre_r, pre_w, layers, args, dev, stream),
               "encoder_cfg4": copy_floor("encoder cfg4", enc_all * 3 // 4, enc_all // 4, 18,
-                                         args, dev, stream)}
+                                         args, dev, stream),
+              "store_cfg3": copy_floor("store cfg3", st_rw, st_rw, layers, args, dev, stream)}
     empty = launch_floor(args, stream)
     depth = depth_probe(dev, stream)
     return {"us_per_launch": round(us, 2), "gbs": round(gbs, 1), "copy": copies,
