@@ -11,12 +11,12 @@
 // A lane moves kStoreWords (4) words per pass, 256 words apart, so consecutive
 // lanes touch consecutive 16-byte words (coalesced on both sides), and it
 // issues every word's load (a DMA into LDS) and slot load before its first
-// store: a wave keeps 4 KiB in flight and pays one round trip per pass.  (One word per lane, with
-// the data load behind its slot check, kept 1 KiB per wave in flight behind
-// two dependent round trips: config 3's 8561 rows ran at 4.05 TB/s.)  Rows are
-// read and written non-temporally: each is touched once.  Indices are 32-bit
-// (the host splits a launch whose words reach 2^31) and divide by
-// multiply-and-shift.
+// store: a wave keeps 4 KiB in flight and pays one round trip per pass.  (One
+// word per lane, with the data load behind its slot check, kept 1 KiB per
+// wave in flight behind two dependent round trips: config 3's 8561 rows ran
+// at 4.05 TB/s.)  Rows are read and written non-temporally: each is touched
+// once.  Indices are 32-bit (the host splits a launch whose words reach
+// 2^31) and divide by multiply-and-shift.
 //
 // An FP8 pool (VA_KV_FP8_E4M3) receives each 16-byte word of 8 16-bit
 // elements as 8 e4m3 codes, x * (1 / scale) saturated to +-448 and rounded
