@@ -371,3 +371,36 @@ def test_fused_prologue_over_fp8_pool(dev, B):
                                      k_scale=ks, v_scale=vs)
     ref = oracle.paged_decode(rq, ek, ev, table, lens_t, 128 ** -0.5, k_scale=ks, v_scale=vs)
     assert _err(out1, ref) <= 2e-2
+
+
+@pytest.mark.parametrize("split", [1024, 4096])
+def test_fp8_decode_either_side_of_the_twelve_wave_bound(dev, split):
+    # Over FP8 pools at head_dim 128 a workgroup that attends at most 2048
+    # tokens runs twelve waves, a longer one eight.  One batch, partitions of
+    # 1024 and of 4096 tokens, with the fused prologue, the key mask and the
+    # fused store: both match the oracle on the dequantised pool.
+    lens = [1, 17, 700, 2500, 5000]
+    ks, vs = 0.05, 0.08
+    table, kp, vp, q, nk, nv = _fp8_batch(lens, dev, seed=split, k_scale=ks, v_scale=vs)
+    g = torch.Generator().manual_seed(split + 1)
+    wq = (torch.rand(128, generator=g) + 0.5).to(torch.bfloat16)
+    wk = (torch.rand(128, generator=g) + 0.5).to(torch.bfloat16)
+    cs = oracle.rope_cache(128, 8192, 1_000_000.0)
+    pos = torch.tensor(lens) - 1
+    lens_t = torch.tensor(lens, dtype=torch.int32)
+    valid = torch.rand(len(lens), max(lens) + 3, generator=g) < 0.85
+    print(f"fp8 decode, partitions of {split} tokens", flush=True)
+    pro = ops.QKPrologue(wq.to(dev), wk.to(dev), 1e-6, cs.to(dev), pos.to(dev))
+    kd, vd = kp.to(dev), vp.to(dev)
+    out = ops.paged_decode(q.to(dev), kd, vd, table.to(dev), lens_t.to(dev),
+                           max_seq_len=max(lens), split_tokens=split, scale=128 ** -0.5,
+                           valid_mask=valid.to(dev), new_k=nk.to(dev), new_v=nv.to(dev),
+                           prologue=pro, k_scale=ks, v_scale=vs)
+    torch.cuda.synchronize()
+    rq, rk = oracle.qk_norm_rope(q, nk, pos, wq, wk, 1e-6, cs)
+    ek, ev = oracle.write_current_kv(kp, vp, table, lens_t, rk, nv, layout=ops.LAYOUT_NHD,
+                                     k_scale=ks, v_scale=vs)
+    assert torch.equal(_codes(kd.cpu()), _codes(ek)) and torch.equal(_codes(vd.cpu()), _codes(ev))
+    ref = oracle.paged_decode(rq, ek, ev, table, lens_t, 128 ** -0.5, valid_mask=valid,
+                              k_scale=ks, v_scale=vs)
+    assert _err(out, ref) <= 2e-2

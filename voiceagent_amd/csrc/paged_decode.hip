@@ -18,7 +18,12 @@ struct DecodePlan {
   int max_parts;
   int dyn_split;
   size_t ml_bytes, o_bytes, total_bytes;
+  int64_t wg_tokens;  // most tokens one workgroup attends (bound from max_seq_len)
 };
+
+// FP8 pools at head_dim 128 take twelve-wave workgroups when no workgroup
+// attends more tokens than this (see MfmaWaves).
+constexpr int64_t kWave12Tokens = 2048;
 
 template <typename ET, int D, int G>
 static int decode_unit() {
@@ -95,6 +100,7 @@ static DecodePlan plan_decode(const va_decode_args* a) {
   if (small_head_decode(a)) {  // one workgroup per (sequence, query head), no split
     pl.max_parts = 1;
     pl.split_tokens = a->max_seq_len > 0 ? a->max_seq_len : 1;
+    pl.wg_tokens = pl.split_tokens;
     return pl;
   }
   const int G = a->num_kv_heads > 0 ? a->num_heads / a->num_kv_heads : 1;
@@ -141,6 +147,7 @@ static DecodePlan plan_decode(const va_decode_args* a) {
       P = (P + kDynGrain - 1) / kDynGrain * kDynGrain;
       pl.split_tokens = P;
       pl.max_parts = (max_len + P - 1) / P;
+      pl.wg_tokens = P;
       pl.ml_bytes = ((size_t)pairs * pl.max_parts * G * 2 * 4 + 255) / 256 * 256;
       pl.o_bytes = (size_t)pairs * pl.max_parts * G * a->head_dim * 4;
       pl.total_bytes = pl.ml_bytes + pl.o_bytes;
@@ -150,6 +157,7 @@ static DecodePlan plan_decode(const va_decode_args* a) {
       pl.dyn_split = 1;
       pl.split_tokens = kDynGrain;
       pl.max_parts = (int)parts;
+      pl.wg_tokens = (max_len + parts - 1) / parts;
       pl.ml_bytes = ((size_t)pairs * pl.max_parts * G * 2 * 4 + 255) / 256 * 256;
       pl.o_bytes = (size_t)pairs * pl.max_parts * G * a->head_dim * 4;
       pl.total_bytes = pl.ml_bytes + pl.o_bytes;
@@ -164,6 +172,7 @@ static DecodePlan plan_decode(const va_decode_args* a) {
   if (P < unit) P = unit;
   pl.split_tokens = P;
   pl.max_parts = (max_len + P - 1) / P;
+  pl.wg_tokens = P < max_len ? P : max_len;
   if (pl.max_parts > 1) {
     pl.ml_bytes = ((size_t)pairs * pl.max_parts * G * 2 * 4 + 255) / 256 * 256;
     pl.o_bytes = (size_t)pairs * pl.max_parts * G * a->head_dim * 4;
@@ -434,6 +443,7 @@ int va::paged_decode_impl(const va_decode_args* a, void* stream) {
   // output (applied after the weighted sum).
   p.scale_log2 = a->scale * (f8 ? a->pool.k_scale : 1.0f) * 1.4426950408889634f;
   p.kv_fp8 = f8;
+  p.wave12 = f8 && a->head_dim == 128 && pl.wg_tokens <= kWave12Tokens;
   p.v_scale = f8 ? a->pool.v_scale : 1.0f;
   p.inv_k = f8 ? 1.0f / a->pool.k_scale : 1.0f;
   p.inv_v = f8 ? 1.0f / a->pool.v_scale : 1.0f;

@@ -9,9 +9,10 @@
 // of its group.
 //
 // Work decomposition.  A workgroup is W wave64s (8, two per SIMD, for head
-// dims up to 128; 4 for 256).  The partition's 16-token tiles go round robin
-// to the waves (tile c to wave c % W), and each wave runs its own pipeline
-// with no workgroup barrier:
+// dims up to 128; 4 for 256; 12 over FP8 pools at head_dim 128 when a
+// workgroup attends few tokens, see MfmaWaves).  The partition's 16-token
+// tiles go round robin to the waves (tile c to wave c % W), and each wave
+// runs its own pipeline with no workgroup barrier:
 //   * the K and V rows of a tile (16 rows of one block) are copied from HBM
 //     straight into the wave's LDS ring of S stages with
 //     global_load_lds_dwordx4 (1 KiB per instruction, 16-byte chunks stored
@@ -104,6 +105,22 @@ struct MfmaDecodeShape {
   static constexpr int RPL = 64 / LPR;         // rows per wave in the row layout
 };
 
+// Waves per workgroup and LDS bytes per wave.  kW12: twelve waves (three per
+// SIMD) with 12 KiB each, for FP8 pools at head_dim 128 when a workgroup
+// streams few tokens (the host's choice, DecodeParams::wave12).  Over FP8 a
+// long context's tail is bound by its tiles' arithmetic (code reads,
+// conversions and the transposed V reads each wait on LDS), and a third wave
+// per SIMD hides more of it: config 2 over FP8 pools 11.5 -> 10.8 us/layer,
+// one 16K context 14.4 -> 13.8; with ~4K tokens per workgroup (config 5's
+// eight long contexts) two stages per wave instead of three lost (45.0 ->
+// 45.9), so those keep eight waves.
+template <int D, bool kW12>
+struct MfmaWaves {
+  static_assert(!kW12 || D == 128, "twelve waves at head_dim 128 only");
+  static constexpr int W = kW12 ? 12 : MfmaDecodeShape<D>::W;
+  static constexpr int WAVE_B = kW12 ? 12 * 1024 : MfmaDecodeShape<D>::WAVE_B;
+};
+
 // Tokens per partition unit of the matrix-core kernel: one round of S tiles
 // on every wave.
 template <int D>
@@ -135,12 +152,14 @@ constexpr float kDecLazy = 8.0f;
 // into a 16-bit tile in the wave's conversion area, which the transposed
 // reads below use as they use a staged 16-bit tile.  k_scale is folded into
 // the softmax scale and v_scale into the output.
-template <typename ET, int D, int G, bool kProlog, bool kMask, bool kF8>
-__global__ __launch_bounds__(MfmaDecodeShape<D>::W * 64, 1) void paged_decode_mfma_kernel(
+template <typename ET, int D, int G, bool kProlog, bool kMask, bool kF8, bool kW12 = false>
+__global__ __launch_bounds__((MfmaWaves<D, kW12>::W * 64), 1) void paged_decode_mfma_kernel(
     DecodeParams p) {
+  static_assert(!kW12 || kF8, "twelve waves over FP8 pools only");
   using Sh = MfmaDecodeShape<D>;
   using M = DecodeMma<ET>;
-  constexpr int W = Sh::W, ROWB = Sh::ROWB;
+  constexpr int W = MfmaWaves<D, kW12>::W, ROWB = Sh::ROWB;
+  constexpr int RING_B = MfmaWaves<D, kW12>::WAVE_B;  // LDS bytes per wave
   constexpr int TILE_B = Sh::TILE_B, DS = Sh::DS, DT = Sh::DT;
   constexpr int LPR = Sh::LPR, RPL = Sh::RPL, E = 8;
   // A tile as the DMA stages it: 16-bit rows, or rows of D e4m3 codes.
@@ -154,11 +173,11 @@ __global__ __launch_bounds__(MfmaDecodeShape<D>::W * 64, 1) void paged_decode_mf
   // 16-bit conversion area (one tile), so the wave's LDS holds more stages
   // of codes than of 16-bit rows (3 for head_dim 128, at most 4).
   constexpr int CONV_B = kF8 ? TILE_B : 0;
-  constexpr int S_F8 = (Sh::WAVE_B - CONV_B) / STAGE_B;
+  constexpr int S_F8 = (RING_B - CONV_B) / STAGE_B;
   constexpr int S = kF8 ? (S_F8 > 4 ? 4 : S_F8) : Sh::S;  // stages of the wave's ring
   static_assert(S >= 2, "two stages at least");
   constexpr int WAVE_B = S * STAGE_B + CONV_B;  // LDS bytes per wave
-  static_assert(WAVE_B <= Sh::WAVE_B, "FP8 stages and conversion area fit the 16-bit ring");
+  static_assert(WAVE_B <= RING_B, "FP8 stages and conversion area fit the wave's LDS");
   constexpr int NT = W * 64;
   constexpr int QROWS = (G + RPL - 1) / RPL;  // query rows per lane in the row layout
   static_assert(G <= 16, "at most 16 query heads per kv head");
@@ -168,10 +187,10 @@ __global__ __launch_bounds__(MfmaDecodeShape<D>::W * 64, 1) void paged_decode_mf
   // reuse the ring once every wave is done with it.
   constexpr int MERGE_B = W * G * D * 4 + 2 * G * W * 4;
   constexpr int Q_B = kProlog ? W * G * ROWB : 16;
-  constexpr bool kOwnMerge = W * Sh::WAVE_B + MERGE_B + Q_B <= 160 * 1024;
-  static_assert(MERGE_B <= W * Sh::WAVE_B, "merge scratch");
+  constexpr bool kOwnMerge = W * RING_B + MERGE_B + Q_B <= 160 * 1024;
+  static_assert(MERGE_B <= W * RING_B, "merge scratch");
 
-  __shared__ __align__(1024) char s_buf[W * Sh::WAVE_B];
+  __shared__ __align__(1024) char s_buf[W * RING_B];
   // Apart from the tile ring, so that early tile DMAs cannot land on them:
   // the query rows of the prologue (per wave).
   __shared__ __align__(16) char s_q[Q_B];
@@ -723,23 +742,37 @@ __global__ __launch_bounds__(MfmaDecodeShape<D>::W * 64, 1) void paged_decode_mf
 }
 
 // ------------------------------------------------------------- launching
-template <typename ET, int D, int G, bool kF8>
-static void launch_decode_mfma(const DecodeParams& p, dim3 grid, hipStream_t s) {
-  constexpr int NT = MfmaDecodeShape<D>::W * 64;
+template <typename ET, int D, int G, bool kF8, bool kW12>
+static void launch_decode_mfma_w(const DecodeParams& p, dim3 grid, hipStream_t s) {
+  constexpr int NT = MfmaWaves<D, kW12>::W * 64;
   const dim3 hgrid(grid.y, grid.x, grid.z);  // (kv head, sequence, partition)
   const bool mask = p.valid != nullptr && p.valid_len > 0;
   if (p.has_pro && mask)
-    hipLaunchKernelGGL((paged_decode_mfma_kernel<ET, D, G, true, true, kF8>), hgrid, dim3(NT), 0,
-                       s, p);
+    hipLaunchKernelGGL((paged_decode_mfma_kernel<ET, D, G, true, true, kF8, kW12>), hgrid,
+                       dim3(NT), 0, s, p);
   else if (p.has_pro)
-    hipLaunchKernelGGL((paged_decode_mfma_kernel<ET, D, G, true, false, kF8>), hgrid, dim3(NT), 0,
-                       s, p);
+    hipLaunchKernelGGL((paged_decode_mfma_kernel<ET, D, G, true, false, kF8, kW12>), hgrid,
+                       dim3(NT), 0, s, p);
   else if (mask)
-    hipLaunchKernelGGL((paged_decode_mfma_kernel<ET, D, G, false, true, kF8>), hgrid, dim3(NT), 0,
-                       s, p);
+    hipLaunchKernelGGL((paged_decode_mfma_kernel<ET, D, G, false, true, kF8, kW12>), hgrid,
+                       dim3(NT), 0, s, p);
   else
-    hipLaunchKernelGGL((paged_decode_mfma_kernel<ET, D, G, false, false, kF8>), hgrid, dim3(NT), 0,
-                       s, p);
+    hipLaunchKernelGGL((paged_decode_mfma_kernel<ET, D, G, false, false, kF8, kW12>), hgrid,
+                       dim3(NT), 0, s, p);
+}
+
+template <typename ET, int D, int G, bool kF8>
+static void launch_decode_mfma(const DecodeParams& p, dim3 grid, hipStream_t s) {
+  // Twelve waves: FP8 pools at head_dim 128 and groups up to 4 (a G = 8
+  // prologue's query rows would not fit beside twelve waves' LDS).
+  bool done = false;
+  if constexpr (kF8 && D == 128 && G <= 4) {
+    if (p.wave12) {
+      launch_decode_mfma_w<ET, D, G, kF8, true>(p, grid, s);
+      done = true;
+    }
+  }
+  if (!done) launch_decode_mfma_w<ET, D, G, kF8, false>(p, grid, s);
   if (p.max_parts > 1)
     hipLaunchKernelGGL((paged_decode_merge_kernel<ET, D, G, kF8 ? 1 : 0>), dim3(grid.y, grid.x),
                        dim3(256), 0, s, p);
