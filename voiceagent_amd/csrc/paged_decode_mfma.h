@@ -46,6 +46,8 @@ typedef _Float16 mf_f16x4 __attribute__((ext_vector_type(4)));
 typedef short mf_s16x4 __attribute__((ext_vector_type(4)));
 typedef float mf_f32x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) mf_s16x4 mf_lds_s16x4;
+typedef int mf_s32x2 __attribute__((ext_vector_type(2)));
+typedef __attribute__((address_space(3))) mf_s32x2 mf_lds_s32x2;
 
 template <typename ET>
 struct DecodeMma;
@@ -105,20 +107,23 @@ struct MfmaDecodeShape {
   static constexpr int RPL = 64 / LPR;         // rows per wave in the row layout
 };
 
-// Waves per workgroup and LDS bytes per wave.  kW12: twelve waves (three per
-// SIMD) with 12 KiB each, for FP8 pools at head_dim 128 when a workgroup
-// streams few tokens (the host's choice, DecodeParams::wave12).  Over FP8 a
-// long context's tail is bound by its tiles' arithmetic (code reads,
-// conversions and the transposed V reads each wait on LDS), and a third wave
-// per SIMD hides more of it: config 2 over FP8 pools 11.5 -> 10.8 us/layer,
-// one 16K context 14.4 -> 13.8; with ~4K tokens per workgroup (config 5's
-// eight long contexts) two stages per wave instead of three lost (45.0 ->
-// 45.9), so those keep eight waves.
+// Waves per workgroup and the most LDS bytes a wave's ring may take.  kW12:
+// twelve waves (three per SIMD) with two stages of codes each, for FP8 pools
+// at head_dim 128 when a workgroup streams few tokens (the host's choice,
+// DecodeParams::wave12).  Over FP8 a long context's tail is bound by its
+// tiles' arithmetic (code reads and conversions wait on LDS), and a third
+// wave per SIMD hides more of it (config 2 over FP8 pools 11.5 -> 10.7
+// us/layer, one 16K context 14.3 -> 13.8, measured when V still went through
+// a 16-bit conversion area).  With ~4K tokens per workgroup (config 5's
+// eight long contexts) two stages are too few (44.6 -> 45.6 us/layer), so
+// those keep eight waves with three stages.  (Measured and dropped: sixteen
+// waves with two stages, config 2 10.5 and one 16K context 14.0 against 10.3
+// and 13.5.)
 template <int D, bool kW12>
 struct MfmaWaves {
   static_assert(!kW12 || D == 128, "twelve waves at head_dim 128 only");
   static constexpr int W = kW12 ? 12 : MfmaDecodeShape<D>::W;
-  static constexpr int WAVE_B = kW12 ? 12 * 1024 : MfmaDecodeShape<D>::WAVE_B;
+  static constexpr int WAVE_B = kW12 ? 8 * 1024 : MfmaDecodeShape<D>::WAVE_B;
 };
 
 // Tokens per partition unit of the matrix-core kernel: one round of S tiles
@@ -148,10 +153,10 @@ constexpr float kDecLazy = 8.0f;
 // kMask: the launch has a key_valid_mask (a separate instantiation, so the
 // kernel without one carries none of its loads or branches).  kF8: the pool
 // holds OCP e4m3 codes.  S^T reads a staged K tile's codes, eight per lane,
-// and converts them, exactly, in registers; a staged V tile is converted
-// into a 16-bit tile in the wave's conversion area, which the transposed
-// reads below use as they use a staged 16-bit tile.  k_scale is folded into
-// the softmax scale and v_scale into the output.
+// and converts them, exactly, in registers; V^T is read from the staged V
+// codes with ds_read_b64_tr_b8, one read giving the lane its four tokens of
+// two 16-dim blocks, converted in registers as well.  k_scale is folded
+// into the softmax scale and v_scale into the output.
 template <typename ET, int D, int G, bool kProlog, bool kMask, bool kF8, bool kW12 = false>
 __global__ __launch_bounds__((MfmaWaves<D, kW12>::W * 64), 1) void paged_decode_mfma_kernel(
     DecodeParams p) {
@@ -169,15 +174,16 @@ __global__ __launch_bounds__((MfmaWaves<D, kW12>::W * 64), 1) void paged_decode_
   constexpr int NI = kChunk / RPI;          // DMA instructions per tile, K or V
   constexpr int PTILE = kChunk * PROWB;     // staged bytes of one K (or V) tile
   constexpr int STAGE_B = 2 * PTILE;
-  // FP8: K is read as codes straight from its stage; only V goes through a
-  // 16-bit conversion area (one tile), so the wave's LDS holds more stages
-  // of codes than of 16-bit rows (3 for head_dim 128, at most 4).
-  constexpr int CONV_B = kF8 ? TILE_B : 0;
-  constexpr int S_F8 = (RING_B - CONV_B) / STAGE_B;
-  constexpr int S = kF8 ? (S_F8 > 4 ? 4 : S_F8) : Sh::S;  // stages of the wave's ring
+  // FP8: K and V are read as codes straight from their stage, half the bytes
+  // of 16-bit rows, and the wave keeps at most three stages of them: a
+  // fourth (a third with twelve waves) only enlarges the launch's first
+  // burst of requests, whose last tiles then land later (config 2 over FP8
+  // pools 10.3 -> 11.0 us/layer, one 16K context 13.5 -> 14.2).
+  constexpr int S_F8 = RING_B / STAGE_B < 3 ? RING_B / STAGE_B : 3;
+  constexpr int S = kF8 ? S_F8 : Sh::S;  // stages of the wave's ring
   static_assert(S >= 2, "two stages at least");
-  constexpr int WAVE_B = S * STAGE_B + CONV_B;  // LDS bytes per wave
-  static_assert(WAVE_B <= RING_B, "FP8 stages and conversion area fit the wave's LDS");
+  constexpr int WAVE_B = S * STAGE_B;  // LDS bytes per wave
+  static_assert(WAVE_B <= RING_B, "the stages fit the wave's LDS");
   constexpr int NT = W * 64;
   constexpr int QROWS = (G + RPL - 1) / RPL;  // query rows per lane in the row layout
   static_assert(G <= 16, "at most 16 query heads per kv head");
@@ -187,10 +193,10 @@ __global__ __launch_bounds__((MfmaWaves<D, kW12>::W * 64), 1) void paged_decode_
   // reuse the ring once every wave is done with it.
   constexpr int MERGE_B = W * G * D * 4 + 2 * G * W * 4;
   constexpr int Q_B = kProlog ? W * G * ROWB : 16;
-  constexpr bool kOwnMerge = W * RING_B + MERGE_B + Q_B <= 160 * 1024;
-  static_assert(MERGE_B <= W * RING_B, "merge scratch");
+  constexpr bool kOwnMerge = W * WAVE_B + MERGE_B + Q_B <= 160 * 1024;
+  static_assert(MERGE_B <= W * WAVE_B, "merge scratch");
 
-  __shared__ __align__(1024) char s_buf[W * RING_B];
+  __shared__ __align__(1024) char s_buf[W * WAVE_B];
   // Apart from the tile ring, so that early tile DMAs cannot land on them:
   // the query rows of the prologue (per wave).
   __shared__ __align__(16) char s_q[Q_B];
@@ -327,16 +333,15 @@ __global__ __launch_bounds__((MfmaWaves<D, kW12>::W * 64), 1) void paged_decode_
   // ---- tile DMA: instruction i of a tile moves rows RPI i .. RPI i + RPI - 1;
   // lane l writes row RPI i + l / CPR at chunk position l % CPR, i.e. reads
   // logical chunk (l % CPR) ^ swz(row) of that row ----
-  // FP8: K code chunks go to chunk (c ^ row % CPR) of their row, so that
-  // the 8-code reads of S^T spread over the banks; V codes are staged in
-  // order, as the conversion reads them.
-  uint32_t loff[NI], loffv[NI];
+  // FP8: code chunks of K and V go to chunk (c ^ row % CPR) of their row, so
+  // that the 8-code reads of S^T and the transposed V reads spread over the
+  // banks.
+  uint32_t loff[NI];
 #pragma unroll
   for (int i = 0; i < NI; ++i) {
     const int row = RPI * i + lane / CPR;
     const int pos = kF8 ? (lane % CPR) ^ (row % CPR) : (lane % CPR) ^ dec_swz<D>(row);
     loff[i] = (uint32_t)(row * p.s_slot) + (uint32_t)(pos << 4);
-    loffv[i] = kF8 ? (uint32_t)(row * p.s_slot) + (uint32_t)((lane % CPR) << 4) : loff[i];
   }
   const char* zero_row = reinterpret_cast<const char*>(&kDecZeroRow);
   const int64_t head_off = (int64_t)h * p.s_head;
@@ -364,7 +369,7 @@ __global__ __launch_bounds__((MfmaWaves<D, kW12>::W * 64), 1) void paged_decode_
 #pragma unroll
       for (int i = 0; i < NI; ++i) dma16_nt(loff[i], kb, dst + i * 1024);
 #pragma unroll
-      for (int i = 0; i < NI; ++i) dma16_nt(loffv[i], vb, dst + PTILE + i * 1024);
+      for (int i = 0; i < NI; ++i) dma16_nt(loff[i], vb, dst + PTILE + i * 1024);
     } else {
 #pragma unroll
       for (int i = 0; i < 2 * NI; ++i) dma16(zero_row, dst + i * 1024);
@@ -534,26 +539,6 @@ __global__ __launch_bounds__((MfmaWaves<D, kW12>::W * 64), 1) void paged_decode_
       wait_vmcnt<0>();
     char* sK = s_wave + (k % S) * STAGE_B;
     char* sV = sK + PTILE;
-    if constexpr (kF8) {
-      // V codes to 16-bit rows in the conversion area, each 16-byte chunk of
-      // the 16-bit tile at its swizzled position (the transposed V reads
-      // below need 16-bit rows).  K stays as codes: S^T converts the eight
-      // codes of each A operand in registers.  The wave's LDS operations run
-      // in order, so the reads below see these writes.
-      char* cV = s_wave + S * STAGE_B;
-      constexpr int NCH = PTILE / 16 / 64;  // V code chunks per lane
-#pragma unroll
-      for (int i = 0; i < NCH; ++i) {
-        const int e = lane + 64 * i;
-        const int row = e / CPR, c8 = e % CPR;
-        const int p0 = ((2 * c8) ^ dec_swz<D>(row)) << 4;
-        const int p1 = ((2 * c8 + 1) ^ dec_swz<D>(row)) << 4;
-        const uint4 cv = *reinterpret_cast<const uint4*>(sV + e * 16);
-        *reinterpret_cast<uint4*>(cV + row * ROWB + p0) = f8_dequant8<ET>(make_uint2(cv.x, cv.y));
-        *reinterpret_cast<uint4*>(cV + row * ROWB + p1) = f8_dequant8<ET>(make_uint2(cv.z, cv.w));
-      }
-      sV = cV;
-    }
     const int c = wave + W * k;  // partition chunk of this tile
     const int tb = start + c * kChunk;
     if (k > 0 && (k & 63) == 0) {
@@ -573,12 +558,14 @@ __global__ __launch_bounds__((MfmaWaves<D, kW12>::W * 64), 1) void paged_decode_
       if (slot >= 0 && slot < cap && rg == 0) {
         const int r = new_tok - tb;
         const int pos16 = (col ^ dec_swz<D>(r)) << 4;
-        if constexpr (kF8)  // the lane's eight codes, in the K stage's layout
-          *reinterpret_cast<uint2*>(sK + r * PROWB + (((col >> 1) ^ (r % CPR)) << 4) +
-                                    (col & 1) * 8) = kq;
-        else
+        if constexpr (kF8) {  // the lane's eight codes, in the stages' layout
+          const int off8 = r * PROWB + (((col >> 1) ^ (r % CPR)) << 4) + (col & 1) * 8;
+          *reinterpret_cast<uint2*>(sK + off8) = kq;
+          *reinterpret_cast<uint2*>(sV + off8) = vq;
+        } else {
           *reinterpret_cast<uint4*>(sK + r * ROWB + pos16) = kcur;
-        *reinterpret_cast<uint4*>(sV + r * ROWB + pos16) = vcur;
+          *reinterpret_cast<uint4*>(sV + r * ROWB + pos16) = vcur;
+        }
         const int64_t sb = p.slot_small ? (int64_t)fast_div((uint32_t)slot, p.bs_div)
                                         : slot / p.block_size;
         cur_dst = sb * p.s_blk + (slot - sb * p.block_size) * p.s_slot + head_off +
@@ -602,9 +589,24 @@ __global__ __launch_bounds__((MfmaWaves<D, kW12>::W * 64), 1) void paged_decode_
       }
       sacc = M::qk(a, qb[j], sacc);
     }
+    // FP8: V^T's codes, read now so that the stage can take the wave's tile
+    // k + S before the softmax.  Read q gives lane (r16, c4) the codes of
+    // tokens 4 c4 .. 4 c4 + 3 at dim 16 (2 q) + r16 (bytes 0-3) and at dim
+    // 16 (2 q + 1) + r16 (bytes 4-7): the A operands of two 16x16x16
+    // products.  Byte j of lane 16 c4 + i is byte i % 8 of the word lane
+    // 16 c4 + 2 j + i / 8 points at, so lane (t, c4) points at token
+    // 4 c4 + (t / 2) % 4, dims 16 (2 q + t / 8) + 8 (t % 2) .. + 7.
+    uint2 vraw[kF8 ? DT / 2 : 1];
     if constexpr (kF8) {
-      // Both halves of the stage have been read (V by the conversion, K
-      // just now): it takes the wave's tile k + S.
+      const int trow = 4 * c4 + ((r16 >> 1) & 3);
+#pragma unroll
+      for (int q = 0; q < DT / 2; ++q) {
+        const int dt = 2 * q + (r16 >> 3);
+        const int off = trow * PROWB + ((dt ^ (trow % CPR)) << 4) + (r16 & 1) * 8;
+        vraw[q] = __builtin_bit_cast(
+            uint2, __builtin_amdgcn_ds_read_tr8_b64_v2i32((mf_lds_s32x2*)(sV + off)));
+      }
+      // Both halves of the stage have been read: it takes tile k + S.
       wait_lgkmcnt0();
       if (k + S < ntw) issue(k + S);
     }
@@ -650,17 +652,29 @@ __global__ __launch_bounds__((MfmaWaves<D, kW12>::W * 64), 1) void paged_decode_
     pb.y = M::pack2(pr[2], pr[3]);
 
     // O^T += V^T P^T over this tile's 16 tokens.
+    if constexpr (kF8) {
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt) {
-      const int off = vrow * ROWB + (((2 * dt + ((r16 >> 1) & 1)) ^ vswz) << 4) + ((r16 & 1) << 3);
-      uint2 au = __builtin_bit_cast(
-          uint2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((mf_lds_s16x4*)(sV + off)));
-      au.x &= keep0;
-      au.y &= keep1;
-      o[dt] = M::pv(__builtin_bit_cast(mf_s16x4, au), pb, o[dt]);
+      for (int q = 0; q < DT / 2; ++q) {
+        const uint4 u = f8_dequant8<ET>(vraw[q]);
+        o[2 * q] = M::pv(__builtin_bit_cast(mf_s16x4, make_uint2(u.x & keep0, u.y & keep1)), pb,
+                         o[2 * q]);
+        o[2 * q + 1] = M::pv(__builtin_bit_cast(mf_s16x4, make_uint2(u.z & keep0, u.w & keep1)),
+                             pb, o[2 * q + 1]);
+      }
+    } else {
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) {
+        const int off =
+            vrow * ROWB + (((2 * dt + ((r16 >> 1) & 1)) ^ vswz) << 4) + ((r16 & 1) << 3);
+        uint2 au = __builtin_bit_cast(
+            uint2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((mf_lds_s16x4*)(sV + off)));
+        au.x &= keep0;
+        au.y &= keep1;
+        o[dt] = M::pv(__builtin_bit_cast(mf_s16x4, au), pb, o[dt]);
+      }
     }
     // The stage is free once its LDS reads have returned (an FP8 stage was
-    // reissued after its conversion).
+    // reissued after its V reads above).
     if constexpr (!kF8) {
       wait_lgkmcnt0();
       if (k + S < ntw) issue(k + S);
