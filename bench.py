@@ -59,7 +59,7 @@ def decode_kernel_name() -> str:
     VA_DECODE_KERNEL=general selects the general one."""
     if os.environ.get("VA_DECODE_KERNEL") == "general":
         return "paged_decode_kernel<BF16,128,2,true,false>"
-    return "paged_decode_mfma_kernel<BF16,128,2,false,false,false,false>"
+    return "paged_decode_mfma_kernel<BF16,128,2,false,false,false,0>"
 
 
 TIMINGS: dict[str, dict] = {}  # per timed graph: median / mean / min ms per replay

@@ -270,3 +270,46 @@ def test_key_valid_mask_past_64_tiles_per_wave(dev, dtype):
                            valid_mask=valid.to(dev)).cpu()
     ref = oracle.paged_decode(q, kp, vp, table, lt, 128 ** -0.5, valid_mask=valid)
     assert _err(out, ref) <= TOL
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("hq,hkv,B,split", [(16, 8, 32, 0), (16, 8, 48, 0), (16, 8, 20, 256),
+                                           (8, 1, 300, 0)])
+def test_four_wave_workgroups_with_prologue_mask_and_store(dev, dtype, hq, hkv, B, split):
+    # 16-bit pools at head_dim 128 take four-wave workgroups when a launch has
+    # more workgroups than CUs (B = 48 x 8 kv heads; 20 x 8 in partitions of
+    # 256 tokens, merged; 300 sequences of one kv head), eight waves at one per
+    # CU (32 x 8).  With the fused prologue, the key mask and the fused store:
+    # bit for bit the two-launch path (va_qk_norm_rope, then the decode), output
+    # and pools, and the oracle within the tolerance.  (The prologue's sum of
+    # squares is reduced in another order than the oracle's mean, so the stored
+    # keys may differ from the oracle's by an ulp.)
+    g = torch.Generator().manual_seed(B + hq)
+    lens = torch.randint(1, 700, (B,), generator=g).tolist()
+    q, kp, vp, table, lt = _nhd_case(lens, 16, dtype, hq=hq, hkv=hkv, seed=B)
+    nk = torch.randn(B, hkv, 128, generator=g).to(dtype)
+    nv = torch.randn(B, hkv, 128, generator=g).to(dtype)
+    wq = (torch.rand(128, generator=g) + 0.5).to(dtype)
+    wk = (torch.rand(128, generator=g) + 0.5).to(dtype)
+    cs = oracle.rope_cache(128, 1024, 1_000_000.0)
+    pos = lt.long() - 1
+    valid = torch.rand(B, max(lens) + 5, generator=g) < 0.85
+    print(f"four-wave case {dtype} hq={hq} hkv={hkv} B={B} split={split}", flush=True)
+    pro = ops.QKPrologue(wq.to(dev), wk.to(dev), 1e-6, cs.to(dev), pos.to(dev))
+    common = dict(max_seq_len=max(lens), scale=128 ** -0.5, split_tokens=split,
+                  valid_mask=valid.to(dev), new_v=nv.to(dev))
+    td, ld = table.to(dev), lt.to(dev)
+    kd1, vd1 = kp.to(dev), vp.to(dev)
+    kd2, vd2 = kd1.clone(), vd1.clone()
+    out1 = ops.paged_decode(q.to(dev), kd1, vd1, td, ld, new_k=nk.to(dev), prologue=pro,
+                            **common)
+    qn, kn = ops.qk_norm_rope(q.to(dev), nk.to(dev), pro)
+    out2 = ops.paged_decode(qn, kd2, vd2, td, ld, new_k=kn, **common)
+    torch.cuda.synchronize()
+    assert torch.equal(out1, out2)
+    assert torch.equal(kd1, kd2) and torch.equal(vd1, vd2)
+    rq, rk = oracle.qk_norm_rope(q, nk, pos, wq, wk, 1e-6, cs)
+    ek, ev = oracle.write_current_kv(kp, vp, table, lt, rk, nv, layout=ops.LAYOUT_NHD)
+    assert torch.equal(vd1.cpu(), ev)
+    ref = oracle.paged_decode(rq, ek, ev, table, lt, 128 ** -0.5, valid_mask=valid)
+    assert _err(out1, ref) <= TOL

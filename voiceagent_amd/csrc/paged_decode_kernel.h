@@ -79,7 +79,7 @@ struct DecodeParams {
   int32_t has_pro;  // apply the Qwen3 q/k prologue to q and the current row
   PrologueParams pro;
   int32_t kv_fp8;        // the pool holds e4m3 codes (matrix-core kernel only)
-  int32_t wave12;        // FP8, head_dim 128, short partitions: twelve-wave workgroups
+  int32_t waves;         // matrix-core kernel: 0 (the default for head_dim), 12 or 4
   float v_scale;         // output factor: v_scale of an FP8 pool, else 1
   float inv_k, inv_v;    // FP8 pool: 1 / k_scale, 1 / v_scale (current-row quantisation)
 };

@@ -9,8 +9,9 @@
 // of its group.
 //
 // Work decomposition.  A workgroup is W wave64s (8, two per SIMD, for head
-// dims up to 128; 4 for 256; 12 over FP8 pools at head_dim 128 when a
-// workgroup attends few tokens, see MfmaWaves).  The partition's 16-token
+// dims up to 128; 4 for 256; at head_dim 128, 12 over FP8 pools when a
+// workgroup attends few tokens and 4 over 16-bit pools when a launch has
+// more workgroups than CUs, see MfmaWaves).  The partition's 16-token
 // tiles go round robin to the waves (tile c to wave c % W), and each wave
 // runs its own pipeline with no workgroup barrier:
 //   * the K and V rows of a tile (16 rows of one block) are copied from HBM
@@ -107,23 +108,30 @@ struct MfmaDecodeShape {
   static constexpr int RPL = 64 / LPR;         // rows per wave in the row layout
 };
 
-// Waves per workgroup and the most LDS bytes a wave's ring may take.  kW12:
-// twelve waves (three per SIMD) with two stages of codes each, for FP8 pools
-// at head_dim 128 when a workgroup streams few tokens (the host's choice,
-// DecodeParams::wave12).  Over FP8 a long context's tail is bound by its
-// tiles' arithmetic (code reads and conversions wait on LDS), and a third
-// wave per SIMD hides more of it (config 2 over FP8 pools 11.5 -> 10.7
-// us/layer, one 16K context 14.3 -> 13.8, measured when V still went through
-// a 16-bit conversion area).  With ~4K tokens per workgroup (config 5's
-// eight long contexts) two stages are too few (44.6 -> 45.6 us/layer), so
-// those keep eight waves with three stages.  (Measured and dropped: sixteen
-// waves with two stages, config 2 10.5 and one 16K context 14.0 against 10.3
-// and 13.5.)
-template <int D, bool kW12>
+// Waves per workgroup and the most LDS bytes a wave's ring may take, for
+// the host's choice kWaves (DecodeParams::waves): 0 takes the default for D.
+//   12: twelve waves (three per SIMD) with two stages of codes each, for FP8
+//   pools at head_dim 128 when a workgroup streams few tokens.  Over FP8 a
+//   long context's tail is bound by its tiles' arithmetic (code reads and
+//   conversions wait on LDS), and a third wave per SIMD hides more of it
+//   (config 2 over FP8 pools 11.5 -> 10.7 us/layer, one 16K context 14.3 ->
+//   13.8, measured when V still went through a 16-bit conversion area).
+//   With ~4K tokens per workgroup (config 5's eight long contexts) two stages
+//   are too few (44.6 -> 45.6 us/layer), so those keep eight waves with three
+//   stages.  (Measured and dropped: sixteen waves with two stages, config 2
+//   10.5 and one 16K context 14.0 against 10.3 and 13.5.)
+//   4: four waves with the default two stages (64 KiB of ring), for 16-bit
+//   pools at head_dim 128 when the launch has more workgroups than CUs: two
+//   workgroups share a CU, so one's start-up round trips overlap the other's
+//   stream instead of following it.  Batch 64 x U[60,600] 22.2 -> 20.7
+//   us/layer, 256: 72.3 -> 65.9; with one workgroup per CU (config 2's 256)
+//   eight waves stay faster (13.1 against 13.9).
+template <int D, int kWaves>
 struct MfmaWaves {
-  static_assert(!kW12 || D == 128, "twelve waves at head_dim 128 only");
-  static constexpr int W = kW12 ? 12 : MfmaDecodeShape<D>::W;
-  static constexpr int WAVE_B = kW12 ? 8 * 1024 : MfmaDecodeShape<D>::WAVE_B;
+  static_assert(kWaves == 0 || D == 128, "twelve or four waves at head_dim 128 only");
+  static_assert(kWaves == 0 || kWaves == 12 || kWaves == 4, "0, 12 or 4 waves");
+  static constexpr int W = kWaves == 0 ? MfmaDecodeShape<D>::W : kWaves;
+  static constexpr int WAVE_B = kWaves == 12 ? 8 * 1024 : MfmaDecodeShape<D>::WAVE_B;
 };
 
 // Tokens per partition unit of the matrix-core kernel: one round of S tiles
@@ -157,14 +165,15 @@ constexpr float kDecLazy = 8.0f;
 // codes with ds_read_b64_tr_b8, one read giving the lane its four tokens of
 // two 16-dim blocks, converted in registers as well.  k_scale is folded
 // into the softmax scale and v_scale into the output.
-template <typename ET, int D, int G, bool kProlog, bool kMask, bool kF8, bool kW12 = false>
-__global__ __launch_bounds__((MfmaWaves<D, kW12>::W * 64), 1) void paged_decode_mfma_kernel(
+template <typename ET, int D, int G, bool kProlog, bool kMask, bool kF8, int kWaves = 0>
+__global__ __launch_bounds__((MfmaWaves<D, kWaves>::W * 64), 1) void paged_decode_mfma_kernel(
     DecodeParams p) {
-  static_assert(!kW12 || kF8, "twelve waves over FP8 pools only");
+  static_assert(kWaves != 12 || kF8, "twelve waves over FP8 pools only");
+  static_assert(kWaves != 4 || !kF8, "four waves over 16-bit pools only");
   using Sh = MfmaDecodeShape<D>;
   using M = DecodeMma<ET>;
-  constexpr int W = MfmaWaves<D, kW12>::W, ROWB = Sh::ROWB;
-  constexpr int RING_B = MfmaWaves<D, kW12>::WAVE_B;  // LDS bytes per wave
+  constexpr int W = MfmaWaves<D, kWaves>::W, ROWB = Sh::ROWB;
+  constexpr int RING_B = MfmaWaves<D, kWaves>::WAVE_B;  // LDS bytes per wave
   constexpr int TILE_B = Sh::TILE_B, DS = Sh::DS, DT = Sh::DT;
   constexpr int LPR = Sh::LPR, RPL = Sh::RPL, E = 8;
   // A tile as the DMA stages it: 16-bit rows, or rows of D e4m3 codes.
@@ -756,37 +765,44 @@ __global__ __launch_bounds__((MfmaWaves<D, kW12>::W * 64), 1) void paged_decode_
 }
 
 // ------------------------------------------------------------- launching
-template <typename ET, int D, int G, bool kF8, bool kW12>
+template <typename ET, int D, int G, bool kF8, int kWaves>
 static void launch_decode_mfma_w(const DecodeParams& p, dim3 grid, hipStream_t s) {
-  constexpr int NT = MfmaWaves<D, kW12>::W * 64;
+  constexpr int NT = MfmaWaves<D, kWaves>::W * 64;
   const dim3 hgrid(grid.y, grid.x, grid.z);  // (kv head, sequence, partition)
   const bool mask = p.valid != nullptr && p.valid_len > 0;
   if (p.has_pro && mask)
-    hipLaunchKernelGGL((paged_decode_mfma_kernel<ET, D, G, true, true, kF8, kW12>), hgrid,
+    hipLaunchKernelGGL((paged_decode_mfma_kernel<ET, D, G, true, true, kF8, kWaves>), hgrid,
                        dim3(NT), 0, s, p);
   else if (p.has_pro)
-    hipLaunchKernelGGL((paged_decode_mfma_kernel<ET, D, G, true, false, kF8, kW12>), hgrid,
+    hipLaunchKernelGGL((paged_decode_mfma_kernel<ET, D, G, true, false, kF8, kWaves>), hgrid,
                        dim3(NT), 0, s, p);
   else if (mask)
-    hipLaunchKernelGGL((paged_decode_mfma_kernel<ET, D, G, false, true, kF8, kW12>), hgrid,
+    hipLaunchKernelGGL((paged_decode_mfma_kernel<ET, D, G, false, true, kF8, kWaves>), hgrid,
                        dim3(NT), 0, s, p);
   else
-    hipLaunchKernelGGL((paged_decode_mfma_kernel<ET, D, G, false, false, kF8, kW12>), hgrid,
+    hipLaunchKernelGGL((paged_decode_mfma_kernel<ET, D, G, false, false, kF8, kWaves>), hgrid,
                        dim3(NT), 0, s, p);
 }
 
 template <typename ET, int D, int G, bool kF8>
 static void launch_decode_mfma(const DecodeParams& p, dim3 grid, hipStream_t s) {
   // Twelve waves: FP8 pools at head_dim 128 and groups up to 4 (a G = 8
-  // prologue's query rows would not fit beside twelve waves' LDS).
+  // prologue's query rows would not fit beside twelve waves' LDS).  Four
+  // waves: 16-bit pools at head_dim 128.
   bool done = false;
-  if constexpr (kF8 && D == 128 && G <= 4) {
-    if (p.wave12) {
-      launch_decode_mfma_w<ET, D, G, kF8, true>(p, grid, s);
+  if constexpr (D == 128 && kF8 && G <= 4) {
+    if (p.waves == 12) {
+      launch_decode_mfma_w<ET, D, G, kF8, 12>(p, grid, s);
       done = true;
     }
   }
-  if (!done) launch_decode_mfma_w<ET, D, G, kF8, false>(p, grid, s);
+  if constexpr (D == 128 && !kF8) {
+    if (p.waves == 4) {
+      launch_decode_mfma_w<ET, D, G, kF8, 4>(p, grid, s);
+      done = true;
+    }
+  }
+  if (!done) launch_decode_mfma_w<ET, D, G, kF8, 0>(p, grid, s);
   if (p.max_parts > 1)
     hipLaunchKernelGGL((paged_decode_merge_kernel<ET, D, G, kF8 ? 1 : 0>), dim3(grid.y, grid.x),
                        dim3(256), 0, s, p);
