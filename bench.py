@@ -194,10 +194,11 @@ def bench_decode_warm(args, dev, stream, dec):
 
 
 def bench_decode_batches(args, dev, stream):
-    """Config 2's decode at larger batches (contexts U[60, 600], 28 cold layers):
-    with several rounds of workgroups the dispatcher hands each CU a new pair as
-    it frees, so the longest contexts no longer set the end alone.  Reported
-    beside the headline, not instead of it."""
+    """Config 2's decode at larger batches (contexts U[60, 600], 28 cold layers),
+    over the bf16 pools and over FP8 copies of them: with several rounds of
+    workgroups the dispatcher hands each CU a new pair as it frees, so the
+    longest contexts no longer set the end alone.  Reported beside the
+    headline, not instead of it."""
     res = {}
     for B in (64, 128, 256):
         lens = workloads.cfg2_lens(0, batch=B)
@@ -229,7 +230,26 @@ def bench_decode_batches(args, dev, stream):
             f"({gbs / HBM_PEAK_GBS:.3f} of HBM peak)")
         res[f"b{B}"] = {"us_per_layer": round(us, 2), "gbs": round(gbs, 1),
                         "frac": round(gbs / HBM_PEAK_GBS, 4), "bytes_per_layer": nbytes}
-        del batch, qs, nks, nvs, outs
+        # The same step over FP8 copies of the pools (half the K/V bytes).
+        kf, vf = fp8_pools(batch.k_pools, batch.v_pools)
+
+        def step_fp8():
+            for i in range(layers):
+                ops.paged_decode(qs[i], kf[i], vf[i], batch.block_tables, batch.cu_seqlens_k,
+                                 lens_cumulative=True, max_seq_len=batch.max_seq_len,
+                                 scale=batch.scale, new_k=nks[i], new_v=nvs[i],
+                                 new_slots=batch.slot_mapping, out=outs[i], k_scale=FP8_SCALE,
+                                 v_scale=FP8_SCALE)
+
+        ms8, _ = timed_graph(step_fp8, args.steps, args.warmup, stream, name=f"decode_b{B}_fp8")
+        us8 = ms8 * 1000.0 / layers
+        nbytes8 = decode_launch_bytes(lens, kv_elem=1)
+        gbs8 = nbytes8 / (us8 * 1e-6) / 1e9
+        log(f"[decode batch fp8] B={B}: {us8:.2f} us/layer, {gbs8:.0f} GB/s of "
+            f"{nbytes8 / 1e6:.1f} MB ({gbs8 / HBM_PEAK_GBS:.3f} of HBM peak)")
+        res[f"b{B}"]["fp8"] = {"us_per_layer": round(us8, 2), "gbs": round(gbs8, 1),
+                               "frac": round(gbs8 / HBM_PEAK_GBS, 4), "bytes_per_layer": nbytes8}
+        del batch, qs, nks, nvs, outs, kf, vf
         torch.cuda.empty_cache()
     return res
 

@@ -404,3 +404,45 @@ def test_fp8_decode_either_side_of_the_twelve_wave_bound(dev, split):
     ref = oracle.paged_decode(rq, ek, ev, table, lens_t, 128 ** -0.5, valid_mask=valid,
                               k_scale=ks, v_scale=vs)
     assert _err(out, ref) <= 2e-2
+
+
+@pytest.mark.parametrize("hq,hkv,B", [(16, 8, 32), (16, 8, 48), (8, 1, 300)])
+def test_fp8_four_wave_workgroups(dev, hq, hkv, B):
+    # A launch with more workgroups than CUs takes four-wave workgroups over
+    # FP8 pools too (48 x 8 kv heads, 300 sequences of one kv head); 32 x 8
+    # takes twelve waves.  With the fused prologue, the key mask and the fused
+    # store: bit for bit the two-launch path (va_qk_norm_rope, then the
+    # decode), output and pools, and the oracle on the dequantised pool within
+    # 2e-2.
+    g = torch.Generator().manual_seed(B + hq + 1)
+    lens = torch.randint(1, 700, (B,), generator=g).tolist()
+    ks, vs = 0.05, 0.08
+    table, kp, vp, q, nk, nv = _fp8_batch(lens, dev, seed=B, hq=hq, hkv=hkv, k_scale=ks,
+                                          v_scale=vs)
+    wq = (torch.rand(128, generator=g) + 0.5).to(torch.bfloat16)
+    wk = (torch.rand(128, generator=g) + 0.5).to(torch.bfloat16)
+    cs = oracle.rope_cache(128, 1024, 1_000_000.0)
+    pos = torch.tensor(lens) - 1
+    lens_t = torch.tensor(lens, dtype=torch.int32)
+    valid = torch.rand(B, max(lens) + 5, generator=g) < 0.85
+    print(f"fp8 four-wave case hq={hq} hkv={hkv} B={B}", flush=True)
+    pro = ops.QKPrologue(wq.to(dev), wk.to(dev), 1e-6, cs.to(dev), pos.to(dev))
+    common = dict(max_seq_len=max(lens), scale=128 ** -0.5, valid_mask=valid.to(dev),
+                  new_v=nv.to(dev), k_scale=ks, v_scale=vs)
+    td, ld = table.to(dev), lens_t.to(dev)
+    kd1, vd1 = kp.to(dev), vp.to(dev)
+    kd2, vd2 = kd1.clone(), vd1.clone()
+    out1 = ops.paged_decode(q.to(dev), kd1, vd1, td, ld, new_k=nk.to(dev), prologue=pro,
+                            **common)
+    qn, kn = ops.qk_norm_rope(q.to(dev), nk.to(dev), pro)
+    out2 = ops.paged_decode(qn, kd2, vd2, td, ld, new_k=kn, **common)
+    torch.cuda.synchronize()
+    assert torch.equal(out1, out2)
+    assert torch.equal(_codes(kd1), _codes(kd2)) and torch.equal(_codes(vd1), _codes(vd2))
+    rq, rk = oracle.qk_norm_rope(q, nk, pos, wq, wk, 1e-6, cs)
+    ek, ev = oracle.write_current_kv(kp, vp, table, lens_t, rk, nv, layout=ops.LAYOUT_NHD,
+                                     k_scale=ks, v_scale=vs)
+    assert torch.equal(_codes(vd1.cpu()), _codes(ev))
+    ref = oracle.paged_decode(rq, ek, ev, table, lens_t, 128 ** -0.5, valid_mask=valid,
+                              k_scale=ks, v_scale=vs)
+    assert _err(out1, ref) <= 2e-2

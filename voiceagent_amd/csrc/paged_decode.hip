@@ -443,13 +443,14 @@ int va::paged_decode_impl(const va_decode_args* a, void* stream) {
   // output (applied after the weighted sum).
   p.scale_log2 = a->scale * (f8 ? a->pool.k_scale : 1.0f) * 1.4426950408889634f;
   p.kv_fp8 = f8;
-  // Matrix-core workgroup shape (MfmaWaves): twelve waves over FP8 pools
-  // whose workgroups attend few tokens; four over 16-bit pools when the
-  // launch has more workgroups than CUs, so that two share a CU.
+  // Matrix-core workgroup shape (MfmaWaves): four waves when the launch has
+  // more workgroups than CUs, so that several share a CU; otherwise twelve
+  // over FP8 pools whose workgroups attend few tokens.
   const int64_t wgs = (int64_t)a->num_seqs * a->num_kv_heads * pl.max_parts;
-  p.waves = a->head_dim != 128 ? 0
-            : f8              ? (pl.wg_tokens <= kWave12Tokens ? 12 : 0)
-                              : (wgs > current_device_cus() ? 4 : 0);
+  p.waves = a->head_dim != 128                ? 0
+            : wgs > current_device_cus()      ? 4
+            : f8 && pl.wg_tokens <= kWave12Tokens ? 12
+                                              : 0;
   p.v_scale = f8 ? a->pool.v_scale : 1.0f;
   p.inv_k = f8 ? 1.0f / a->pool.k_scale : 1.0f;
   p.inv_v = f8 ? 1.0f / a->pool.v_scale : 1.0f;

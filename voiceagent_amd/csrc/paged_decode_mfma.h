@@ -10,8 +10,8 @@
 //
 // Work decomposition.  A workgroup is W wave64s (8, two per SIMD, for head
 // dims up to 128; 4 for 256; at head_dim 128, 12 over FP8 pools when a
-// workgroup attends few tokens and 4 over 16-bit pools when a launch has
-// more workgroups than CUs, see MfmaWaves).  The partition's 16-token
+// workgroup attends few tokens and 4 when a launch has
+// more workgroups than CUs (16-bit or FP8 pools), see MfmaWaves).  The partition's 16-token
 // tiles go round robin to the waves (tile c to wave c % W), and each wave
 // runs its own pipeline with no workgroup barrier:
 //   * the K and V rows of a tile (16 rows of one block) are copied from HBM
@@ -120,12 +120,14 @@ struct MfmaDecodeShape {
 //   are too few (44.6 -> 45.6 us/layer), so those keep eight waves with three
 //   stages.  (Measured and dropped: sixteen waves with two stages, config 2
 //   10.5 and one 16K context 14.0 against 10.3 and 13.5.)
-//   4: four waves with the default two stages (64 KiB of ring), for 16-bit
-//   pools at head_dim 128 when the launch has more workgroups than CUs: two
-//   workgroups share a CU, so one's start-up round trips overlap the other's
-//   stream instead of following it.  Batch 64 x U[60,600] 22.2 -> 20.7
-//   us/layer, 256: 72.3 -> 65.9; with one workgroup per CU (config 2's 256)
-//   eight waves stay faster (13.1 against 13.9).
+//   4: four waves with two stages each, at head_dim 128 when the launch has
+//   more workgroups than CUs: several workgroups share a CU (two over 16-bit
+//   pools, 64 KiB of ring each; four over FP8 pools, 32 KiB), so one's
+//   start-up round trips overlap the others' streams instead of following
+//   them.  Batch 64 x U[60,600] 22.2 -> 20.7 us/layer, 256: 72.3 -> 65.9;
+//   over FP8 pools (against twelve waves) 18.4 -> 15.2 and 61.7 -> 40.7.
+//   With one workgroup per CU (config 2's 256) eight waves stay faster over
+//   16-bit pools (13.1 against 13.9).
 template <int D, int kWaves>
 struct MfmaWaves {
   static_assert(kWaves == 0 || D == 128, "twelve or four waves at head_dim 128 only");
@@ -169,7 +171,6 @@ template <typename ET, int D, int G, bool kProlog, bool kMask, bool kF8, int kWa
 __global__ __launch_bounds__((MfmaWaves<D, kWaves>::W * 64), 1) void paged_decode_mfma_kernel(
     DecodeParams p) {
   static_assert(kWaves != 12 || kF8, "twelve waves over FP8 pools only");
-  static_assert(kWaves != 4 || !kF8, "four waves over 16-bit pools only");
   using Sh = MfmaDecodeShape<D>;
   using M = DecodeMma<ET>;
   constexpr int W = MfmaWaves<D, kWaves>::W, ROWB = Sh::ROWB;
@@ -188,7 +189,9 @@ __global__ __launch_bounds__((MfmaWaves<D, kWaves>::W * 64), 1) void paged_decod
   // fourth (a third with twelve waves) only enlarges the launch's first
   // burst of requests, whose last tiles then land later (config 2 over FP8
   // pools 10.3 -> 11.0 us/layer, one 16K context 13.5 -> 14.2).
-  constexpr int S_F8 = RING_B / STAGE_B < 3 ? RING_B / STAGE_B : 3;
+  // Four-wave workgroups keep two, so that four share a CU (three stages,
+  // two per CU: batch 256 over FP8 pools 42.8 against 40.7 us/layer).
+  constexpr int S_F8 = kWaves == 4 ? 2 : (RING_B / STAGE_B < 3 ? RING_B / STAGE_B : 3);
   constexpr int S = kF8 ? S_F8 : Sh::S;  // stages of the wave's ring
   static_assert(S >= 2, "two stages at least");
   constexpr int WAVE_B = S * STAGE_B;  // LDS bytes per wave
@@ -788,7 +791,7 @@ template <typename ET, int D, int G, bool kF8>
 static void launch_decode_mfma(const DecodeParams& p, dim3 grid, hipStream_t s) {
   // Twelve waves: FP8 pools at head_dim 128 and groups up to 4 (a G = 8
   // prologue's query rows would not fit beside twelve waves' LDS).  Four
-  // waves: 16-bit pools at head_dim 128.
+  // waves: head_dim 128.
   bool done = false;
   if constexpr (D == 128 && kF8 && G <= 4) {
     if (p.waves == 12) {
@@ -796,7 +799,7 @@ static void launch_decode_mfma(const DecodeParams& p, dim3 grid, hipStream_t s) 
       done = true;
     }
   }
-  if constexpr (D == 128 && !kF8) {
+  if constexpr (D == 128) {
     if (p.waves == 4) {
       launch_decode_mfma_w<ET, D, G, kF8, 4>(p, grid, s);
       done = true;
