@@ -197,6 +197,7 @@ __global__ __launch_bounds__((MfmaWaves<D, kWaves>::W * 64), 1) void paged_decod
   constexpr int WAVE_B = S * STAGE_B;  // LDS bytes per wave
   static_assert(WAVE_B <= RING_B, "the stages fit the wave's LDS");
   constexpr int NT = W * 64;
+  static_assert(W % 4 == 0, "the wave merge reads (m, l) of four waves at a time");
   constexpr int QROWS = (G + RPL - 1) / RPL;  // query rows per lane in the row layout
   static_assert(G <= 16, "at most 16 query heads per kv head");
   // The waves' partial results for the merge: o [W][G][D], then m and l
