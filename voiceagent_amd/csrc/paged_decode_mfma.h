@@ -189,8 +189,9 @@ __global__ __launch_bounds__((MfmaWaves<D, kWaves>::W * 64), 1) void paged_decod
   // fourth (a third with twelve waves) only enlarges the launch's first
   // burst of requests, whose last tiles then land later (config 2 over FP8
   // pools 10.3 -> 11.0 us/layer, one 16K context 13.5 -> 14.2).
-  // Four-wave workgroups keep two, so that four share a CU (three stages,
-  // two per CU: batch 256 over FP8 pools 42.8 against 40.7 us/layer).
+  // Four-wave workgroups keep two, so that four share a CU (with three
+  // stages, ~53 KB of LDS each: batch 256 over FP8 pools 42.8 against 40.7
+  // us/layer).
   constexpr int S_F8 = kWaves == 4 ? 2 : (RING_B / STAGE_B < 3 ? RING_B / STAGE_B : 3);
   constexpr int S = kF8 ? S_F8 : Sh::S;  // stages of the wave's ring
   static_assert(S >= 2, "two stages at least");
